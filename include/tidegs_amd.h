@@ -1,0 +1,210 @@
+/*
+ * tidegs_amd.h — C ABI of the MI355X (gfx950) TideGS hot-path kernels.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer (hipMalloc'd / PyTorch caching
+ *     allocator) unless stated otherwise; the library never allocates or frees
+ *     device memory.  Temporary storage is passed in as `workspace` after a
+ *     `*_workspace_size` query, like the reference's CUB_WRAPPER
+ *     (gsplat/cuda/csrc/bindings.h:16-23).
+ *   - All work is enqueued on the given `stream`; calls are reentrant (no
+ *     mutable globals apart from a thread-local error string).
+ *   - Return 0 on success, a positive hipError_t on a HIP failure, or a
+ *     negative TGS_ERR_* code for an argument error; tgs_last_error() then
+ *     describes it (the reference raises through TORCH_CHECK / AT_ERROR,
+ *     bindings.h:7-13).
+ *   - Floating point is fp32 throughout.
+ */
+#ifndef TIDEGS_AMD_H
+#define TIDEGS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* tgs_stream_t; /* == hipStream_t */
+
+#define TGS_OK 0
+#define TGS_ERR_ARG (-1)
+#define TGS_ERR_UNSUPPORTED (-2)
+#define TGS_ERR_WORKSPACE (-3)
+
+/* ---- library ---------------------------------------------------------- */
+int tgs_abi_version(void);
+const char* tgs_last_error(void);
+/* Zero/constant fill used instead of hipMemsetAsync (kernel node under capture). */
+int tgs_fill_u32(void* ptr, uint64_t n_words, uint32_t value, tgs_stream_t stream);
+
+/* ---- projection ------------------------------------------------------- */
+/* Replaces fully_fused_projection_fwd_tensor
+ * (gsplat/cuda/csrc/fully_fused_projection_fwd.cu:132-181; pybind ext.cpp).
+ * means [N,3]; covars [N,6] or null; quats [N,4] (w,x,y,z) + scales [N,3]
+ * when covars is null; viewmats [C,4,4] row-major w2c; Ks [C,3,3].
+ * Outputs radii [C,N] i32, means2d [C,N,2], depths [C,N], conics [C,N,3],
+ * compensations [C,N] or null.  Culled entries: radius 0 and zeros. */
+int tgs_fully_fused_projection_fwd(uint32_t C, uint32_t N, const float* means,
+                                   const float* covars, const float* quats, const float* scales,
+                                   const float* viewmats, const float* Ks, int32_t image_width,
+                                   int32_t image_height, float eps2d, float near_plane,
+                                   float far_plane, float radius_clip, int32_t* radii,
+                                   float* means2d, float* depths, float* conics,
+                                   float* compensations, tgs_stream_t stream);
+
+/* Replaces fully_fused_projection_bwd_tensor
+ * (gsplat/cuda/csrc/fully_fused_projection_bwd.cu:187-268).  Writes v_means
+ * and v_quats/v_scales (or v_covars) for every Gaussian (no zero-fill needed);
+ * v_viewmats (nullable) is accumulated and must be zeroed by the caller.
+ * v_depths and v_compensations may be null (treated as zero / absent). */
+int tgs_fully_fused_projection_bwd(uint32_t C, uint32_t N, const float* means,
+                                   const float* covars, const float* quats, const float* scales,
+                                   const float* viewmats, const float* Ks, int32_t image_width,
+                                   int32_t image_height, float eps2d, const int32_t* radii,
+                                   const float* conics, const float* compensations,
+                                   const float* v_means2d, const float* v_depths,
+                                   const float* v_conics, const float* v_compensations,
+                                   float* v_means, float* v_covars, float* v_quats,
+                                   float* v_scales, float* v_viewmats, tgs_stream_t stream);
+
+/* ---- spherical harmonics ---------------------------------------------- */
+/* Replaces compute_sh_fwd_tensor (gsplat/cuda/csrc/compute_sh_fwd.cu:31-58).
+ * dirs [n,3], coeffs [n,K,3], masks [n] u8/bool or null -> colors [n,3]. */
+int tgs_compute_sh_fwd(uint32_t n, uint32_t K, int32_t degrees_to_use, const float* dirs,
+                       const float* coeffs, const uint8_t* masks, float* colors,
+                       tgs_stream_t stream);
+/* Replaces compute_sh_bwd_tensor (gsplat/cuda/csrc/compute_sh_bwd.cu:101-136).
+ * Writes all of v_coeffs [n,K,3]; v_dirs [n,3] nullable. */
+int tgs_compute_sh_bwd(uint32_t n, uint32_t K, int32_t degrees_to_use, const float* dirs,
+                       const float* coeffs, const uint8_t* masks, const float* v_colors,
+                       float* v_coeffs, float* v_dirs, tgs_stream_t stream);
+
+/* ---- tile intersection ------------------------------------------------- */
+/* bit_width(v): floor(log2 v) + 1 (isect_tiles.cu:143-144). */
+uint32_t tgs_bit_width(uint32_t v);
+/* First pass of isect_tiles (isect_tiles.cu:14-71,155-164): tiles_per_gauss. */
+int tgs_isect_tiles_count(uint64_t total, const float* means2d, const int32_t* radii,
+                          uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
+                          int32_t* tiles_per_gauss, tgs_stream_t stream);
+/* torch.cumsum replacement (isect_tiles.cu:165): int32 in, int64 inclusive out. */
+size_t tgs_scan_workspace_size(uint64_t n);
+int tgs_inclusive_scan_i32_i64(const int32_t* in, int64_t* out, uint64_t n, void* workspace,
+                               size_t workspace_bytes, tgs_stream_t stream);
+int tgs_exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, void* workspace,
+                           size_t workspace_bytes, tgs_stream_t stream);
+/* Second pass of isect_tiles (isect_tiles.cu:73-98,171-187).  camera_ids
+ * [total] i64 for packed inputs, else null with N Gaussians per camera. */
+int tgs_isect_tiles_emit(uint64_t total, uint32_t N, const int64_t* camera_ids,
+                         const float* means2d, const int32_t* radii, const float* depths,
+                         const int64_t* cum_tiles_per_gauss, uint32_t tile_size,
+                         uint32_t tile_width, uint32_t tile_height, uint32_t tile_n_bits,
+                         int64_t* isect_ids, int32_t* flatten_ids, tgs_stream_t stream);
+/* cub::DeviceRadixSort::SortPairs replacement (isect_tiles.cu:189-227): stable
+ * ascending sort on key bits [begin_bit, end_bit); double-buffered, *selector
+ * (host int) = 0 if the result is in keys/vals, 1 if in keys_alt/vals_alt. */
+size_t tgs_radix_sort_workspace_size(uint64_t n);
+int tgs_radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
+                         uint64_t n, int begin_bit, int end_bit, void* workspace,
+                         size_t workspace_bytes, int* selector, tgs_stream_t stream);
+/* Replaces isect_offset_encode_tensor (isect_tiles.cu:234-301); offsets [C,th,tw]. */
+int tgs_isect_offset_encode(uint64_t n_isects, const int64_t* isect_ids, uint32_t C,
+                            uint32_t tile_width, uint32_t tile_height, int32_t* offsets,
+                            tgs_stream_t stream);
+
+/* ---- rasterization ---------------------------------------------------- */
+/* Channel counts with an instantiated kernel; returns their number. */
+int tgs_rasterize_supported_channels(int32_t* out, int32_t cap);
+/* Replaces rasterize_to_pixels_fwd_tensor (rasterize_to_pixels_fwd.cu:236-284).
+ * means2d/conics/colors/opacities [C,N,*] or packed [nnz,*]; backgrounds
+ * [C,channels] or null; render_colors [C,H,W,ch], render_alphas [C,H,W,1],
+ * last_ids [C,H,W] i32. tile_size 8 or 16. */
+int tgs_rasterize_to_pixels_fwd(uint32_t C, uint32_t channels, const float* means2d,
+                                const float* conics, const float* colors, const float* opacities,
+                                const float* backgrounds, uint32_t image_width,
+                                uint32_t image_height, uint32_t tile_size, uint32_t tile_width,
+                                uint32_t tile_height, const int32_t* tile_offsets,
+                                const int32_t* flatten_ids, uint32_t n_isects,
+                                float* render_colors, float* render_alphas, int32_t* last_ids,
+                                tgs_stream_t stream);
+/* Replaces rasterize_to_pixels_bwd_tensor (rasterize_to_pixels_bwd.cu:347-402).
+ * Gradient outputs are accumulated: zero them first.  v_render_alphas and
+ * v_means2d_abs (absgrad) may be null. */
+int tgs_rasterize_to_pixels_bwd(uint32_t C, uint32_t channels, const float* means2d,
+                                const float* conics, const float* colors, const float* opacities,
+                                const float* backgrounds, uint32_t image_width,
+                                uint32_t image_height, uint32_t tile_size, uint32_t tile_width,
+                                uint32_t tile_height, const int32_t* tile_offsets,
+                                const int32_t* flatten_ids, uint32_t n_isects,
+                                const float* render_alphas, const int32_t* last_ids,
+                                const float* v_render_colors, const float* v_render_alphas,
+                                float* v_means2d_abs, float* v_means2d, float* v_conics,
+                                float* v_colors, float* v_opacities, tgs_stream_t stream);
+
+/* ---- fused SSIM -------------------------------------------------------- */
+/* Replaces fusedssim (clm_kernels/ssim.cu:368-408): NCHW img1/img2 ->
+ * ssim_map and (all or none) of the three partial maps. */
+int tgs_fused_ssim_fwd(int32_t B, int32_t CH, int32_t H, int32_t W, float C1, float C2,
+                       const float* img1, const float* img2, float* ssim_map, float* dm_dmu1,
+                       float* dm_dsigma1_sq, float* dm_dsigma12, tgs_stream_t stream);
+/* Replaces fusedssim_backward (clm_kernels/ssim.cu:410-444). */
+int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, float C1, float C2,
+                       const float* img1, const float* img2, const float* dL_dmap,
+                       const float* dm_dmu1, const float* dm_dsigma1_sq, const float* dm_dsigma12,
+                       float* dL_dimg1, tgs_stream_t stream);
+/* Fused L1 + SSIM training loss of strategies/base_engine.py:464-488 on the
+ * rendered HWC image: sums[0] += sum|I - gt'|, sums[1] += sum SSIM (double[2],
+ * caller-zeroed), gt' = clamp(gt_chw / gt_div, 0, 1); partial maps [3,H,W]. */
+int tgs_tide_loss_fwd(int32_t H, int32_t W, const float* image_hwc, const float* gt_chw,
+                      float gt_div, float* dm_dmu1, float* dm_dsigma1_sq, float* dm_dsigma12,
+                      double* sums, tgs_stream_t stream);
+/* dL/dI (HWC) of L = (1-lambda) mean|I-gt'| + lambda (1 - mean SSIM). */
+int tgs_tide_loss_bwd(int32_t H, int32_t W, const float* image_hwc, const float* gt_chw,
+                      float gt_div, float lambda_dssim, const float* dm_dmu1,
+                      const float* dm_dsigma1_sq, const float* dm_dsigma12, float* v_image_hwc,
+                      tgs_stream_t stream);
+
+/* ---- resident optimizer ------------------------------------------------ */
+/* Replaces the six _fused_resident_adam_kernel launches of GPUResidentAdam.step
+ * (strategies/tide_engine/gpu_resident_optimizer.py:16-70, :397-418, :474-499)
+ * and its searchsorted slot mapping (:266-300) with one launch.
+ * local_rows [n_rows] (i64 if index_is_i64 else i32) index the working-set
+ * params; block layout = sorted [start,end) slices with their state slots
+ * (device i64 arrays of n_layout); bias tables per slot (:302-337).
+ * Host arrays (length n_components <= 8, total width <= 64): params, grads
+ * ([n_rows, w] rows), exp_avg, exp_avg_sq ([slots*block_size, w] rows) device
+ * pointers, widths, lrs, and row_strides [3*n_components] (param, grad,
+ * state row strides in elements; null = dense rows of `width`), so split
+ * component tensors and column views of one [N,59] table both work.  error_flag (device int, caller-zeroed) becomes
+ * nonzero if a row lies outside every block. */
+int tgs_resident_adam_step(int64_t n_rows, const void* local_rows, int index_is_i64,
+                           const int64_t* block_starts, const int64_t* block_ends,
+                           const int64_t* block_slots, int64_t n_layout, int64_t block_size,
+                           const float* bias_correction1, const float* denom_scale,
+                           int n_components, float* const* params, const float* const* grads,
+                           float* const* exp_avg, float* const* exp_avg_sq,
+                           const int32_t* widths, const int64_t* row_strides, const float* lrs,
+                           float beta1, float beta2, float eps, float batch_size,
+                           int* error_flag, tgs_stream_t stream);
+/* Sophia-style step (no reference implementation; defined from Liu et al.
+ * 2023): m = b1 m + (1-b1) g; h = b2 h + (1-b2) g*g when update_hessian;
+ * p -= lr clamp(m / max(h, eps), -rho, rho).  Same layout as Adam. */
+int tgs_resident_sophia_step(int64_t n_rows, const void* local_rows, int index_is_i64,
+                             const int64_t* block_starts, const int64_t* block_ends,
+                             const int64_t* block_slots, int64_t n_layout, int64_t block_size,
+                             int n_components, float* const* params, const float* const* grads,
+                             float* const* exp_avg, float* const* hessian, const int32_t* widths,
+                             const int64_t* row_strides, const float* lrs, float beta1,
+                             float beta2, float eps, float rho, float batch_size,
+                             int update_hessian, int* error_flag, tgs_stream_t stream);
+/* Touched rows per layout entry (replaces unique_consecutive at
+ * gpu_resident_optimizer.py:293-297): counts [n_layout] i64. */
+int tgs_block_touch_counts(int64_t n_rows, const void* rows, int index_is_i64,
+                           const int64_t* block_starts, const int64_t* block_ends,
+                           int64_t n_layout, int64_t* counts, tgs_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TIDEGS_AMD_H */

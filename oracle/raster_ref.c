@@ -1,0 +1,143 @@
+/*
+ * CPU restatement of gsplat's tile rasterizer (test oracle, not product code).
+ *
+ * Forward follows gsplat/cuda/csrc/rasterize_to_pixels_fwd.cu:14-160, backward
+ * rasterize_to_pixels_bwd.cu:14-249, pixel by pixel and Gaussian by Gaussian in
+ * the same order.  REAL is float (oracle_raster_f32) or double
+ * (oracle_raster_f64); gradients are accumulated in double.  exp() is libm's.
+ * The 32-lane "warp.any" skip of the reference only skips work whose
+ * contributions are zero, so it has no counterpart here.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#ifndef REAL
+#define REAL float
+#endif
+#ifndef SUFFIX
+#define SUFFIX f32
+#endif
+#define CAT2(a, b) a##_##b
+#define CAT(a, b) CAT2(a, b)
+#define FN(name) CAT(name, SUFFIX)
+
+static REAL rmin(REAL a, REAL b) { return a < b ? a : b; }
+
+static REAL rexp(REAL x) { return (REAL)exp((double)x); }
+
+/* means2d [*,2], conics [*,3], colors [*,D], opac [*]; offsets [C,th,tw];
+ * outputs colors [C,H,W,D], alphas [C,H,W], last_ids [C,H,W]. */
+void FN(oracle_raster_fwd)(int C, int D, const REAL* means2d, const REAL* conics,
+                           const REAL* colors, const REAL* opac, const REAL* backgrounds, int W,
+                           int H, int tile, int tw, int th, const int32_t* offsets,
+                           const int32_t* flat, int n_isects, REAL* out_colors, REAL* out_alphas,
+                           int32_t* last_ids) {
+  REAL pix[64];
+  for (int c = 0; c < C; ++c) {
+    for (int i = 0; i < H; ++i) {
+      for (int j = 0; j < W; ++j) {
+        const int tid = (i / tile) * tw + (j / tile);
+        const int64_t toff = (int64_t)c * th * tw + tid;
+        const int start = offsets[toff];
+        const int end = (c == C - 1 && tid == tw * th - 1) ? n_isects : offsets[toff + 1];
+        const REAL px = (REAL)j + (REAL)0.5, py = (REAL)i + (REAL)0.5;
+        REAL T = 1;
+        int cur = 0;
+        for (int k = 0; k < D; ++k) pix[k] = 0;
+        for (int idx = start; idx < end; ++idx) {
+          const int g = flat[idx];
+          const REAL dx = means2d[2 * (int64_t)g] - px, dy = means2d[2 * (int64_t)g + 1] - py;
+          const REAL a = conics[3 * (int64_t)g], b = conics[3 * (int64_t)g + 1],
+                     cc = conics[3 * (int64_t)g + 2];
+          const REAL sigma = (REAL)0.5 * (a * dx * dx + cc * dy * dy) + b * dx * dy;
+          const REAL alpha = rmin((REAL)0.999, opac[g] * rexp(-sigma));
+          if (sigma < 0 || alpha < (REAL)1 / (REAL)255) continue;
+          const REAL next_T = T * (1 - alpha);
+          if (next_T <= (REAL)1e-4) break;
+          const REAL vis = alpha * T;
+          for (int k = 0; k < D; ++k) pix[k] += colors[(int64_t)g * D + k] * vis;
+          cur = idx;
+          T = next_T;
+        }
+        const int64_t pid = ((int64_t)c * H + i) * W + j;
+        out_alphas[pid] = 1 - T;
+        for (int k = 0; k < D; ++k)
+          out_colors[pid * D + k] = backgrounds ? pix[k] + T * backgrounds[c * D + k] : pix[k];
+        last_ids[pid] = cur;
+      }
+    }
+  }
+}
+
+/* Gradients (double, zero-initialised by the caller): v_means2d [*,2],
+ * v_conics [*,3], v_colors [*,D], v_opac [*], v_abs [*,2] (nullable). */
+void FN(oracle_raster_bwd)(int C, int D, const REAL* means2d, const REAL* conics,
+                           const REAL* colors, const REAL* opac, const REAL* backgrounds, int W,
+                           int H, int tile, int tw, int th, const int32_t* offsets,
+                           const int32_t* flat, int n_isects, const REAL* alphas,
+                           const int32_t* last_ids, const REAL* v_out, const REAL* v_alpha_out,
+                           double* v_means2d, double* v_conics, double* v_colors, double* v_opac,
+                           double* v_abs) {
+  REAL buffer[64], v_rc[64];
+  for (int c = 0; c < C; ++c) {
+    for (int i = 0; i < H; ++i) {
+      for (int j = 0; j < W; ++j) {
+        const int tid = (i / tile) * tw + (j / tile);
+        const int64_t toff = (int64_t)c * th * tw + tid;
+        const int start = offsets[toff];
+        const int end = (c == C - 1 && tid == tw * th - 1) ? n_isects : offsets[toff + 1];
+        const REAL px = (REAL)j + (REAL)0.5, py = (REAL)i + (REAL)0.5;
+        const int64_t pid = ((int64_t)c * H + i) * W + j;
+        const REAL T_final = 1 - alphas[pid];
+        REAL T = T_final;
+        const int bin_final = last_ids[pid];
+        REAL bg_dot = 0;
+        for (int k = 0; k < D; ++k) {
+          buffer[k] = 0;
+          v_rc[k] = v_out[pid * D + k];
+          if (backgrounds) bg_dot += backgrounds[c * D + k] * v_rc[k];
+        }
+        const REAL v_ra = v_alpha_out ? v_alpha_out[pid] : 0;
+        for (int idx = end - 1; idx >= start; --idx) {
+          if (idx > bin_final) continue;
+          const int g = flat[idx];
+          const REAL dx = means2d[2 * (int64_t)g] - px, dy = means2d[2 * (int64_t)g + 1] - py;
+          const REAL a = conics[3 * (int64_t)g], b = conics[3 * (int64_t)g + 1],
+                     cc = conics[3 * (int64_t)g + 2];
+          const REAL op = opac[g];
+          const REAL sigma = (REAL)0.5 * (a * dx * dx + cc * dy * dy) + b * dx * dy;
+          const REAL vis = rexp(-sigma);
+          const REAL alpha = rmin((REAL)0.999, op * vis);
+          if (sigma < 0 || alpha < (REAL)1 / (REAL)255) continue;
+          const REAL ra = 1 / (1 - alpha);
+          T *= ra;
+          const REAL fac = alpha * T;
+          REAL v_alpha = 0;
+          for (int k = 0; k < D; ++k) {
+            v_colors[(int64_t)g * D + k] += (double)(fac * v_rc[k]);
+            v_alpha += (colors[(int64_t)g * D + k] * T - buffer[k] * ra) * v_rc[k];
+          }
+          v_alpha += T_final * ra * v_ra;
+          if (backgrounds) v_alpha += -T_final * ra * bg_dot;
+          if (op * vis <= (REAL)0.999) {
+            const REAL v_sigma = -op * vis * v_alpha;
+            v_conics[3 * (int64_t)g + 0] += (double)((REAL)0.5 * v_sigma * dx * dx);
+            v_conics[3 * (int64_t)g + 1] += (double)(v_sigma * dx * dy);
+            v_conics[3 * (int64_t)g + 2] += (double)((REAL)0.5 * v_sigma * dy * dy);
+            const REAL vx = v_sigma * (a * dx + b * dy);
+            const REAL vy = v_sigma * (b * dx + cc * dy);
+            v_means2d[2 * (int64_t)g + 0] += (double)vx;
+            v_means2d[2 * (int64_t)g + 1] += (double)vy;
+            if (v_abs) {
+              v_abs[2 * (int64_t)g + 0] += fabs((double)vx);
+              v_abs[2 * (int64_t)g + 1] += fabs((double)vy);
+            }
+            v_opac[g] += (double)(vis * v_alpha);
+          }
+          for (int k = 0; k < D; ++k) buffer[k] += colors[(int64_t)g * D + k] * fac;
+        }
+      }
+    }
+  }
+}

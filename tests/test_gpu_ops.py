@@ -1,0 +1,293 @@
+"""GPU parity of the gsplat / clm_kernels drop-in ops against the CPU oracle.
+
+Tolerances: integer/index outputs bit-exact (isect ids, flatten ids,
+offsets, sort); floating-point gradients within relative L2 <= 1e-4 of the
+oracle (atomics reorder sums), forward values within
+1e-4 relative.  Radii may differ by +-1 on a small fraction of Gaussians, as
+gsplat's own test allows (test_basic.py:219-221).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gsplat_ref as G
+from oracle import raster_ref as R
+from oracle import ssim_ref as S
+from tests.gpu_util import announce, rel_l2, to_np
+from tidegs_amd import gsplat_ops as ops
+from tidegs_amd import scenes
+from tidegs_amd.clm_ops import FusedSSIMMap, fused_ssim
+
+pytestmark = pytest.mark.gpu
+
+
+def _proj_inputs(seed=0, n=3000, C=3, W=96, H=64):
+    sc = scenes.small(seed=seed, n=n, n_cams=C, W=W, H=H)
+    means, quats, scales, opac, sh = scenes.activations(sc.params)
+    return sc, means.contiguous(), quats.contiguous(), scales.contiguous()
+
+
+@pytest.mark.parametrize("calc_comp", [False, True])
+def test_projection_fwd_bwd(gpu, calc_comp):
+    announce(f"projection calc_comp={calc_comp}")
+    sc, means, quats, scales = _proj_inputs()
+    W, H = sc.width, sc.height
+    dm = means.to(gpu).requires_grad_()
+    dq = quats.to(gpu).requires_grad_()
+    ds = scales.to(gpu).requires_grad_()
+    dv = sc.viewmats.to(gpu).requires_grad_()
+    radii, m2d, depths, conics, comps = ops.fully_fused_projection(
+        dm, None, dq, ds, dv, sc.Ks.to(gpu), W, H, calc_compensations=calc_comp)
+    o_radii, o_m2d, o_depths, o_conics, o_comps = G.project_fwd(
+        means, quats, scales, sc.viewmats, sc.Ks, W, H)
+    r_gpu, r_ref = to_np(radii), to_np(o_radii)
+    assert (r_ref > 0).sum() > 1000
+    same = r_gpu == r_ref
+    assert same.mean() > 0.998, same.mean()
+    assert np.abs(r_gpu - r_ref).max() <= 1 or same.mean() > 0.999
+    both = (r_gpu > 0) & (r_ref > 0)
+    assert rel_l2(to_np(m2d)[both], to_np(o_m2d)[both]) < 1e-6
+    assert rel_l2(to_np(depths)[both], to_np(o_depths)[both]) < 1e-6
+    assert rel_l2(to_np(conics)[both], to_np(o_conics)[both]) < 1e-5
+    if calc_comp:
+        assert rel_l2(to_np(comps)[both], to_np(o_comps)[both]) < 1e-5
+    # backward with cotangents on entries live in both
+    g = torch.Generator().manual_seed(1)
+    live = torch.from_numpy(both)
+    w_m = torch.randn(m2d.shape, generator=g) * live[..., None]
+    w_d = torch.randn(depths.shape, generator=g) * live
+    w_c = torch.randn(conics.shape, generator=g) * live[..., None]
+    w_k = torch.randn(depths.shape, generator=g) * live if calc_comp else None
+    L = (m2d * w_m.to(gpu)).sum() + (depths * w_d.to(gpu)).sum() + (conics * w_c.to(gpu)).sum()
+    if calc_comp:
+        L = L + (comps * w_k.to(gpu)).sum()
+    L.backward()
+    rad_both = torch.from_numpy(np.where(both, r_ref, 0))
+    v_means, v_quats, v_scales, _, v_vm = G.project_bwd(
+        means, quats, scales, sc.viewmats, sc.Ks, W, H, 0.3, rad_both, o_conics, w_m, w_d, w_c,
+        compensations=o_comps if calc_comp else None, v_compensations=w_k, want_viewmats=True)
+    assert rel_l2(to_np(dm.grad), v_means) < 1e-4
+    assert rel_l2(to_np(dq.grad), v_quats) < 1e-4
+    assert rel_l2(to_np(ds.grad), v_scales) < 1e-4
+    assert rel_l2(to_np(dv.grad)[:, :3], to_np(v_vm)[:, :3]) < 1e-4
+
+
+def test_projection_covars(gpu):
+    announce("projection covars")
+    sc, means, quats, scales = _proj_inputs(seed=1, C=2)
+    W, H = sc.width, sc.height
+    cov6 = G.covar_from_quat_scale(quats.double(), scales.double())[:, [0, 0, 0, 1, 1, 2],
+                                                                    [0, 1, 2, 1, 2, 2]].float()
+    dm = means.to(gpu).requires_grad_()
+    dc = cov6.to(gpu).requires_grad_()
+    radii, m2d, depths, conics, _ = ops.fully_fused_projection(
+        dm, dc, None, None, sc.viewmats.to(gpu), sc.Ks.to(gpu), W, H)
+    o_radii, o_m2d, o_depths, o_conics, _ = G.project_fwd(means, None, None, sc.viewmats, sc.Ks,
+                                                          W, H, covars=cov6)
+    both = (to_np(radii) > 0) & (to_np(o_radii) > 0) & (to_np(radii) == to_np(o_radii))
+    assert rel_l2(to_np(conics)[both], to_np(o_conics)[both]) < 1e-5
+    g = torch.Generator().manual_seed(2)
+    live = torch.from_numpy(both)
+    w_m = torch.randn(m2d.shape, generator=g) * live[..., None]
+    w_c = torch.randn(conics.shape, generator=g) * live[..., None]
+    ((m2d * w_m.to(gpu)).sum() + (conics * w_c.to(gpu)).sum()).backward()
+    v_means, _, _, v_cov, _ = G.project_bwd(
+        means, None, None, sc.viewmats, sc.Ks, W, H, 0.3, torch.from_numpy(np.where(both, 1, 0)),
+        o_conics, w_m, None, w_c, covars=cov6)
+    assert rel_l2(to_np(dm.grad), v_means) < 1e-4
+    assert rel_l2(to_np(dc.grad), v_cov) < 1e-4
+
+
+@pytest.mark.parametrize("degree,K", [(0, 16), (1, 16), (2, 9), (3, 16), (4, 25)])
+def test_spherical_harmonics(gpu, degree, K):
+    announce(f"sh degree={degree} K={K}")
+    g = torch.Generator().manual_seed(degree)
+    dirs = torch.randn((4097, 3), generator=g)
+    coeffs = torch.randn((4097, K, 3), generator=g)
+    masks = torch.rand(4097, generator=g) > 0.2
+    v = torch.randn((4097, 3), generator=g)
+    d_dirs = dirs.to(gpu).requires_grad_()
+    d_coeffs = coeffs.to(gpu).requires_grad_()
+    col = ops.spherical_harmonics(degree, d_dirs, d_coeffs, masks=masks.to(gpu))
+    ref = G.sh_fwd(degree, dirs, coeffs) * masks[:, None]
+    assert rel_l2(to_np(col), ref) < 1e-6
+    (col * v.to(gpu)).sum().backward()
+    vc, vd = G.sh_bwd(degree, dirs, coeffs, v * masks[:, None])
+    assert rel_l2(to_np(d_coeffs.grad), vc) < 1e-6
+    if degree > 0:
+        assert rel_l2(to_np(d_dirs.grad), vd) < 1e-5
+    else:
+        assert float(d_dirs.grad.abs().max()) == 0.0
+
+
+def _projected(gpu, seed=0, n=20000, C=2, W=200, H=120, log_scale_mu=-2.5):
+    sc = scenes.small(seed=seed, n=n, n_cams=C, W=W, H=H, log_scale_mu=log_scale_mu)
+    means, quats, scales, opac, sh = scenes.activations(sc.params)
+    with torch.no_grad():
+        radii, m2d, depths, conics, _ = ops.fully_fused_projection(
+            means.to(gpu), None, quats.to(gpu), scales.to(gpu), sc.viewmats.to(gpu),
+            sc.Ks.to(gpu), W, H)
+    return sc, radii, m2d, depths, conics, opac
+
+
+@pytest.mark.parametrize("C", [1, 3])
+def test_isect_tiles_bit_exact(gpu, C):
+    announce(f"isect C={C}")
+    sc, radii, m2d, depths, conics, _ = _projected(gpu, seed=3, C=C)
+    W, H, ts = sc.width, sc.height, 16
+    tw, th = -(-W // ts), -(-H // ts)
+    tiles, ids, flat = ops.isect_tiles(m2d, radii, depths, ts, tw, th)
+    o_tiles, o_ids, o_flat = R.isect_tiles(to_np(m2d), to_np(radii), to_np(depths), ts, tw, th)
+    assert ids.numel() > 10000
+    np.testing.assert_array_equal(to_np(tiles), o_tiles)
+    np.testing.assert_array_equal(to_np(ids), o_ids)
+    np.testing.assert_array_equal(to_np(flat), o_flat)
+    offs = ops.isect_offset_encode(ids, C, tw, th)
+    np.testing.assert_array_equal(to_np(offs), R.isect_offset_encode(o_ids, C, tw, th))
+
+
+def test_isect_tiles_packed_and_empty(gpu):
+    announce("isect packed + empty")
+    sc, radii, m2d, depths, _, _ = _projected(gpu, seed=4, C=2)
+    W, H, ts = sc.width, sc.height, 16
+    tw, th = -(-W // ts), -(-H // ts)
+    cam, gid = torch.nonzero(radii > 0, as_tuple=True)
+    tiles, ids, flat = ops.isect_tiles(m2d[cam, gid].contiguous(), radii[cam, gid].contiguous(),
+                                       depths[cam, gid].contiguous(), ts, tw, th, packed=True,
+                                       n_cameras=2, camera_ids=cam, gaussian_ids=gid)
+    o_tiles, o_ids, o_flat = R.isect_tiles(to_np(m2d[cam, gid]), to_np(radii[cam, gid]),
+                                           to_np(depths[cam, gid]), ts, tw, th,
+                                           camera_ids=to_np(cam))
+    np.testing.assert_array_equal(to_np(ids), o_ids)
+    np.testing.assert_array_equal(to_np(flat), o_flat)
+    # nothing visible: empty outputs and all-zero offsets (isect_tiles.cu:298)
+    z = torch.zeros_like(radii)
+    tiles, ids, flat = ops.isect_tiles(m2d, z, depths, ts, tw, th)
+    assert ids.numel() == 0 and int(tiles.abs().sum()) == 0
+    offs = ops.isect_offset_encode(ids, 2, tw, th)
+    assert offs.shape == (2, th, tw) and int(offs.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("n,begin,end", [(1, 0, 64), (100, 0, 46), (4097, 3, 40),
+                                         (1_000_003, 0, 46), (70_000, 0, 64)])
+def test_radix_sort_pairs_stable(gpu, n, begin, end):
+    announce(f"radix n={n} bits=[{begin},{end})")
+    rng = np.random.default_rng(n)
+    keys = rng.integers(-2 ** 62, 2 ** 62, size=n, dtype=np.int64)
+    keys[: n // 3] = keys[n // 3: 2 * (n // 3)]  # duplicates exercise stability
+    vals = np.arange(n, dtype=np.int32)
+    k, v = ops.radix_sort_pairs(torch.from_numpy(keys).to(gpu), torch.from_numpy(vals).to(gpu),
+                                begin, end)
+    span = end - begin
+    masked = (keys.view(np.uint64) >> np.uint64(begin)) & np.uint64((1 << span) - 1 if span < 64
+                                                                    else 2 ** 64 - 1)
+    order = np.argsort(masked, kind="stable")
+    np.testing.assert_array_equal(to_np(v), vals[order])
+    np.testing.assert_array_equal(to_np(k), keys[order])
+
+
+def _raster_case(gpu, seed, C=2, D=3, W=200, H=120, tile=16, packed=False):
+    sc, radii, m2d, depths, conics, opac = _projected(gpu, seed=seed, C=C, W=W, H=H)
+    tw, th = -(-W // tile), -(-H // tile)
+    g = torch.Generator().manual_seed(seed)
+    Nn = radii.shape[1]
+    colors = torch.rand((C, Nn, D), generator=g).to(gpu)
+    opacs = opac[None].repeat(C, 1).to(gpu).contiguous()
+    if packed:
+        cam, gid = torch.nonzero(radii > 0, as_tuple=True)
+        m2d, conics, colors, opacs = (m2d[cam, gid].contiguous(), conics[cam, gid].contiguous(),
+                                      colors[cam, gid].contiguous(), opacs[cam, gid].contiguous())
+        _, ids, flat = ops.isect_tiles(m2d, radii[cam, gid].contiguous(),
+                                       depths[cam, gid].contiguous(), tile, tw, th, packed=True,
+                                       n_cameras=C, camera_ids=cam, gaussian_ids=gid)
+    else:
+        _, ids, flat = ops.isect_tiles(m2d, radii, depths, tile, tw, th)
+    offs = ops.isect_offset_encode(ids, C, tw, th)
+    return m2d, conics, colors, opacs, offs, flat
+
+
+@pytest.mark.parametrize("D,tile,bg,packed,absgrad", [
+    (3, 16, False, False, False), (3, 16, True, False, True), (1, 16, False, False, False),
+    (4, 8, True, False, False), (5, 16, False, False, False), (32, 16, False, True, False),
+    (3, 16, False, True, True)])
+def test_rasterize_fwd_bwd(gpu, D, tile, bg, packed, absgrad):
+    announce(f"raster D={D} tile={tile} bg={bg} packed={packed} absgrad={absgrad}")
+    C, W, H = 2, 200, 120
+    m2d, conics, colors, opacs, offs, flat = _raster_case(gpu, seed=10 + D, C=C, D=D, W=W, H=H,
+                                                          tile=tile, packed=packed)
+    g = torch.Generator().manual_seed(D)
+    bgs = torch.rand((C, D), generator=g).to(gpu) if bg else None
+    leaves = [t.clone().requires_grad_() for t in (m2d, conics, colors, opacs)]
+    if bg:
+        bgs.requires_grad_()
+    rc, ra = ops.rasterize_to_pixels(*leaves, W, H, tile, offs, flat, backgrounds=bgs,
+                                     packed=packed, absgrad=absgrad)
+    ref_c, ref_a, ref_last = R.rasterize_fwd(
+        to_np(m2d).reshape(-1, 2), to_np(conics).reshape(-1, 3), to_np(colors).reshape(-1, D),
+        to_np(opacs).reshape(-1), W, H, tile, to_np(offs), to_np(flat),
+        backgrounds=to_np(bgs) if bg else None)
+    assert rel_l2(to_np(rc), ref_c) < 1e-5
+    assert rel_l2(to_np(ra)[..., 0], ref_a) < 1e-5
+    wc = torch.randn(rc.shape, generator=g)
+    wa = torch.randn(ra.shape, generator=g)
+    ((rc * wc.to(gpu)).sum() + (ra * wa.to(gpu)).sum()).backward()
+    # oracle backward from the GPU's own forward state
+    _, _, last = R.rasterize_fwd(
+        to_np(m2d).reshape(-1, 2), to_np(conics).reshape(-1, 3), to_np(colors).reshape(-1, D),
+        to_np(opacs).reshape(-1), W, H, tile, to_np(offs), to_np(flat))
+    vm, vc, vcol, vo, vabs = R.rasterize_bwd(
+        to_np(m2d).reshape(-1, 2), to_np(conics).reshape(-1, 3), to_np(colors).reshape(-1, D),
+        to_np(opacs).reshape(-1), W, H, tile, to_np(offs), to_np(flat), ref_a, ref_last,
+        to_np(wc), v_alphas=to_np(wa)[..., 0], backgrounds=to_np(bgs) if bg else None,
+        absgrad=absgrad)
+    assert rel_l2(to_np(leaves[0].grad).reshape(-1, 2), vm) < 1e-4
+    assert rel_l2(to_np(leaves[1].grad).reshape(-1, 3), vc) < 1e-4
+    assert rel_l2(to_np(leaves[2].grad).reshape(-1, D), vcol) < 1e-4
+    assert rel_l2(to_np(leaves[3].grad).reshape(-1), vo) < 1e-4
+    if absgrad:
+        assert rel_l2(to_np(leaves[0].absgrad).reshape(-1, 2), vabs) < 1e-4
+    if bg:
+        ref_vbg = (to_np(wc) * (1 - ref_a[..., None])).sum(axis=(1, 2))
+        assert rel_l2(to_np(bgs.grad), ref_vbg) < 1e-5
+
+
+def test_fused_ssim(gpu):
+    announce("fused_ssim")
+    g = torch.Generator().manual_seed(0)
+    a = torch.rand((2, 3, 67, 91), generator=g)
+    b = torch.rand((2, 3, 67, 91), generator=g)
+    da = a.to(gpu).requires_grad_()
+    m = FusedSSIMMap.apply(0.01 ** 2, 0.03 ** 2, da, b.to(gpu), "same", True)
+    rm, d1, d2, d3 = S.ssim_fwd(a.numpy(), b.numpy())
+    assert rel_l2(to_np(m), rm) < 1e-5
+    gm = torch.randn(m.shape, generator=g)
+    (m * gm.to(gpu)).sum().backward()
+    ref = S.ssim_bwd(a.numpy(), b.numpy(), gm.numpy(), d1, d2, d3)
+    assert rel_l2(to_np(da.grad), ref) < 1e-5
+    val = fused_ssim(a.to(gpu), b.to(gpu), padding="valid")
+    assert abs(float(val) - float(rm[:, :, 5:-5, 5:-5].mean())) < 1e-5
+
+
+def test_tide_loss_kernels(gpu):
+    announce("tide loss (L1 + SSIM)")
+    from tidegs_amd import _native as N
+
+    g = torch.Generator().manual_seed(3)
+    H, W = 70, 130
+    img = torch.rand((H, W, 3), generator=g)
+    gt = torch.rand((3, H, W), generator=g) * 300 - 20
+    d_img, d_gt = img.to(gpu), gt.to(gpu)
+    parts = [torch.empty((3, H, W), device=gpu) for _ in range(3)]
+    sums = torch.zeros(2, dtype=torch.float64, device=gpu)
+    s = N.stream_handle()
+    N.call("tgs_tide_loss_fwd", H, W, N.ptr(d_img), N.ptr(d_gt), 255.0, *[N.ptr(p) for p in parts],
+           N.ptr(sums), s)
+    v = torch.empty((H, W, 3), device=gpu)
+    N.call("tgs_tide_loss_bwd", H, W, N.ptr(d_img), N.ptr(d_gt), 255.0, 0.2,
+           *[N.ptr(p) for p in parts], N.ptr(v), s)
+    loss_ref, grad_ref = S.tide_loss(img.permute(2, 0, 1).numpy(), gt.numpy())
+    n = 3 * H * W
+    sums = to_np(sums)
+    loss = 0.8 * sums[0] / n + 0.2 * (1 - sums[1] / n)
+    assert abs(loss - loss_ref) < 1e-6
+    assert rel_l2(to_np(v).transpose(2, 0, 1), grad_ref) < 1e-5

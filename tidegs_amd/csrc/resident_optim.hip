@@ -1,0 +1,291 @@
+// Fused resident-slot optimizer steps (Adam and Sophia) over touched rows.
+//
+// Semantics follow TideGS's GPUResidentAdam
+// (strategies/tide_engine/gpu_resident_optimizer.py:16-70 kernel, :266-300 slot
+// mapping, :302-337 per-slot bias tables):
+//   g  = grad / batch_size
+//   m  = b1*m + (1-b1)*g
+//   v  = b2*v + (1-b2)*g*g
+//   p -= (lr_col / bias1[slot]) * m / (sqrt(v)/denom_scale[slot] + eps)
+// where a touched working-set row maps to its resident state row through the
+// block layout (sorted [start,end) slices, one state slot per block):
+//   pos = #ends <= row, state_row = slot[pos]*block_size + (row - start[pos]).
+//
+// The reference issues one Triton launch per component (6 per step) plus host
+// searchsorted/index_select.  Here a single launch covers all 59 columns: one
+// wavefront owns one touched row at a time, lane l handles column l (59 of 64
+// lanes busy), and the row -> (slot, state row) lookup is a wave-uniform binary
+// search that runs on the scalar unit.  The column -> (component tensor,
+// column) map is fixed per lane, so the same kernel serves six split component
+// tensors or one unified [N,59] table.
+//
+// Sophia (no reference; Liu et al. 2023, arXiv 2305.14342, Alg. 3 with the
+// per-coordinate clip of SURVEY row A14):
+//   m  = b1*m + (1-b1)*g
+//   h  = b2*h + (1-b2)*g*g        (only on Hessian-refresh steps)
+//   p -= lr_col * clamp(m / max(h, eps), -rho, rho)
+
+#include "tgs_common.cuh"
+
+#define TGS_MAX_COMP 8
+
+struct OptimComponents {
+  float* param[TGS_MAX_COMP];
+  const float* grad[TGS_MAX_COMP];
+  float* m[TGS_MAX_COMP];
+  float* v[TGS_MAX_COMP];
+  int width[TGS_MAX_COMP];
+  int64_t pstride[TGS_MAX_COMP];  // row strides (elements) of param, grad, state
+  int64_t gstride[TGS_MAX_COMP];
+  int64_t sstride[TGS_MAX_COMP];
+  float lr[TGS_MAX_COMP];
+  int n;
+};
+
+struct OptimLayout {
+  const int64_t* starts;  // [L] sorted ascending
+  const int64_t* ends;    // [L]
+  const int64_t* slots;   // [L]
+  int64_t n;              // L
+  int64_t block_size;
+};
+
+// Resolve lane -> (component, column); lanes beyond the total width get comp=-1.
+__device__ __forceinline__ void lane_column(const OptimComponents& c, int lane, int& comp,
+                                            int& col) {
+  comp = -1;
+  col = 0;
+  int base = 0;
+#pragma unroll
+  for (int k = 0; k < TGS_MAX_COMP; ++k) {
+    if (k < c.n) {
+      if (lane >= base && lane < base + c.width[k]) {
+        comp = k;
+        col = lane - base;
+      }
+      base += c.width[k];
+    }
+  }
+}
+
+// Number of ends <= row (searchsorted right=True), wave-uniform.
+__device__ __forceinline__ int64_t layout_search(const OptimLayout& L, int64_t row) {
+  int64_t lo = 0, hi = L.n;
+  while (lo < hi) {
+    int64_t mid = (lo + hi) >> 1;
+    if (L.ends[mid] <= row)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+template <typename IdxT, bool SOPHIA>
+__global__ void __launch_bounds__(256) resident_optim_kernel(
+    int64_t n_rows, const IdxT* __restrict__ local_rows, OptimLayout L,
+    const float* __restrict__ bias1, const float* __restrict__ denom_scale, OptimComponents C,
+    float beta1, float beta2, float eps, float batch_size, float rho, int update_h,
+    int* __restrict__ error_flag) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t n_waves = (int64_t)gridDim.x * (blockDim.x >> 6);
+
+  int comp, col;
+  lane_column(C, lane, comp, col);
+  const bool active = comp >= 0;
+  float* param = nullptr;
+  const float* grad = nullptr;
+  float* m = nullptr;
+  float* v = nullptr;
+  int64_t pstride = 0, gstride = 0, sstride = 0;
+  float lr = 0.f;
+  if (active) {
+    param = C.param[comp];
+    grad = C.grad[comp];
+    m = C.m[comp];
+    v = C.v[comp];
+    pstride = C.pstride[comp];
+    gstride = C.gstride[comp];
+    sstride = C.sstride[comp];
+    lr = C.lr[comp];
+  }
+  const float one_m_b1 = 1.0f - beta1;
+  const float one_m_b2 = 1.0f - beta2;
+
+  for (int64_t t = wave; t < n_rows; t += n_waves) {
+    const int64_t row = (int64_t)local_rows[t];
+    const int64_t pos = layout_search(L, row);
+    bool ok = pos < L.n;
+    int64_t in_block = 0, slot = 0;
+    if (ok) {
+      in_block = row - L.starts[pos];
+      slot = L.slots[pos];
+      ok = in_block >= 0 && in_block < L.block_size && row < L.ends[pos];
+    }
+    if (!ok) {
+      // A touched row outside every resident block: the host checks this flag
+      // and raises (the reference raises on a missing slot, :275-279).
+      if (lane == 0) atomicOr(error_flag, 1);
+      continue;
+    }
+    if (!active) continue;
+    const int64_t state_row = slot * L.block_size + in_block;
+    const int64_t poff = row * pstride + col;
+    const int64_t soff = state_row * sstride + col;
+    float g = grad[t * gstride + col] / batch_size;
+    float mm = m[soff];
+    float vv = v[soff];
+    float p = param[poff];
+    mm = beta1 * mm + one_m_b1 * g;
+    if (SOPHIA) {
+      if (update_h) vv = beta2 * vv + one_m_b2 * g * g;
+      float r = mm / fmaxf(vv, eps);
+      r = fminf(fmaxf(r, -rho), rho);
+      p -= lr * r;
+    } else {
+      vv = beta2 * vv + one_m_b2 * g * g;
+      const float denom = sqrtf(vv) / denom_scale[slot] + eps;
+      p -= (lr / bias1[slot]) * mm / denom;
+    }
+    m[soff] = mm;
+    v[soff] = vv;
+    param[poff] = p;
+  }
+}
+
+// Per layout entry: number of touched rows inside [start,end) of the sorted
+// touched-row list (replaces unique_consecutive + D2H at :293-297 with one
+// tiny kernel; the host still reads the counts back to advance slot steps).
+template <typename IdxT>
+__global__ void block_touch_counts_kernel(int64_t n_rows, const IdxT* __restrict__ rows,
+                                          OptimLayout L, int64_t* __restrict__ counts) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= L.n) return;
+  auto lower = [&](int64_t key) {
+    int64_t lo = 0, hi = n_rows;
+    while (lo < hi) {
+      int64_t mid = (lo + hi) >> 1;
+      if ((int64_t)rows[mid] < key)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    return lo;
+  };
+  counts[i] = lower(L.ends[i]) - lower(L.starts[i]);
+}
+
+static int fill_components(OptimComponents& C, int n_comp, float* const* params,
+                           const float* const* grads, float* const* m, float* const* v,
+                           const int32_t* widths, const int64_t* strides, const float* lrs) {
+  TGS_CHECK_ARG(n_comp >= 1 && n_comp <= TGS_MAX_COMP, "n_components must be in [1,%d]",
+                TGS_MAX_COMP);
+  int total = 0;
+  C.n = n_comp;
+  for (int k = 0; k < TGS_MAX_COMP; ++k) {
+    if (k < n_comp) {
+      TGS_CHECK_ARG(params[k] && grads[k] && m[k] && v[k], "component %d has a null pointer", k);
+      TGS_CHECK_ARG(widths[k] >= 1, "component %d width must be >= 1", k);
+      C.param[k] = params[k];
+      C.grad[k] = grads[k];
+      C.m[k] = m[k];
+      C.v[k] = v[k];
+      C.width[k] = widths[k];
+      C.pstride[k] = strides ? strides[3 * k + 0] : widths[k];
+      C.gstride[k] = strides ? strides[3 * k + 1] : widths[k];
+      C.sstride[k] = strides ? strides[3 * k + 2] : widths[k];
+      TGS_CHECK_ARG(C.pstride[k] >= widths[k] && C.gstride[k] >= widths[k] &&
+                        C.sstride[k] >= widths[k],
+                    "component %d: row stride smaller than its width", k);
+      C.lr[k] = lrs[k];
+      total += widths[k];
+    } else {
+      C.param[k] = nullptr;
+      C.grad[k] = nullptr;
+      C.m[k] = nullptr;
+      C.v[k] = nullptr;
+      C.width[k] = 0;
+      C.pstride[k] = C.gstride[k] = C.sstride[k] = 0;
+      C.lr[k] = 0.f;
+    }
+  }
+  TGS_CHECK_ARG(total <= 64, "total row width %d exceeds one wavefront (64)", total);
+  return TGS_OK;
+}
+
+template <bool SOPHIA>
+static int launch_optim(int64_t n_rows, const void* local_rows, int index_is_i64,
+                        const int64_t* starts, const int64_t* ends, const int64_t* slots,
+                        int64_t n_layout, int64_t block_size, const float* bias1,
+                        const float* denom_scale, int n_comp, float* const* params,
+                        const float* const* grads, float* const* m, float* const* v,
+                        const int32_t* widths, const int64_t* strides, const float* lrs,
+                        float beta1, float beta2, float eps, float batch_size, float rho,
+                        int update_h, int* error_flag, hipStream_t stream) {
+  TGS_CHECK_ARG(n_rows >= 0, "n_rows must be >= 0");
+  if (n_rows == 0) return TGS_OK;
+  TGS_CHECK_ARG(local_rows && starts && ends && slots && error_flag, "null index pointer");
+  TGS_CHECK_ARG(n_layout >= 1 && block_size >= 1, "empty block layout");
+  if (!SOPHIA) TGS_CHECK_ARG(bias1 && denom_scale, "null bias table");
+  OptimComponents C;
+  int rc = fill_components(C, n_comp, params, grads, m, v, widths, strides, lrs);
+  if (rc) return rc;
+  OptimLayout L{starts, ends, slots, n_layout, block_size};
+  const int threads = 256;
+  // ~8 resident waves per SIMD over 256 CUs; rows are strided over waves.
+  int64_t waves_needed = n_rows;
+  int64_t blocks = (waves_needed + 3) / 4;
+  if (blocks > 256 * 32) blocks = 256 * 32;
+  if (index_is_i64)
+    hipLaunchKernelGGL((resident_optim_kernel<int64_t, SOPHIA>), dim3((unsigned)blocks),
+                       dim3(threads), 0, stream, n_rows, (const int64_t*)local_rows, L, bias1,
+                       denom_scale, C, beta1, beta2, eps, batch_size, rho, update_h, error_flag);
+  else
+    hipLaunchKernelGGL((resident_optim_kernel<int32_t, SOPHIA>), dim3((unsigned)blocks),
+                       dim3(threads), 0, stream, n_rows, (const int32_t*)local_rows, L, bias1,
+                       denom_scale, C, beta1, beta2, eps, batch_size, rho, update_h, error_flag);
+  TGS_RETURN_LAUNCH(SOPHIA ? "tgs_resident_sophia_step" : "tgs_resident_adam_step");
+}
+
+extern "C" int tgs_resident_adam_step(
+    int64_t n_rows, const void* local_rows, int index_is_i64, const int64_t* block_starts,
+    const int64_t* block_ends, const int64_t* block_slots, int64_t n_layout, int64_t block_size,
+    const float* bias_correction1, const float* denom_scale, int n_components,
+    float* const* params, const float* const* grads, float* const* exp_avg,
+    float* const* exp_avg_sq, const int32_t* widths, const int64_t* row_strides, const float* lrs,
+    float beta1, float beta2, float eps, float batch_size, int* error_flag, hipStream_t stream) {
+  return launch_optim<false>(n_rows, local_rows, index_is_i64, block_starts, block_ends,
+                             block_slots, n_layout, block_size, bias_correction1, denom_scale,
+                             n_components, params, grads, exp_avg, exp_avg_sq, widths, row_strides,
+                             lrs, beta1, beta2, eps, batch_size, 0.f, 1, error_flag, stream);
+}
+
+extern "C" int tgs_resident_sophia_step(
+    int64_t n_rows, const void* local_rows, int index_is_i64, const int64_t* block_starts,
+    const int64_t* block_ends, const int64_t* block_slots, int64_t n_layout, int64_t block_size,
+    int n_components, float* const* params, const float* const* grads, float* const* exp_avg,
+    float* const* hessian, const int32_t* widths, const int64_t* row_strides, const float* lrs,
+    float beta1, float beta2, float eps, float rho, float batch_size, int update_hessian,
+    int* error_flag, hipStream_t stream) {
+  return launch_optim<true>(n_rows, local_rows, index_is_i64, block_starts, block_ends,
+                            block_slots, n_layout, block_size, nullptr, nullptr, n_components,
+                            params, grads, exp_avg, hessian, widths, row_strides, lrs, beta1,
+                            beta2, eps, batch_size, rho, update_hessian, error_flag, stream);
+}
+
+extern "C" int tgs_block_touch_counts(int64_t n_rows, const void* rows, int index_is_i64,
+                                      const int64_t* block_starts, const int64_t* block_ends,
+                                      int64_t n_layout, int64_t* counts, hipStream_t stream) {
+  TGS_CHECK_ARG(n_layout >= 0 && n_rows >= 0, "negative size");
+  if (n_layout == 0) return TGS_OK;
+  TGS_CHECK_ARG(block_starts && block_ends && counts && (rows || n_rows == 0), "null pointer");
+  OptimLayout L{block_starts, block_ends, nullptr, n_layout, 0};
+  if (index_is_i64)
+    hipLaunchKernelGGL(block_touch_counts_kernel<int64_t>, dim3(tgs_blocks(n_layout, 256)),
+                       dim3(256), 0, stream, n_rows, (const int64_t*)rows, L, counts);
+  else
+    hipLaunchKernelGGL(block_touch_counts_kernel<int32_t>, dim3(tgs_blocks(n_layout, 256)),
+                       dim3(256), 0, stream, n_rows, (const int32_t*)rows, L, counts);
+  TGS_RETURN_LAUNCH("tgs_block_touch_counts");
+}

@@ -1,0 +1,286 @@
+// Fused 11x11 Gaussian-window SSIM (sigma 1.5, zero padding, "same" output)
+// forward with the three partial-derivative maps, and its backward.
+//
+// Reference: clm_kernels/ssim.cu:187-286 (fusedssimCUDA), :288-366
+// (fusedssim_backwardCUDA), clm_kernels/__init__.py:23-61 (autograd wrapper;
+// C1 = 0.01^2, C2 = 0.03^2).  Per pixel and channel:
+//   mu = G*x, sigma_xx = G*(x^2) - mu^2, sigma_xy = G*(xy) - mu1 mu2
+//   C = 2 mu1 mu2 + C1, D = 2 sigma12 + C2, A = mu1^2 + mu2^2 + C1,
+//   B = sigma1^2 + sigma2^2 + C2, m = C D / (A B)
+//   dm/dmu1, dm/dsigma1^2 (= -C D / (A B^2)), dm/dsigma12 (= 2 C / (A B))
+// Backward: dL/dx = G*(g dm/dmu1) + 2 x G*(g dm/dsigma1^2) + y G*(g dm/dsigma12).
+//
+// Layout is given by strides (channel, row, column) so one kernel serves NCHW
+// tensors (drop-in fused_ssim) and the HWC rendered image of the fused step.
+// A 16x16 output tile per 256-thread workgroup with a 26x26 halo in LDS;
+// separable passes in the same order as the reference (x first, then y).
+// The fused-step mode also folds in the L1 term and the clamp(gt/255, 0, 1)
+// target normalisation of strategies/base_engine.py:472-488.
+#include "tgs_common.cuh"
+
+#define SS_T 16
+#define SS_R 5
+#define SS_H (SS_T + 2 * SS_R)  // 26
+
+// Normalised Gaussian window, w_i = exp(-(i-5)^2 / 4.5) / sum_j exp(-(j-5)^2 / 4.5).
+__constant__ float c_gauss[11] = {
+    0.001028380123898387f, 0.0075987582094967365f, 0.036000773310661316f,
+    0.10936068743467331f,  0.21300552785396576f,   0.26601171493530273f,
+    0.21300552785396576f,  0.10936068743467331f,   0.036000773310661316f,
+    0.0075987582094967365f, 0.001028380123898387f};
+
+struct Img {
+  const float* p;
+  int64_t bs, cs, ys, xs;  // batch, channel, row, column strides (elements)
+  float div;               // value = clamp?(p / div)
+  int clamp01;
+  __device__ __forceinline__ float at(int b, int c, int y, int x, int H, int W) const {
+    if (x < 0 || y < 0 || x >= W || y >= H) return 0.f;
+    float v = p[b * bs + c * cs + (int64_t)y * ys + (int64_t)x * xs] / div;
+    if (clamp01) v = fminf(fmaxf(v, 0.f), 1.f);
+    return v;
+  }
+};
+
+struct OutImg {
+  float* p;
+  int64_t bs, cs, ys, xs;
+  __device__ __forceinline__ float& at(int b, int c, int y, int x) const {
+    return p[b * bs + c * cs + (int64_t)y * ys + (int64_t)x * xs];
+  }
+};
+
+// Horizontal pass over the 26 halo rows for the 16 output columns, then the
+// vertical pass for this thread's output pixel.  `q` computes the quantity to
+// filter from the two halo tiles.
+template <int NQ, class Q>
+__device__ __forceinline__ void sep_conv(float (*h)[SS_H][SS_T], Q q, float out[NQ]) {
+  const int tid = threadIdx.x;
+  for (int e = tid; e < SS_H * SS_T; e += 256) {
+    const int r = e / SS_T, c = e % SS_T;
+    float acc[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) acc[k] = 0.f;
+#pragma unroll
+    for (int t = 0; t < 11; ++t) {
+      float v[NQ];
+      q(r, c + t, v);
+#pragma unroll
+      for (int k = 0; k < NQ; ++k) acc[k] += c_gauss[t] * v[k];
+    }
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) h[k][r][c] = acc[k];
+  }
+  __syncthreads();
+  const int ty = tid / SS_T, tx = tid % SS_T;
+#pragma unroll
+  for (int k = 0; k < NQ; ++k) {
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < 11; ++t) acc += c_gauss[t] * h[k][ty + t][tx];
+    out[k] = acc;
+  }
+}
+
+__global__ void __launch_bounds__(256) ssim_fwd_kernel(int B, int CH, int H, int W, float C1,
+                                                       float C2, Img a, Img b, OutImg map,
+                                                       OutImg d_mu1, OutImg d_s11, OutImg d_s12,
+                                                       double* __restrict__ sums) {
+  __shared__ float s1[SS_H][SS_H];
+  __shared__ float s2[SS_H][SS_H];
+  __shared__ float h[5][SS_H][SS_T];
+  __shared__ float red[2][4];
+  const int bidx = blockIdx.z;
+  const int x0 = blockIdx.x * SS_T, y0 = blockIdx.y * SS_T;
+  const int tid = threadIdx.x;
+  const int ty = tid / SS_T, tx = tid % SS_T;
+  const int px = x0 + tx, py = y0 + ty;
+  const bool inside = px < W && py < H;
+  float l1_acc = 0.f, m_acc = 0.f;
+
+  for (int c = 0; c < CH; ++c) {
+    __syncthreads();
+    for (int e = tid; e < SS_H * SS_H; e += 256) {
+      const int r = e / SS_H, col = e % SS_H;
+      s1[r][col] = a.at(bidx, c, y0 + r - SS_R, x0 + col - SS_R, H, W);
+      s2[r][col] = b.at(bidx, c, y0 + r - SS_R, x0 + col - SS_R, H, W);
+    }
+    __syncthreads();
+    float f[5];
+    sep_conv<5>(h, [&](int r, int col, float v[5]) {
+      const float u = s1[r][col], w = s2[r][col];
+      v[0] = u;
+      v[1] = w;
+      v[2] = u * u;
+      v[3] = w * w;
+      v[4] = u * w;
+    }, f);
+    const float mu1 = f[0], mu2 = f[1];
+    const float sigma1_sq = f[2] - mu1 * mu1;
+    const float sigma2_sq = f[3] - mu2 * mu2;
+    const float sigma12 = f[4] - mu1 * mu2;
+    const float Cc = 2.f * mu1 * mu2 + C1;
+    const float D = 2.f * sigma12 + C2;
+    const float A = mu1 * mu1 + mu2 * mu2 + C1;
+    const float Bb = sigma1_sq + sigma2_sq + C2;
+    const float m = (Cc * D) / (A * Bb);
+    if (inside) {
+      if (map.p) map.at(bidx, c, py, px) = m;
+      if (d_mu1.p) {
+        d_mu1.at(bidx, c, py, px) = (mu2 * 2.f * D) / (A * Bb) - (mu2 * 2.f * Cc) / (A * Bb) -
+                                    (mu1 * 2.f * Cc * D) / (A * A * Bb) +
+                                    (mu1 * 2.f * Cc * D) / (A * Bb * Bb);
+        d_s11.at(bidx, c, py, px) = (-Cc * D) / (A * Bb * Bb);
+        d_s12.at(bidx, c, py, px) = (2.f * Cc) / (A * Bb);
+      }
+      if (sums) {
+        l1_acc += fabsf(s1[ty + SS_R][tx + SS_R] - s2[ty + SS_R][tx + SS_R]);
+        m_acc += m;
+      }
+    }
+  }
+  if (sums) {
+    const float l1 = tgs_wave_sum(l1_acc);
+    const float ms = tgs_wave_sum(m_acc);
+    const int lane = tid & 63, wave = tid >> 6;
+    if (lane == 0) {
+      red[0][wave] = l1;
+      red[1][wave] = ms;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      atomicAdd(&sums[0], (double)(red[0][0] + red[0][1] + red[0][2] + red[0][3]));
+      atomicAdd(&sums[1], (double)(red[1][0] + red[1][1] + red[1][2] + red[1][3]));
+    }
+  }
+}
+
+// dL/dimg1.  dmap == null means dL/dmap is the constant `dmap_const` (the
+// fused step's mean-SSIM loss).  When l1_weight != 0 the L1 term
+// l1_weight * sign(x - y) is added (sign(0) = 0, as torch's abs backward).
+__global__ void __launch_bounds__(256) ssim_bwd_kernel(int B, int CH, int H, int W, Img a, Img b,
+                                                       Img dmap, float dmap_const, Img d_mu1,
+                                                       Img d_s11, Img d_s12, float l1_weight,
+                                                       OutImg out) {
+  __shared__ float s[3][SS_H][SS_H];
+  __shared__ float h[3][SS_H][SS_T];
+  const int bidx = blockIdx.z;
+  const int x0 = blockIdx.x * SS_T, y0 = blockIdx.y * SS_T;
+  const int tid = threadIdx.x;
+  const int ty = tid / SS_T, tx = tid % SS_T;
+  const int px = x0 + tx, py = y0 + ty;
+  const bool inside = px < W && py < H;
+  for (int c = 0; c < CH; ++c) {
+    __syncthreads();
+    for (int e = tid; e < SS_H * SS_H; e += 256) {
+      const int r = e / SS_H, col = e % SS_H;
+      const int yy = y0 + r - SS_R, xx = x0 + col - SS_R;
+      const bool in_img = xx >= 0 && yy >= 0 && xx < W && yy < H;
+      const float g = dmap.p ? dmap.at(bidx, c, yy, xx, H, W) : (in_img ? dmap_const : 0.f);
+      s[0][r][col] = g * d_mu1.at(bidx, c, yy, xx, H, W);
+      s[1][r][col] = g * d_s11.at(bidx, c, yy, xx, H, W);
+      s[2][r][col] = g * d_s12.at(bidx, c, yy, xx, H, W);
+    }
+    __syncthreads();
+    float f[3];
+    sep_conv<3>(h, [&](int r, int col, float v[3]) {
+      v[0] = s[0][r][col];
+      v[1] = s[1][r][col];
+      v[2] = s[2][r][col];
+    }, f);
+    if (inside) {
+      const float x = a.at(bidx, c, py, px, H, W);
+      const float y = b.at(bidx, c, py, px, H, W);
+      float gr = f[0] + 2.f * x * f[1] + y * f[2];
+      if (l1_weight != 0.f) {
+        const float d = x - y;
+        gr += d > 0.f ? l1_weight : (d < 0.f ? -l1_weight : 0.f);
+      }
+      out.at(bidx, c, py, px) = gr;
+    }
+  }
+}
+
+static Img nchw(const float* p, int CH, int H, int W) {
+  return Img{p, (int64_t)CH * H * W, (int64_t)H * W, W, 1, 1.f, 0};
+}
+static OutImg nchw_out(float* p, int CH, int H, int W) {
+  return OutImg{p, (int64_t)CH * H * W, (int64_t)H * W, W, 1};
+}
+
+extern "C" int tgs_fused_ssim_fwd(int32_t B, int32_t CH, int32_t H, int32_t W, float C1, float C2,
+                                  const float* img1, const float* img2, float* ssim_map,
+                                  float* dm_dmu1, float* dm_dsigma1_sq, float* dm_dsigma12,
+                                  hipStream_t stream) {
+  if ((int64_t)B * CH * H * W == 0) return TGS_OK;
+  TGS_CHECK_ARG(img1 && img2 && ssim_map, "fused_ssim_fwd: null pointer");
+  TGS_CHECK_ARG((dm_dmu1 && dm_dsigma1_sq && dm_dsigma12) ||
+                    (!dm_dmu1 && !dm_dsigma1_sq && !dm_dsigma12),
+                "fused_ssim_fwd: partial maps must be all set or all null");
+  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, B);
+  hipLaunchKernelGGL(ssim_fwd_kernel, grid, dim3(256), 0, stream, B, CH, H, W, C1, C2,
+                     nchw(img1, CH, H, W), nchw(img2, CH, H, W), nchw_out(ssim_map, CH, H, W),
+                     nchw_out(dm_dmu1, CH, H, W), nchw_out(dm_dsigma1_sq, CH, H, W),
+                     nchw_out(dm_dsigma12, CH, H, W), (double*)nullptr);
+  TGS_RETURN_LAUNCH("tgs_fused_ssim_fwd");
+}
+
+extern "C" int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, float C1, float C2,
+                                  const float* img1, const float* img2, const float* dL_dmap,
+                                  const float* dm_dmu1, const float* dm_dsigma1_sq,
+                                  const float* dm_dsigma12, float* dL_dimg1, hipStream_t stream) {
+  (void)C1;
+  (void)C2;
+  if ((int64_t)B * CH * H * W == 0) return TGS_OK;
+  TGS_CHECK_ARG(img1 && img2 && dL_dmap && dm_dmu1 && dm_dsigma1_sq && dm_dsigma12 && dL_dimg1,
+                "fused_ssim_bwd: null pointer");
+  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, B);
+  hipLaunchKernelGGL(ssim_bwd_kernel, grid, dim3(256), 0, stream, B, CH, H, W,
+                     nchw(img1, CH, H, W), nchw(img2, CH, H, W), nchw(dL_dmap, CH, H, W), 0.f,
+                     nchw(dm_dmu1, CH, H, W), nchw(dm_dsigma1_sq, CH, H, W),
+                     nchw(dm_dsigma12, CH, H, W), 0.f, nchw_out(dL_dimg1, CH, H, W));
+  TGS_RETURN_LAUNCH("tgs_fused_ssim_bwd");
+}
+
+// Fused-step loss, L = (1-lambda) mean|I - gt'| + lambda (1 - mean SSIM(I, gt')),
+// gt' = clamp(gt / gt_div, 0, 1), with I the rendered [H,W,3] image (HWC) and
+// gt [3,H,W] (CHW).  Forward accumulates sums[0] += sum|I-gt'| and
+// sums[1] += sum SSIM into a double[2] the caller zeroes, and stores the three
+// partial maps ([3,H,W] each) for the backward.
+extern "C" int tgs_tide_loss_fwd(int32_t H, int32_t W, const float* image_hwc, const float* gt_chw,
+                                 float gt_div, float* dm_dmu1, float* dm_dsigma1_sq,
+                                 float* dm_dsigma12, double* sums, hipStream_t stream) {
+  if ((int64_t)H * W == 0) return TGS_OK;
+  TGS_CHECK_ARG(image_hwc && gt_chw && dm_dmu1 && dm_dsigma1_sq && dm_dsigma12 && sums,
+                "tide_loss_fwd: null pointer");
+  const int CH = 3;
+  Img a{image_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH, 1.f, 0};
+  Img b{gt_chw, (int64_t)CH * H * W, (int64_t)H * W, W, 1, gt_div, 1};
+  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, 1);
+  hipLaunchKernelGGL(ssim_fwd_kernel, grid, dim3(256), 0, stream, 1, CH, H, W, 1e-4f, 9e-4f, a, b,
+                     OutImg{nullptr, 0, 0, 0, 0}, nchw_out(dm_dmu1, CH, H, W),
+                     nchw_out(dm_dsigma1_sq, CH, H, W), nchw_out(dm_dsigma12, CH, H, W), sums);
+  TGS_RETURN_LAUNCH("tgs_tide_loss_fwd");
+}
+
+// dL/dI in HWC layout for the loss above.
+extern "C" int tgs_tide_loss_bwd(int32_t H, int32_t W, const float* image_hwc, const float* gt_chw,
+                                 float gt_div, float lambda_dssim, const float* dm_dmu1,
+                                 const float* dm_dsigma1_sq, const float* dm_dsigma12,
+                                 float* v_image_hwc, hipStream_t stream) {
+  if ((int64_t)H * W == 0) return TGS_OK;
+  TGS_CHECK_ARG(image_hwc && gt_chw && dm_dmu1 && dm_dsigma1_sq && dm_dsigma12 && v_image_hwc,
+                "tide_loss_bwd: null pointer");
+  const int CH = 3;
+  const float inv_n = 1.f / (float)((int64_t)CH * H * W);
+  Img a{image_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH, 1.f, 0};
+  Img b{gt_chw, (int64_t)CH * H * W, (int64_t)H * W, W, 1, gt_div, 1};
+  Img none{nullptr, 0, 0, 0, 0, 1.f, 0};
+  OutImg out{v_image_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH};
+  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, 1);
+  hipLaunchKernelGGL(ssim_bwd_kernel, grid, dim3(256), 0, stream, 1, CH, H, W, a, b, none,
+                     -lambda_dssim * inv_n, nchw(dm_dmu1, CH, H, W),
+                     nchw(dm_dsigma1_sq, CH, H, W), nchw(dm_dsigma12, CH, H, W),
+                     (1.f - lambda_dssim) * inv_n, out);
+  TGS_RETURN_LAUNCH("tgs_tide_loss_bwd");
+}

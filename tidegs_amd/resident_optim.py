@@ -1,0 +1,399 @@
+"""Resident-block Adam / Sophia for the TideGS working set (drop-in).
+
+``GPUResidentAdam`` mirrors ``strategies/tide_engine/gpu_resident_optimizer.py:73-513``:
+moments exist only for resident blocks, each resident block owns a state slot
+with its own step counter and bias correction (``:302-337``), eviction discards
+the slot and re-admission cold-starts it (``:219-264``), gradients are divided by
+the batch size, and ``step()`` returns the same stats dicts.  The host keeps
+that bookkeeping; the update of all 59 columns runs as ONE HIP launch
+(``tgs_resident_adam_step``) instead of six Triton launches, with the
+row -> slot mapping resolved on the GPU.
+
+Moments live in one ``[slots * block_size, 59]`` array per moment (row-contiguous),
+so a touched row's state is a single 236-byte span.
+
+``GPUResidentSophia`` uses the same slots with a diagonal-Hessian EMA instead of
+the second moment (Liu et al. 2023; no TideGS counterpart, see the kernel).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Any, Dict, List, Optional, Tuple
+
+import torch
+
+from . import _native as N
+
+
+class GPUResidentAdam:
+    """Adam with moments stored only for the current resident block set."""
+
+    COMPONENT_SPECS = (
+        ("xyz", "_xyz", 3, 0),
+        ("opacity", "_opacity", 1, 1),
+        ("scaling", "_scaling", 3, 2),
+        ("rotation", "_rotation", 4, 3),
+        ("features_dc", "_features_dc", 3, 4),
+        ("features_rest", "_features_rest", 45, 5),
+    )
+    TOTAL_WIDTH = sum(spec[2] for spec in COMPONENT_SPECS)
+    # Column offsets of each component inside the unified state rows.
+    _STATE_COLS = {}
+    _c = 0
+    for _name, _, _w, _ in COMPONENT_SPECS:
+        _STATE_COLS[_name] = _c
+        _c += _w
+    del _c, _name, _w
+
+    def __init__(self, batch_size: int = 1, block_size: int = 4096, capacity_blocks: int = 0,
+                 device: str = "cuda"):
+        self.batch_size = int(batch_size)
+        self.block_size = int(block_size)
+        self.capacity_blocks = max(0, int(capacity_blocks))
+        self.device = torch.device(device)
+        self.state_mode = "resident_blocks"
+
+        self._resident_blocks = set()
+        self._resident_streaks: Dict[int, int] = {}
+        self._completed_streak_total = 0
+        self._completed_streak_count = 0
+
+        self._allocated_slots = 0
+        self._block_to_slot: Dict[int, int] = {}
+        self._slot_to_block: List[Optional[int]] = []
+        self._free_slots: List[int] = []
+        self._slot_steps: List[int] = []
+        self._slot_initialized: List[bool] = []
+        self._slot_row_counts: List[int] = []
+        self._exp_avg: Optional[torch.Tensor] = None     # [slots*block, 59]
+        self._exp_avg_sq: Optional[torch.Tensor] = None  # [slots*block, 59]
+        self._bias_correction1: Optional[torch.Tensor] = None
+        self._denom_scale: Optional[torch.Tensor] = None
+        self._error_flag = torch.zeros(1, dtype=torch.int32, device=self.device)
+
+        self._logical_state_blocks = 0
+        self._logical_state_bytes = 0
+        self._stats = {
+            "state_mode": "resident_blocks",
+            "resident_target_blocks": 0,
+            "resident_state_blocks": 0,
+            "resident_state_bytes": 0,
+            "allocated_state_bytes": 0,
+            "cold_restarts": 0,
+            "state_evictions": 0,
+            "optimizer_rows_touched_total": 0,
+            "cold_restarted_rows_touched_total": 0,
+            "mean_resident_streak": 0.0,
+        }
+
+    # ---- bookkeeping (host) -------------------------------------------------
+    def _physical_state_bytes(self) -> int:
+        return int(self._allocated_slots * self.block_size * self.TOTAL_WIDTH * 2 * 4)
+
+    def _update_state_stats(self) -> None:
+        self._stats["resident_target_blocks"] = len(self._resident_blocks)
+        self._stats["resident_state_blocks"] = int(self._logical_state_blocks)
+        self._stats["resident_state_bytes"] = int(self._logical_state_bytes)
+        self._stats["allocated_state_bytes"] = self._physical_state_bytes()
+        streak_total = self._completed_streak_total + sum(self._resident_streaks.values())
+        streak_count = self._completed_streak_count + len(self._resident_streaks)
+        self._stats["mean_resident_streak"] = float(streak_total) / max(1, streak_count)
+
+    def _normalize_columns_lr(self, columns_lr) -> Dict[str, float]:
+        if columns_lr is None:
+            raise RuntimeError("[GPUResidentAdam] optimizer.columns_lr is required")
+        if torch.is_tensor(columns_lr):
+            cols = columns_lr.detach().to(device="cpu", dtype=torch.float32)
+        else:
+            cols = torch.tensor(columns_lr, dtype=torch.float32)
+        cols = cols.flatten().contiguous()
+        if cols.numel() == 6:
+            grouped = cols
+        elif cols.numel() == 59:
+            grouped = cols[torch.tensor([0, 3, 4, 7, 11, 14])]
+        else:
+            raise RuntimeError(
+                f"[GPUResidentAdam] Unexpected columns_lr width={cols.numel()}; "
+                "expected 6 grouped or 59 expanded entries"
+            )
+        return {name: float(grouped[g].item()) for name, _, _, g in self.COMPONENT_SPECS}
+
+    def _ensure_storage(self, required_slots: int) -> None:
+        if required_slots <= self._allocated_slots:
+            return
+        target = max(required_slots, self.capacity_blocks, max(1, self._allocated_slots * 2))
+        old_slots = self._allocated_slots
+        old_rows = old_slots * self.block_size
+        new_rows = target * self.block_size
+        avg = torch.empty((new_rows, self.TOTAL_WIDTH), dtype=torch.float32, device=self.device)
+        avg_sq = torch.empty_like(avg)
+        if old_rows:
+            avg[:old_rows].copy_(self._exp_avg)
+            avg_sq[:old_rows].copy_(self._exp_avg_sq)
+        bias = torch.empty((target,), dtype=torch.float32, device=self.device)
+        denom = torch.empty((target,), dtype=torch.float32, device=self.device)
+        if old_slots:
+            bias[:old_slots].copy_(self._bias_correction1)
+            denom[:old_slots].copy_(self._denom_scale)
+        self._exp_avg, self._exp_avg_sq = avg, avg_sq
+        self._bias_correction1, self._denom_scale = bias, denom
+        self._slot_to_block.extend([None] * (target - old_slots))
+        self._slot_steps.extend([0] * (target - old_slots))
+        self._slot_initialized.extend([False] * (target - old_slots))
+        self._slot_row_counts.extend([0] * (target - old_slots))
+        self._free_slots.extend(range(target - 1, old_slots - 1, -1))
+        self._allocated_slots = target
+
+    def _clear_slots(self, slots: List[int]) -> None:
+        row_words = self.block_size * self.TOTAL_WIDTH
+        s = N.stream_handle(self.device)
+        for slot in slots:
+            for buf in (self._exp_avg, self._exp_avg_sq):
+                N.call("tgs_fill_u32", buf.data_ptr() + slot * row_words * 4, row_words, 0, s)
+
+    def set_resident_blocks(self, block_ids: List[int]) -> None:
+        next_resident = {int(b) for b in block_ids}
+        previous = set(self._resident_blocks)
+        evicted = previous - next_resident
+        kept = previous & next_resident
+        incoming = next_resident - previous
+
+        for block_id in evicted:
+            streak = int(self._resident_streaks.pop(block_id, 0))
+            if streak > 0:
+                self._completed_streak_total += streak
+                self._completed_streak_count += 1
+            slot = self._block_to_slot.pop(block_id)
+            if self._slot_initialized[slot]:
+                self._stats["state_evictions"] += 1
+                self._logical_state_blocks -= 1
+                self._logical_state_bytes -= self._slot_row_counts[slot] * self.TOTAL_WIDTH * 2 * 4
+            self._slot_to_block[slot] = None
+            self._slot_steps[slot] = 0
+            self._slot_initialized[slot] = False
+            self._slot_row_counts[slot] = 0
+            self._free_slots.append(slot)
+
+        for block_id in kept:
+            self._resident_streaks[block_id] = self._resident_streaks.get(block_id, 0) + 1
+        for block_id in incoming:
+            self._resident_streaks[block_id] = 1
+
+        self._ensure_storage(len(next_resident))
+        incoming_slots: List[int] = []
+        for block_id in sorted(incoming):
+            if not self._free_slots:
+                self._ensure_storage(self._allocated_slots + 1)
+            slot = self._free_slots.pop()
+            self._block_to_slot[block_id] = slot
+            self._slot_to_block[slot] = block_id
+            self._slot_steps[slot] = 0
+            self._slot_initialized[slot] = False
+            self._slot_row_counts[slot] = 0
+            incoming_slots.append(slot)
+        self._clear_slots(incoming_slots)
+        self._resident_blocks = next_resident
+        self._update_state_stats()
+
+    def _layout(self, manager) -> List[Tuple[int, int, int, int]]:
+        layout = []
+        for block_id in manager.loaded_blocks:
+            block_id = int(block_id)
+            block_slice = manager.block_to_gpu_slice.get(block_id)
+            if block_slice is None:
+                continue
+            slot = self._block_to_slot.get(block_id)
+            if slot is None:
+                raise RuntimeError(
+                    f"[GPUResidentAdam] loaded block {block_id} has no resident state slot")
+            layout.append((int(block_slice.start), int(block_slice.stop), block_id, slot))
+        layout.sort(key=lambda item: item[0])
+        if not layout:
+            raise RuntimeError("[GPUResidentAdam] working set contains no resident blocks")
+        return layout
+
+    def _touched_blocks(self, layout, starts, ends, local_rows, index_is_i64):
+        counts = torch.empty(len(layout), dtype=torch.int64, device=self.device)
+        N.call("tgs_block_touch_counts", local_rows.numel(), N.ptr(local_rows), index_is_i64,
+               N.ptr(starts), N.ptr(ends), len(layout), N.ptr(counts), N.stream_handle(self.device))
+        counts_cpu = counts.cpu().tolist()
+        touched = [(layout[i][2], layout[i][3], int(c)) for i, c in enumerate(counts_cpu) if c > 0]
+        return touched
+
+    def _update_touched_slot_metadata(self, manager, touched, beta1: float, beta2: float) -> int:
+        cold_rows = 0
+        slots, bias_values, denom_values = [], [], []
+        for block_id, slot, count in touched:
+            if not self._slot_initialized[slot]:
+                self._slot_initialized[slot] = True
+                block_slice = manager.block_to_gpu_slice[block_id]
+                row_count = int(block_slice.stop - block_slice.start)
+                self._slot_row_counts[slot] = row_count
+                self._logical_state_blocks += 1
+                self._logical_state_bytes += row_count * self.TOTAL_WIDTH * 2 * 4
+                self._stats["cold_restarts"] += 1
+                self._stats["cold_restarted_rows_touched_total"] += int(count)
+                cold_rows += int(count)
+            self._slot_steps[slot] += 1
+            step = self._slot_steps[slot]
+            slots.append(slot)
+            bias_values.append(1.0 - beta1 ** step)
+            denom_values.append(math.sqrt(1.0 - beta2 ** step))
+        if slots:
+            idx = torch.tensor(slots, dtype=torch.long, device=self.device)
+            self._bias_correction1.index_copy_(
+                0, idx, torch.tensor(bias_values, dtype=torch.float32, device=self.device))
+            self._denom_scale.index_copy_(
+                0, idx, torch.tensor(denom_values, dtype=torch.float32, device=self.device))
+        return cold_rows
+
+    # ---- fused update --------------------------------------------------------
+    @staticmethod
+    def _row_view(t: torch.Tensor, width: int, name: str) -> Tuple[int, int]:
+        """(pointer, row stride) of a [rows, width] tensor with unit column stride."""
+        if t.dim() == 1 and width == 1:
+            if t.stride(0) != 1:
+                raise RuntimeError(f"[GPUResidentAdam] {name} must have unit stride")
+            return t.data_ptr(), 1
+        if t.dim() != 2 or t.shape[1] != width or (t.shape[0] > 1 and t.stride(1) != 1):
+            raise RuntimeError(
+                f"[GPUResidentAdam] {name} parameter and gradient must be contiguous "
+                f"[rows, {width}] rows (got shape {tuple(t.shape)}, stride {t.stride()})")
+        return t.data_ptr(), max(t.stride(0), width)
+
+    def _launch(self, kernel: str, n_rows, local_rows, index_is_i64, starts, ends, slots,
+                n_layout, param_views, grads, component_lrs, extra_args):
+        n = len(self.COMPONENT_SPECS)
+        params_p = (ctypes.c_void_p * n)()
+        grads_p = (ctypes.c_void_p * n)()
+        m_p = (ctypes.c_void_p * n)()
+        v_p = (ctypes.c_void_p * n)()
+        widths = (ctypes.c_int32 * n)()
+        strides = (ctypes.c_int64 * (3 * n))()
+        lrs = (ctypes.c_float * n)()
+        for k, (name, _, width, _) in enumerate(self.COMPONENT_SPECS):
+            pp, ps = self._row_view(param_views[name], width, name)
+            gp, gs = self._row_view(grads[name], width, name)
+            col = self._STATE_COLS[name]
+            params_p[k], grads_p[k] = pp, gp
+            m_p[k] = self._exp_avg.data_ptr() + 4 * col
+            v_p[k] = self._exp_avg_sq.data_ptr() + 4 * col
+            widths[k] = width
+            strides[3 * k + 0], strides[3 * k + 1], strides[3 * k + 2] = ps, gs, self.TOTAL_WIDTH
+            lrs[k] = component_lrs[name]
+        self._error_flag.zero_()
+        if kernel == "tgs_resident_adam_step":
+            args = (n_rows, N.ptr(local_rows), index_is_i64, N.ptr(starts), N.ptr(ends), N.ptr(slots),
+                    n_layout, self.block_size, N.ptr(self._bias_correction1),
+                    N.ptr(self._denom_scale), n, params_p, grads_p, m_p, v_p, widths, strides, lrs,
+                    *extra_args, N.ptr(self._error_flag), N.stream_handle(self.device))
+        else:
+            args = (n_rows, N.ptr(local_rows), index_is_i64, N.ptr(starts), N.ptr(ends), N.ptr(slots),
+                    n_layout, self.block_size, n, params_p, grads_p, m_p, v_p, widths, strides, lrs,
+                    *extra_args, N.ptr(self._error_flag), N.stream_handle(self.device))
+        N.call(kernel, *args)
+
+    def _prepare(self, iteration, gaussians, sparse_grad_local_ids, sparse_grad_components):
+        manager = getattr(gaussians, "gpu_working_set_manager", None)
+        if manager is None or manager.local_to_global_idx is None:
+            raise RuntimeError(
+                "[GPUResidentAdam] gpu_working_set_manager with local_to_global_idx is required")
+        local_rows = sparse_grad_local_ids.to(device=self.device)
+        if local_rows.dtype not in (torch.int64, torch.int32):
+            local_rows = local_rows.to(torch.int64)
+        local_rows = local_rows.contiguous()
+        index_is_i64 = 1 if local_rows.dtype == torch.int64 else 0
+        layout = self._layout(manager)
+        table = torch.tensor([[s, e, sl] for s, e, _, sl in layout], dtype=torch.int64)
+        table = table.t().contiguous().to(self.device)
+        starts, ends, slots = table[0], table[1], table[2]
+        for name, _, _, _ in self.COMPONENT_SPECS:
+            if name not in sparse_grad_components:
+                raise KeyError(
+                    f"[GPUResidentAdam] Missing sparse_grad_components[{name!r}] at iter={iteration}")
+        return manager, local_rows, index_is_i64, layout, starts, ends, slots
+
+    def _check_error(self):
+        if int(self._error_flag.item()) != 0:
+            raise RuntimeError(
+                "[GPUResidentAdam] a touched row lies outside every resident block of the layout")
+
+    def step(self, iteration: int, gaussians, sparse_grad_local_ids: torch.Tensor,
+             sparse_grad_components: Dict[str, torch.Tensor]) -> Dict[str, Any]:
+        empty = {"updated_blocks": 0, "updated_block_ids": [], "touched_rows": 0, "cold_rows": 0}
+        if sparse_grad_local_ids is None or sparse_grad_components is None:
+            return empty
+        if sparse_grad_local_ids.numel() == 0:
+            return empty
+        manager, local_rows, idx64, layout, starts, ends, slots = self._prepare(
+            iteration, gaussians, sparse_grad_local_ids, sparse_grad_components)
+        touched = self._touched_blocks(layout, starts, ends, local_rows, idx64)
+        component_lrs = self._normalize_columns_lr(getattr(gaussians.optimizer, "columns_lr", None))
+        beta1, beta2 = gaussians.optimizer.param_groups[0]["betas"]
+        beta1, beta2 = float(beta1), float(beta2)
+        eps = float(gaussians.optimizer.param_groups[0]["eps"])
+        cold_rows = self._update_touched_slot_metadata(manager, touched, beta1, beta2)
+        param_views = {name: getattr(gaussians, attr).data for name, attr, _, _ in self.COMPONENT_SPECS}
+        self._launch("tgs_resident_adam_step", local_rows.numel(), local_rows, idx64, starts, ends,
+                     slots, len(layout), param_views, sparse_grad_components, component_lrs,
+                     (beta1, beta2, eps, float(self.batch_size)))
+        self._check_error()
+        touched_rows = int(local_rows.numel())
+        self._stats["optimizer_rows_touched_total"] += touched_rows
+        self._update_state_stats()
+        return {
+            "updated_blocks": len(touched),
+            "updated_block_ids": [b for b, _, _ in touched],
+            "touched_rows": touched_rows,
+            "cold_rows": int(cold_rows),
+        }
+
+    def get_stats(self) -> Dict[str, Any]:
+        self._update_state_stats()
+        return dict(self._stats)
+
+
+class GPUResidentSophia(GPUResidentAdam):
+    """Sophia-style update on the same resident slots (second moment -> Hessian EMA).
+
+    ``m = b1 m + (1-b1) g``; every ``hessian_interval`` iterations
+    ``h = b2 h + (1-b2) g*g``; ``p -= lr * clamp(m / max(h, eps), -rho, rho)``.
+    ``g`` is the gradient divided by the batch size, as in GPUResidentAdam.
+    """
+
+    def __init__(self, batch_size: int = 1, block_size: int = 4096, capacity_blocks: int = 0,
+                 device: str = "cuda", rho: float = 0.04, hessian_interval: int = 1):
+        super().__init__(batch_size, block_size, capacity_blocks, device)
+        self.rho = float(rho)
+        self.hessian_interval = max(1, int(hessian_interval))
+
+    def step(self, iteration: int, gaussians, sparse_grad_local_ids: torch.Tensor,
+             sparse_grad_components: Dict[str, torch.Tensor]) -> Dict[str, Any]:
+        empty = {"updated_blocks": 0, "updated_block_ids": [], "touched_rows": 0, "cold_rows": 0}
+        if sparse_grad_local_ids is None or sparse_grad_components is None:
+            return empty
+        if sparse_grad_local_ids.numel() == 0:
+            return empty
+        manager, local_rows, idx64, layout, starts, ends, slots = self._prepare(
+            iteration, gaussians, sparse_grad_local_ids, sparse_grad_components)
+        touched = self._touched_blocks(layout, starts, ends, local_rows, idx64)
+        component_lrs = self._normalize_columns_lr(getattr(gaussians.optimizer, "columns_lr", None))
+        beta1, beta2 = gaussians.optimizer.param_groups[0]["betas"]
+        eps = float(gaussians.optimizer.param_groups[0]["eps"])
+        cold_rows = self._update_touched_slot_metadata(manager, touched, float(beta1), float(beta2))
+        update_h = 1 if (int(iteration) % self.hessian_interval) == 0 else 0
+        param_views = {name: getattr(gaussians, attr).data for name, attr, _, _ in self.COMPONENT_SPECS}
+        self._launch("tgs_resident_sophia_step", local_rows.numel(), local_rows, idx64, starts, ends,
+                     slots, len(layout), param_views, sparse_grad_components, component_lrs,
+                     (float(beta1), float(beta2), eps, self.rho, float(self.batch_size), update_h))
+        self._check_error()
+        touched_rows = int(local_rows.numel())
+        self._stats["optimizer_rows_touched_total"] += touched_rows
+        self._update_state_stats()
+        return {
+            "updated_blocks": len(touched),
+            "updated_block_ids": [b for b, _, _ in touched],
+            "touched_rows": touched_rows,
+            "cold_rows": int(cold_rows),
+        }

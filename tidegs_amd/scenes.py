@@ -1,0 +1,168 @@
+"""Seeded synthetic scenes for the benchmark configurations.
+
+The resident table is ``[N, 59]`` fp32 in TideGS's CACHE column order
+(``storage/block_reader.py:35-44``, ``double_buffer_gpu.py:726-734``):
+``xyz | log-scale | quat (w,x,y,z) | opacity logit | SH dc (3) | SH rest (45)``,
+SH coefficient k / channel c at column ``11 + 3k + c``.
+
+Cameras follow the OpenCV/Inria convention used by TideGS (x right, y down,
+z forward; ``viewmat`` = world-to-camera, row-major).  Ground-truth images are
+``[3, H, W]`` on a 0..255 scale, as ``camera.original_image`` is consumed by
+``strategies/base_engine.py:476``.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+ROW = 59
+COL_XYZ = slice(0, 3)
+COL_SCALE = slice(3, 6)
+COL_ROT = slice(6, 10)
+COL_OPAC = slice(10, 11)
+COL_SH = slice(11, 59)
+COL_DC = slice(11, 14)
+COL_REST = slice(14, 59)
+
+
+@dataclass
+class Scene:
+    params: torch.Tensor     # [N, 59] CACHE layout
+    viewmats: torch.Tensor   # [C, 4, 4] world-to-camera, row-major
+    Ks: torch.Tensor         # [C, 3, 3]
+    width: int
+    height: int
+    gt: torch.Tensor         # [C, 3, H, W], 0..255
+    name: str = ""
+
+    @property
+    def n(self) -> int:
+        return self.params.shape[0]
+
+    @property
+    def n_cams(self) -> int:
+        return self.viewmats.shape[0]
+
+    def to(self, device) -> "Scene":
+        return Scene(self.params.to(device), self.viewmats.to(device), self.Ks.to(device),
+                     self.width, self.height, self.gt.to(device), self.name)
+
+    def camtoworlds(self) -> torch.Tensor:
+        return torch.linalg.inv(self.viewmats.double()).float()
+
+
+def _gaussian_rows(g: torch.Generator, n: int, means: torch.Tensor, log_scale_mu: float,
+                   log_scale_sigma: float) -> torch.Tensor:
+    p = torch.empty((n, ROW), dtype=torch.float32)
+    p[:, COL_XYZ] = means
+    p[:, COL_SCALE] = torch.randn((n, 3), generator=g) * log_scale_sigma + log_scale_mu
+    q = torch.randn((n, 4), generator=g)
+    p[:, COL_ROT] = q / q.norm(dim=1, keepdim=True)
+    p[:, COL_OPAC] = torch.randn((n, 1), generator=g)
+    p[:, COL_SH] = torch.randn((n, 48), generator=g) * 0.2
+    return p
+
+
+def look_at(eye, target, up=(0.0, 0.0, 1.0)) -> torch.Tensor:
+    """World-to-camera [4,4] (OpenCV: z forward, y down) looking from eye at target."""
+    eye = torch.tensor(eye, dtype=torch.float64)
+    target = torch.tensor(target, dtype=torch.float64)
+    up = torch.tensor(up, dtype=torch.float64)
+    f = target - eye
+    f = f / f.norm()
+    r = torch.linalg.cross(f, up)
+    if r.norm() < 1e-8:
+        r = torch.linalg.cross(f, torch.tensor([0.0, 1.0, 0.0], dtype=torch.float64))
+    r = r / r.norm()
+    d = torch.linalg.cross(f, r)  # camera y (down)
+    R = torch.stack([r, d, f], 0)
+    w2c = torch.eye(4, dtype=torch.float64)
+    w2c[:3, :3] = R
+    w2c[:3, 3] = -R @ eye
+    return w2c.float()
+
+
+def _intrinsics(f: float, W: int, H: int) -> torch.Tensor:
+    return torch.tensor([[f, 0.0, W / 2.0], [0.0, f, H / 2.0], [0.0, 0.0, 1.0]])
+
+
+def cfg1(seed: int = 0, n: int = 10_000) -> Scene:
+    """10k Gaussians, one 256x256 pinhole (fx=fy=256) at the origin looking +z."""
+    g = torch.Generator().manual_seed(seed)
+    xy = torch.rand((n, 2), generator=g) * 2 - 1
+    z = torch.rand((n, 1), generator=g) * 4 + 2
+    p = _gaussian_rows(g, n, torch.cat([xy, z], 1), -4.5, 0.5)
+    W = H = 256
+    gt = torch.rand((1, 3, H, W), generator=g) * 255.0
+    return Scene(p, torch.eye(4)[None], _intrinsics(256.0, W, H)[None], W, H, gt, "cfg1")
+
+
+def cfg2(seed: int = 0, n: int = 1_000_000) -> Scene:
+    """1M Gaussians in x,y in [-10,10], depth 5..40, one 1920x1080 camera (f=1100)."""
+    g = torch.Generator().manual_seed(seed)
+    xy = torch.rand((n, 2), generator=g) * 20 - 10
+    z = torch.rand((n, 1), generator=g) * 35 + 5
+    p = _gaussian_rows(g, n, torch.cat([xy, z], 1), -4.5, 0.5)
+    W, H = 1920, 1080
+    gt = torch.rand((1, 3, H, W), generator=g) * 255.0
+    return Scene(p, torch.eye(4)[None], _intrinsics(1100.0, W, H)[None], W, H, gt, "cfg2")
+
+
+def orbit_cameras(n_cams: int, center=(0.0, 0.0, 10.0), radius: float = 70.0,
+                  height: float = 35.0, arc_deg: float = 90.0):
+    """Poses on a smooth arc around `center`, all looking at it."""
+    mats = []
+    for i in range(n_cams):
+        a = math.radians(-arc_deg / 2 + arc_deg * (i / max(1, n_cams - 1)))
+        eye = (center[0] + radius * math.cos(a), center[1] + radius * math.sin(a),
+               center[2] + height)
+        mats.append(look_at(eye, center))
+    return torch.stack(mats, 0)
+
+
+def cfg3(seed: int = 0, n: int = 4_000_000, n_cams: int = 16, width: int = 1920,
+         height: int = 1080, with_gt: bool = True) -> Scene:
+    """4M Gaussians in a 100x100x20 box (log-scales N(-3.5, 0.7)), 16 cameras on an
+    orbit arc, 1920x1080, f=1100: the north-star training-step configuration."""
+    g = torch.Generator().manual_seed(seed)
+    xy = torch.rand((n, 2), generator=g) * 100 - 50
+    z = torch.rand((n, 1), generator=g) * 20
+    p = _gaussian_rows(g, n, torch.cat([xy, z], 1), -3.5, 0.7)
+    vm = orbit_cameras(n_cams)
+    Ks = _intrinsics(1100.0, width, height)[None].repeat(n_cams, 1, 1)
+    gt = (torch.rand((n_cams, 3, height, width), generator=g) * 255.0 if with_gt
+          else torch.empty((n_cams, 3, height, width)))
+    return Scene(p, vm, Ks, width, height, gt, "cfg3")
+
+
+def small(seed: int = 0, n: int = 2000, n_cams: int = 2, W: int = 96, H: int = 64,
+          log_scale_mu: float = -2.5) -> Scene:
+    """Small multi-camera scene for parity tests (oracle finishes in seconds)."""
+    g = torch.Generator().manual_seed(seed)
+    xy = torch.rand((n, 2), generator=g) * 4 - 2
+    z = torch.rand((n, 1), generator=g) * 4 + 3
+    p = _gaussian_rows(g, n, torch.cat([xy, z], 1), log_scale_mu, 0.5)
+    mats = []
+    for i in range(n_cams):
+        eye = (0.3 * i, -0.2 * i, 0.0)
+        mats.append(look_at(eye, (0.0, 0.0, 5.0), up=(0.0, -1.0, 0.0)))
+    vm = torch.stack(mats, 0)
+    Ks = _intrinsics(0.9 * W, W, H)[None].repeat(n_cams, 1, 1)
+    gt = torch.rand((n_cams, 3, H, W), generator=g) * 255.0
+    return Scene(p, vm, Ks, W, H, gt, "small")
+
+
+def activations(params: torch.Tensor):
+    """Split a CACHE-layout table into TideGS's activated inputs
+    (base_gaussian_model.py:35-50): means, quats (normalised), scales (exp),
+    opacities (sigmoid), SH coefficients [N,16,3]."""
+    means = params[:, COL_XYZ]
+    q = params[:, COL_ROT]
+    quats = torch.nn.functional.normalize(q, dim=-1)
+    scales = torch.exp(params[:, COL_SCALE])
+    opac = torch.sigmoid(params[:, COL_OPAC]).squeeze(1)
+    sh = params[:, COL_SH].reshape(-1, 16, 3)
+    return means, quats, scales, opac, sh
