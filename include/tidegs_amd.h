@@ -152,17 +152,18 @@ int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, float C1, fl
                        const float* img1, const float* img2, const float* dL_dmap,
                        const float* dm_dmu1, const float* dm_dsigma1_sq, const float* dm_dsigma12,
                        float* dL_dimg1, tgs_stream_t stream);
-/* Fused L1 + SSIM training loss of strategies/base_engine.py:464-488 on the
- * rendered HWC image: sums[0] += sum|I - gt'|, sums[1] += sum SSIM (double[2],
- * caller-zeroed), gt' = clamp(gt_chw / gt_div, 0, 1); partial maps [3,H,W]. */
-int tgs_tide_loss_fwd(int32_t H, int32_t W, const float* image_hwc, const float* gt_chw,
-                      float gt_div, float* dm_dmu1, float* dm_dsigma1_sq, float* dm_dsigma12,
-                      double* sums, tgs_stream_t stream);
-/* dL/dI (HWC) of L = (1-lambda) mean|I-gt'| + lambda (1 - mean SSIM). */
-int tgs_tide_loss_bwd(int32_t H, int32_t W, const float* image_hwc, const float* gt_chw,
-                      float gt_div, float lambda_dssim, const float* dm_dmu1,
-                      const float* dm_dsigma1_sq, const float* dm_dsigma12, float* v_image_hwc,
-                      tgs_stream_t stream);
+/* Fused L1 + SSIM training loss of strategies/base_engine.py:464-488 for B
+ * rendered images [B,H,W,3] (HWC) against gt [B,3,H,W]:
+ * sums[2b] += sum|I_b - gt'_b|, sums[2b+1] += sum SSIM (double[2B],
+ * caller-zeroed), gt' = clamp(gt / gt_div, 0, 1); partial maps [B,3,H,W]. */
+int tgs_tide_loss_fwd(int32_t B, int32_t H, int32_t W, const float* images_hwc,
+                      const float* gt_chw, float gt_div, float* dm_dmu1, float* dm_dsigma1_sq,
+                      float* dm_dsigma12, double* sums, tgs_stream_t stream);
+/* dL_b/dI_b (HWC) of L_b = (1-lambda) mean|I_b-gt'_b| + lambda (1 - mean SSIM_b). */
+int tgs_tide_loss_bwd(int32_t B, int32_t H, int32_t W, const float* images_hwc,
+                      const float* gt_chw, float gt_div, float lambda_dssim,
+                      const float* dm_dmu1, const float* dm_dsigma1_sq,
+                      const float* dm_dsigma12, float* v_images_hwc, tgs_stream_t stream);
 
 /* ---- resident optimizer ------------------------------------------------ */
 /* Replaces the six _fused_resident_adam_kernel launches of GPUResidentAdam.step
@@ -202,6 +203,64 @@ int tgs_resident_sophia_step(int64_t n_rows, const void* local_rows, int index_i
 int tgs_block_touch_counts(int64_t n_rows, const void* rows, int index_is_i64,
                            const int64_t* block_starts, const int64_t* block_ends,
                            int64_t n_layout, int64_t* counts, tgs_stream_t stream);
+
+/* ---- fused resident step (one launch per stage for a batch of cameras) ---- */
+/* These replace TideGS's per-camera loop (strategies/tide_engine/engine.py:
+ * 1435-1827 filters + touched rows, 1874-2695 per-camera render/backward,
+ * 2434-2469 scatter_add) over a resident [N,59] fp32 table in CACHE column
+ * order (storage/block_reader.py:35-44).  Cameras per batch: 1..32. */
+/* Row blocks of the visibility/compaction passes for n_rows rows. */
+uint32_t tgs_tide_row_blocks(uint64_t n_rows);
+/* Packed-projection visibility (gsplat fully_fused_projection_packed_fwd.cu:
+ * 50-131) of every row in every camera: masks [N] (bit c = camera c), and
+ * per-block counts [(C+2)*nb] (per camera, touched rows, visits). */
+int tgs_tide_visibility(uint64_t n_rows, const float* params, uint32_t C, const float* viewmats,
+                        const float* Ks, const float* campos, int32_t W, int32_t H, float eps2d,
+                        float near_plane, float far_plane, float radius_clip, uint32_t* masks,
+                        uint32_t* counts, tgs_stream_t stream);
+/* Compaction from offs = exclusive scan of counts: entries (concatenated
+ * per-camera filters, ascending rows, base_engine.py:388-425), touched rows,
+ * visit lists per touched row (entries in camera order), totals [C+3]
+ * (V_c..., T, sum V, visits) and cam_offsets [C+1]. Buffers sized C*N / N. */
+int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* masks, const uint32_t* counts,
+                     const uint32_t* offs, int32_t* entries, int32_t* touched,
+                     int32_t* visit_base, int32_t* visits, uint32_t* totals,
+                     int32_t* cam_offsets, tgs_stream_t stream);
+/* Projection + SH colour + activations per entry (engine.py:458-512 with
+ * base_gaussian_model.py:35-50) -> splats [V,12] (3 x float4:
+ * {x,y,opacity,depth},{a,b,c,radius},{r,g,b,0}) and tile counts [V]. */
+int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries, const int32_t* cam_offsets,
+                         uint32_t C, const float* params, const float* viewmats, const float* Ks,
+                         const float* campos, int32_t W, int32_t H, float eps2d, float near_plane,
+                         float far_plane, float radius_clip, int32_t sh_degree,
+                         uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
+                         float* splats, int32_t* tiles_per_entry, tgs_stream_t stream);
+/* Batched isect emission (isect_tiles.cu:73-98 with camera ids). */
+int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,
+                        const float* splats, const int64_t* cum_tiles, uint32_t tile_size,
+                        uint32_t tile_width, uint32_t tile_height, uint32_t tile_n_bits,
+                        int64_t* isect_ids, int32_t* flatten_ids, tgs_stream_t stream);
+/* Rasterize forward/backward over packed splats (tile 16, 3 channels);
+ * images / v_images [C,H,W,3], alphas [C,H,W], last_ids [C,H,W];
+ * splat_grads [V,9] accumulated (zero first): {mean2d 2, conic 3, color 3, opacity}. */
+int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const float* backgrounds, uint32_t W,
+                           uint32_t H, uint32_t tile_width, uint32_t tile_height,
+                           const int32_t* tile_offsets, const int32_t* flatten_ids,
+                           uint32_t n_isects, float* images, float* alphas, int32_t* last_ids,
+                           tgs_stream_t stream);
+int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const float* backgrounds, uint32_t W,
+                           uint32_t H, uint32_t tile_width, uint32_t tile_height,
+                           const int32_t* tile_offsets, const int32_t* flatten_ids,
+                           uint32_t n_isects, const float* alphas, const int32_t* last_ids,
+                           const float* v_images, float* splat_grads, tgs_stream_t stream);
+/* Per touched row: projection + SH + activation backward over its visits in
+ * camera order; writes the compact gradient row grads[t, 0:59] once. */
+int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched, const int32_t* visit_base,
+                         const int32_t* visits, const int32_t* cam_offsets, uint32_t C,
+                         const float* params, const float* viewmats, const float* Ks,
+                         const float* campos, int32_t W, int32_t H, float eps2d,
+                         int32_t sh_degree, const float* splats, const float* splat_grads,
+                         float* grads, tgs_stream_t stream);
 
 #ifdef __cplusplus
 }

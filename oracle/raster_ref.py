@@ -83,18 +83,19 @@ def isect_tiles(means2d, radii, depths, tile_size, tw, th, sort=True, camera_ids
     tile_bits = bit_width(n_tiles)
     cam_bits = bit_width(C if camera_ids is None else max(C, 1))
     total = int(tiles.astype(np.int64).sum())
-    isect_ids = np.empty(total, dtype=np.int64)
-    flatten_ids = np.empty(total, dtype=np.int32)
     depth_bits = flat_d.view(np.int32).astype(np.int64)  # sign-extended, as the reference
-    cur = 0
-    for idx in np.nonzero(tiles)[0]:
-        ys = np.arange(y0[idx], y1[idx])
-        xs = np.arange(x0[idx], x1[idx])
-        tid = (ys[:, None] * tw + xs[None, :]).reshape(-1)
-        k = tid.size
-        isect_ids[cur:cur + k] = (cams[idx] << (32 + tile_bits)) | (tid << 32) | depth_bits[idx]
-        flatten_ids[cur:cur + k] = idx
-        cur += k
+    # Emission in entry order, row-major over each entry's tile rectangle.
+    live_idx = np.nonzero(tiles)[0]
+    cnt = tiles[live_idx].astype(np.int64)
+    owner = np.repeat(live_idx, cnt)
+    start = np.repeat(np.cumsum(cnt) - cnt, cnt)
+    local = np.arange(total, dtype=np.int64) - start
+    width = nx[owner].astype(np.int64)
+    ty_ = y0[owner] + local // np.maximum(width, 1)
+    tx_ = x0[owner] + local % np.maximum(width, 1)
+    tid = ty_ * tw + tx_
+    isect_ids = (cams[owner] << (32 + tile_bits)) | (tid << 32) | depth_bits[owner]
+    flatten_ids = owner.astype(np.int32)
     if sort and total:
         end_bit = 32 + tile_bits + cam_bits
         mask = np.int64(-1) if end_bit >= 64 else np.int64((1 << end_bit) - 1)

@@ -1,0 +1,134 @@
+"""CPU restatement of one TideGS training batch on a resident table.
+
+Test oracle and CPU baseline only (see ``oracle/__init__.py``).  Follows the
+reference's per-camera loop literally:
+
+* filters: packed projection per camera, ascending Gaussian ids
+  (``strategies/base_engine.py:329-425`` over
+  ``gsplat/cuda/csrc/fully_fused_projection_packed_fwd.cu:19-131``)
+* touched rows: union of the filters (``engine.py:1801-1827``)
+* per camera (``engine.py:2255-2311`` -> ``pipeline_forward_one_step_shs_inplace``
+  ``engine.py:458-571``): activations (``base_gaussian_model.py:35-50``),
+  non-packed projection, SH colours ``clamp_min(sh + 0.5, 0)``, isect + sort,
+  rasterize, loss ``0.8 L1 + 0.2 (1 - SSIM)`` (``base_engine.py:464-488``),
+  then the backward of all of it and ``scatter_add_`` into the compact rows
+  in camera order (``engine.py:2434-2469``).
+* optional resident Adam of the touched rows (``oracle/optim_ref.py``).
+
+Every piece is a function of the other oracle modules, each pinned in
+tests/test_oracle_*.py; this module only composes them.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import gsplat_ref as G
+from . import raster_ref as R
+from . import ssim_ref as S
+
+
+def _split(params: torch.Tensor):
+    xyz = params[:, 0:3]
+    logs = params[:, 3:6]
+    q = params[:, 6:10]
+    logit = params[:, 10]
+    sh = params[:, 11:59].reshape(-1, 16, 3)
+    return xyz, logs, q, logit, sh
+
+
+def packed_filters(params, viewmats, Ks, W, H, eps2d=0.3, near=0.01, far=1e10, radius_clip=0.0,
+                   dtype=torch.float64):
+    """Per-camera ascending row ids visible under the packed-projection rule."""
+    xyz, logs, q, _, _ = _split(params.to(dtype))
+    qn = q / torch.clamp(q.norm(dim=-1, keepdim=True), min=1e-12)
+    Sigma = G.covar_from_quat_scale(qn, torch.exp(logs))
+    pc, m2d, a, b, d, det, conics, comp = G.project_core(xyz, Sigma, viewmats.to(dtype),
+                                                         Ks.to(dtype), W, H, eps2d)
+    z = pc[..., 2]
+    ok = (z >= near) & (z <= far) & (det > 0)
+    bb = 0.5 * (a + d)
+    s = torch.sqrt(torch.clamp(bb * bb - det, min=0.1))
+    radius = torch.ceil(3.0 * torch.sqrt(torch.maximum(bb + s, bb - s)))
+    ok &= ~(radius <= radius_clip)
+    mx, my = m2d[..., 0], m2d[..., 1]
+    ok &= ~((mx + radius <= 0) | (mx - radius >= W) | (my + radius <= 0) | (my - radius >= H))
+    ok &= torch.isfinite(radius)
+    return [torch.nonzero(ok[c]).flatten() for c in range(ok.shape[0])]
+
+
+def camera_step(params, rows, viewmat, K, gt, W, H, sh_degree=3, background=None, tile=16,
+                lambda_dssim=0.2, proj_dtype=torch.float64, raster_dtype=np.float32):
+    """Forward + backward of one camera on the gathered rows.
+
+    Returns (loss, image [H,W,3], grads [len(rows), 59]) with grads in the
+    table's column order (w.r.t. the raw parameters, through the activations).
+    """
+    p = params[rows].to(proj_dtype)
+    xyz, logs, q, logit, sh = _split(p)
+    qnorm = torch.clamp(q.norm(dim=-1, keepdim=True), min=1e-12)
+    qn = q / qnorm
+    scales = torch.exp(logs)
+    opac = torch.sigmoid(logit)
+    vm, Kc = viewmat[None].to(proj_dtype), K[None].to(proj_dtype)
+    radii, m2d, depths, conics, _ = G.project_fwd(xyz, qn, scales, vm, Kc, W, H,
+                                                  dtype=proj_dtype)
+    campos = torch.linalg.inv(viewmat.to(torch.float64))[:3, 3].to(proj_dtype)
+    dirs = xyz - campos
+    col_pre = G.sh_fwd(sh_degree, dirs, sh, dtype=proj_dtype)
+    colors = torch.clamp(col_pre + 0.5, min=0.0)
+    tw, th = -(-W // tile), -(-H // tile)
+    m2d32 = m2d.to(torch.float32).numpy()
+    _, ids, flat = R.isect_tiles(m2d32, radii.numpy(), depths.to(torch.float32).numpy(), tile, tw,
+                                 th)
+    offs = R.isect_offset_encode(ids, 1, tw, th)
+    bg = None if background is None else np.asarray(background, np.float64)[None]
+    m2d64 = m2d.numpy().reshape(-1, 2)
+    img, alphas, last = R.rasterize_fwd(m2d64, conics[0].numpy(),
+                                        colors.numpy(), opac.numpy(), W, H, tile, offs, flat,
+                                        backgrounds=bg, dtype=raster_dtype)
+    loss, v_img = S.tide_loss(img[0].transpose(2, 0, 1), gt.numpy(), lambda_dssim=lambda_dssim,
+                              dtype=np.float64)
+    v_hwc = np.ascontiguousarray(v_img.transpose(1, 2, 0))[None]
+    vm2, vcon, vcol, vop, _ = R.rasterize_bwd(m2d64, conics[0].numpy(),
+                                              colors.numpy(), opac.numpy(), W, H, tile, offs,
+                                              flat, alphas, last, v_hwc, backgrounds=bg,
+                                              dtype=raster_dtype)
+    vm2 = torch.from_numpy(vm2).to(proj_dtype)
+    vcon = torch.from_numpy(vcon).to(proj_dtype)
+    vcol = torch.from_numpy(vcol).to(proj_dtype) * (col_pre + 0.5 >= 0)
+    vop = torch.from_numpy(vop).to(proj_dtype)
+    v_sh, v_dirs = G.sh_bwd(sh_degree, dirs, sh, vcol, dtype=proj_dtype)
+    v_xyz, v_qn, v_s, _, _ = G.project_bwd(xyz, qn, scales, vm, Kc, W, H, 0.3, radii,
+                                           conics, vm2[None], None, vcon[None], dtype=proj_dtype)
+    v_xyz = v_xyz + v_dirs
+    g = torch.zeros((len(rows), 59), dtype=proj_dtype)
+    g[:, 0:3] = v_xyz
+    g[:, 3:6] = v_s * scales
+    g[:, 6:10] = (v_qn - (v_qn * qn).sum(-1, keepdim=True) * qn) / qnorm
+    g[:, 10] = vop * opac * (1 - opac)
+    g[:, 11:59] = v_sh.reshape(-1, 48)
+    return loss, img[0], g
+
+
+def batch_grads(params, viewmats, Ks, gts, W, H, sh_degree=3, backgrounds=None,
+                proj_dtype=torch.float64, raster_dtype=np.float32):
+    """touched rows [T], compact grads [T,59], per-camera losses and images."""
+    filters = packed_filters(params, viewmats, Ks, W, H)
+    touched = torch.unique(torch.cat(filters)) if filters else torch.empty(0, dtype=torch.long)
+    grads = torch.zeros((touched.numel(), 59), dtype=proj_dtype)
+    losses, images = [], []
+    for c, rows in enumerate(filters):
+        if rows.numel() == 0:
+            losses.append(None)
+            images.append(None)
+            continue
+        bg = None if backgrounds is None else backgrounds[c]
+        loss, img, g = camera_step(params, rows, viewmats[c], Ks[c], gts[c], W, H, sh_degree,
+                                   background=bg, proj_dtype=proj_dtype,
+                                   raster_dtype=raster_dtype)
+        idx = torch.searchsorted(touched, rows)
+        grads.index_add_(0, idx, g)
+        losses.append(loss)
+        images.append(img)
+    return touched, grads, losses, images, filters

@@ -280,10 +280,10 @@ def test_tide_loss_kernels(gpu):
     parts = [torch.empty((3, H, W), device=gpu) for _ in range(3)]
     sums = torch.zeros(2, dtype=torch.float64, device=gpu)
     s = N.stream_handle()
-    N.call("tgs_tide_loss_fwd", H, W, N.ptr(d_img), N.ptr(d_gt), 255.0, *[N.ptr(p) for p in parts],
+    N.call("tgs_tide_loss_fwd", 1, H, W, N.ptr(d_img), N.ptr(d_gt), 255.0, *[N.ptr(p) for p in parts],
            N.ptr(sums), s)
     v = torch.empty((H, W, 3), device=gpu)
-    N.call("tgs_tide_loss_bwd", H, W, N.ptr(d_img), N.ptr(d_gt), 255.0, 0.2,
+    N.call("tgs_tide_loss_bwd", 1, H, W, N.ptr(d_img), N.ptr(d_gt), 255.0, 0.2,
            *[N.ptr(p) for p in parts], N.ptr(v), s)
     loss_ref, grad_ref = S.tide_loss(img.permute(2, 0, 1).numpy(), gt.numpy())
     n = 3 * H * W

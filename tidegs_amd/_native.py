@@ -69,8 +69,22 @@ SIGNATURES = {
     "tgs_fused_ssim_bwd": (
         ctypes.c_int, [I32, I32, I32, I32, F32, F32, P, P, P, P, P, P, P, P]
     ),
-    "tgs_tide_loss_fwd": (ctypes.c_int, [I32, I32, P, P, F32, P, P, P, P, P]),
-    "tgs_tide_loss_bwd": (ctypes.c_int, [I32, I32, P, P, F32, F32, P, P, P, P, P]),
+    "tgs_tide_loss_fwd": (ctypes.c_int, [I32, I32, I32, P, P, F32, P, P, P, P, P]),
+    "tgs_tide_loss_bwd": (ctypes.c_int, [I32, I32, I32, P, P, F32, F32, P, P, P, P, P]),
+    "tgs_tide_row_blocks": (U32, [U64]),
+    "tgs_tide_visibility": (
+        ctypes.c_int, [U64, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, P, P, P]),
+    "tgs_tide_compact": (ctypes.c_int, [U64, U32, P, P, P, P, P, P, P, P, P, P]),
+    "tgs_tide_project_fwd": (
+        ctypes.c_int,
+        [U32, P, P, U32, P, P, P, P, I32, I32, F32, F32, F32, F32, I32, U32, U32, U32, P, P, P]),
+    "tgs_tide_isect_emit": (ctypes.c_int, [U32, P, U32, P, P, U32, U32, U32, U32, P, P, P]),
+    "tgs_tide_rasterize_fwd": (ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P]),
+    "tgs_tide_rasterize_bwd": (
+        ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, P]),
+    "tgs_tide_project_bwd": (
+        ctypes.c_int,
+        [U32, P, P, P, P, U32, P, P, P, P, I32, I32, F32, I32, P, P, P, P]),
     "tgs_resident_adam_step": (
         ctypes.c_int,
         [I64, P, ctypes.c_int, P, P, P, I64, I64, P, P, ctypes.c_int, P, P, P, P, P, P, P,

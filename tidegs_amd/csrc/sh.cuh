@@ -114,9 +114,11 @@ __device__ __forceinline__ void sh_eval3(int degree, float dx, float dy, float d
   out[2] = b;
 }
 
-// VJP of sh_eval3.  Writes v_coeffs[k*3+c] for k < (degree+1)^2 (entries above
-// the degree are left to the caller, who zero-fills them) and returns v_dir
-// (the gradient w.r.t. the un-normalised direction) when want_dir is set.
+// VJP of sh_eval3.  Writes (ACCUM: adds to) v_coeffs[k*3+c] for
+// k < (degree+1)^2 (entries above the degree are left to the caller) and
+// returns v_dir (the gradient w.r.t. the un-normalised direction) when
+// want_dir is set.
+template <bool ACCUM = false>
 __device__ __forceinline__ void sh_vjp3(int degree, float dx, float dy, float dz,
                                         const float* __restrict__ coeffs, const float v_col[3],
                                         float* __restrict__ v_coeffs, bool want_dir,
@@ -130,9 +132,15 @@ __device__ __forceinline__ void sh_vjp3(int degree, float dx, float dy, float dz
   }
   float gx = 0.f, gy = 0.f, gz = 0.f;
   sh_foreach(degree, x, y, z, [&](int k, float Y, float Yx, float Yy, float Yz) {
-    v_coeffs[k * 3 + 0] = Y * v_col[0];
-    v_coeffs[k * 3 + 1] = Y * v_col[1];
-    v_coeffs[k * 3 + 2] = Y * v_col[2];
+    if (ACCUM) {
+      v_coeffs[k * 3 + 0] += Y * v_col[0];
+      v_coeffs[k * 3 + 1] += Y * v_col[1];
+      v_coeffs[k * 3 + 2] += Y * v_col[2];
+    } else {
+      v_coeffs[k * 3 + 0] = Y * v_col[0];
+      v_coeffs[k * 3 + 1] = Y * v_col[1];
+      v_coeffs[k * 3 + 2] = Y * v_col[2];
+    }
     if (want_dir && k > 0) {
       const float s = coeffs[k * 3 + 0] * v_col[0] + coeffs[k * 3 + 1] * v_col[1] +
                       coeffs[k * 3 + 2] * v_col[2];

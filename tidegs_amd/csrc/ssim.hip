@@ -149,8 +149,8 @@ __global__ void __launch_bounds__(256) ssim_fwd_kernel(int B, int CH, int H, int
     }
     __syncthreads();
     if (tid == 0) {
-      atomicAdd(&sums[0], (double)(red[0][0] + red[0][1] + red[0][2] + red[0][3]));
-      atomicAdd(&sums[1], (double)(red[1][0] + red[1][1] + red[1][2] + red[1][3]));
+      atomicAdd(&sums[2 * bidx + 0], (double)(red[0][0] + red[0][1] + red[0][2] + red[0][3]));
+      atomicAdd(&sums[2 * bidx + 1], (double)(red[1][0] + red[1][1] + red[1][2] + red[1][3]));
     }
   }
 }
@@ -242,43 +242,46 @@ extern "C" int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, f
   TGS_RETURN_LAUNCH("tgs_fused_ssim_bwd");
 }
 
-// Fused-step loss, L = (1-lambda) mean|I - gt'| + lambda (1 - mean SSIM(I, gt')),
-// gt' = clamp(gt / gt_div, 0, 1), with I the rendered [H,W,3] image (HWC) and
-// gt [3,H,W] (CHW).  Forward accumulates sums[0] += sum|I-gt'| and
-// sums[1] += sum SSIM into a double[2] the caller zeroes, and stores the three
-// partial maps ([3,H,W] each) for the backward.
-extern "C" int tgs_tide_loss_fwd(int32_t H, int32_t W, const float* image_hwc, const float* gt_chw,
-                                 float gt_div, float* dm_dmu1, float* dm_dsigma1_sq,
-                                 float* dm_dsigma12, double* sums, hipStream_t stream) {
-  if ((int64_t)H * W == 0) return TGS_OK;
-  TGS_CHECK_ARG(image_hwc && gt_chw && dm_dmu1 && dm_dsigma1_sq && dm_dsigma12 && sums,
+// Fused-step loss of strategies/base_engine.py:464-488 for a batch of B
+// rendered images: per image b, L_b = (1-lambda) mean|I_b - gt'_b| +
+// lambda (1 - mean SSIM(I_b, gt'_b)), gt' = clamp(gt / gt_div, 0, 1), with
+// I [B,H,W,3] (HWC, as rendered) and gt [B,3,H,W] (CHW).  Forward adds
+// sum|I-gt'| and sum SSIM of image b into sums[2b], sums[2b+1] (double,
+// caller-zeroed) and stores the three partial maps ([B,3,H,W] each).
+extern "C" int tgs_tide_loss_fwd(int32_t B, int32_t H, int32_t W, const float* images_hwc,
+                                 const float* gt_chw, float gt_div, float* dm_dmu1,
+                                 float* dm_dsigma1_sq, float* dm_dsigma12, double* sums,
+                                 hipStream_t stream) {
+  if ((int64_t)B * H * W == 0) return TGS_OK;
+  TGS_CHECK_ARG(images_hwc && gt_chw && dm_dmu1 && dm_dsigma1_sq && dm_dsigma12 && sums,
                 "tide_loss_fwd: null pointer");
   const int CH = 3;
-  Img a{image_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH, 1.f, 0};
+  Img a{images_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH, 1.f, 0};
   Img b{gt_chw, (int64_t)CH * H * W, (int64_t)H * W, W, 1, gt_div, 1};
-  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, 1);
-  hipLaunchKernelGGL(ssim_fwd_kernel, grid, dim3(256), 0, stream, 1, CH, H, W, 1e-4f, 9e-4f, a, b,
+  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, B);
+  hipLaunchKernelGGL(ssim_fwd_kernel, grid, dim3(256), 0, stream, B, CH, H, W, 1e-4f, 9e-4f, a, b,
                      OutImg{nullptr, 0, 0, 0, 0}, nchw_out(dm_dmu1, CH, H, W),
                      nchw_out(dm_dsigma1_sq, CH, H, W), nchw_out(dm_dsigma12, CH, H, W), sums);
   TGS_RETURN_LAUNCH("tgs_tide_loss_fwd");
 }
 
-// dL/dI in HWC layout for the loss above.
-extern "C" int tgs_tide_loss_bwd(int32_t H, int32_t W, const float* image_hwc, const float* gt_chw,
-                                 float gt_div, float lambda_dssim, const float* dm_dmu1,
-                                 const float* dm_dsigma1_sq, const float* dm_dsigma12,
-                                 float* v_image_hwc, hipStream_t stream) {
-  if ((int64_t)H * W == 0) return TGS_OK;
-  TGS_CHECK_ARG(image_hwc && gt_chw && dm_dmu1 && dm_dsigma1_sq && dm_dsigma12 && v_image_hwc,
+// dL_b/dI_b (HWC) for the loss above, for every image of the batch.
+extern "C" int tgs_tide_loss_bwd(int32_t B, int32_t H, int32_t W, const float* images_hwc,
+                                 const float* gt_chw, float gt_div, float lambda_dssim,
+                                 const float* dm_dmu1, const float* dm_dsigma1_sq,
+                                 const float* dm_dsigma12, float* v_images_hwc,
+                                 hipStream_t stream) {
+  if ((int64_t)B * H * W == 0) return TGS_OK;
+  TGS_CHECK_ARG(images_hwc && gt_chw && dm_dmu1 && dm_dsigma1_sq && dm_dsigma12 && v_images_hwc,
                 "tide_loss_bwd: null pointer");
   const int CH = 3;
   const float inv_n = 1.f / (float)((int64_t)CH * H * W);
-  Img a{image_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH, 1.f, 0};
+  Img a{images_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH, 1.f, 0};
   Img b{gt_chw, (int64_t)CH * H * W, (int64_t)H * W, W, 1, gt_div, 1};
   Img none{nullptr, 0, 0, 0, 0, 1.f, 0};
-  OutImg out{v_image_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH};
-  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, 1);
-  hipLaunchKernelGGL(ssim_bwd_kernel, grid, dim3(256), 0, stream, 1, CH, H, W, a, b, none,
+  OutImg out{v_images_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH};
+  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, B);
+  hipLaunchKernelGGL(ssim_bwd_kernel, grid, dim3(256), 0, stream, B, CH, H, W, a, b, none,
                      -lambda_dssim * inv_n, nchw(dm_dmu1, CH, H, W),
                      nchw(dm_dsigma1_sq, CH, H, W), nchw(dm_dsigma12, CH, H, W),
                      (1.f - lambda_dssim) * inv_n, out);

@@ -1,0 +1,580 @@
+// Fused per-batch TideGS step over the resident [N,59] Gaussian table.
+//
+// What TideGS does per batch (strategies/tide_engine/engine.py:1435-2737):
+//   filters  = packed projection per camera (base_engine.py:222-461,
+//              gsplat fully_fused_projection_packed_fwd.cu:19-183)
+//   touched  = union of the filters (engine.py:1801-1827)
+//   per camera: gather rows + activations (engine.py:2255-2268), projection,
+//              SH colors, isect + sort, rasterize, loss, backward, scatter_add
+//              of the row gradients into the compact [T, .] buffers
+//              (engine.py:2434-2469)
+//   resident Adam over the touched rows (runtime.py:1741-1791)
+// Here the same computation is reorganised for one GPU launch per stage over
+// the whole batch:
+//   tide_visibility  one pass over rows: per-camera visibility bits with the
+//                    packed-projection rule, per-block counts
+//   tide_compact     per-camera visible lists ("entries", ascending rows as the
+//                    reference filters), the touched-row list and, per touched
+//                    row, the list of its entries in camera order ("visits")
+//   tide_project_fwd projection + SH colour + activations for every entry,
+//                    written as one 48-byte splat record
+//   tide_isect_emit  batched keys camera|tile|depth for one sort of the batch
+//   (rasterize fwd / bwd with the packed splat policy, see raster.cuh)
+//   tide_project_bwd one thread per touched row walks its visits in camera
+//                    order, accumulates the projection/SH/activation VJPs and
+//                    writes the row's 59 gradients once (no atomics and no
+//                    read-modify-write of the compact gradient).
+// Resident table columns (TideGS CACHE order, storage/block_reader.py:35-44):
+//   xyz 0..2 | log-scale 3..5 | quat 6..9 (w,x,y,z) | opacity logit 10 | SH 11..58
+// with SH coefficient k, channel c at column 11 + 3k + c.
+#include "projection.cuh"
+#include "raster.cuh"
+#include "sh.cuh"
+
+#define TIDE_ROW 59
+#define TIDE_MAX_CAMS 32
+#define VIS_THREADS 256
+
+struct TideCams {
+  const float* viewmats;  // [C,16]
+  const float* Ks;        // [C,9]
+  const float* campos;    // [C,3] camera centres in world space
+  uint32_t C;
+};
+
+struct CamLDS {
+  Cam cam[TIDE_MAX_CAMS];
+  float campos[TIDE_MAX_CAMS][3];
+};
+
+__device__ __forceinline__ void load_cams_lds(const TideCams& tc, CamLDS& s) {
+  for (uint32_t c = threadIdx.x; c < tc.C; c += blockDim.x) {
+    s.cam[c] = load_cam(tc.viewmats + c * 16, tc.Ks + c * 9);
+    s.campos[c][0] = tc.campos[c * 3 + 0];
+    s.campos[c][1] = tc.campos[c * 3 + 1];
+    s.campos[c][2] = tc.campos[c * 3 + 2];
+  }
+  __syncthreads();
+}
+
+// torch.nn.functional.normalize: q / max(|q|, 1e-12)
+__device__ __forceinline__ void normalize4(const float* q, float out[4], float& inv_norm) {
+  const float n = sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+  const float d = fmaxf(n, 1e-12f);
+  inv_norm = 1.f / d;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) out[k] = q[k] / d;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
+// Packed-projection visibility (fully_fused_projection_packed_fwd.cu:50-131):
+// same culls as the render projection but radius = ceil(3 sqrt(max(v1, v2)))
+// with the 0.1 floor.
+__device__ __forceinline__ bool packed_visible(const float p[3], const m3& Sigma, const Cam& cam,
+                                               int W, int H, float eps2d, float near_plane,
+                                               float far_plane, float radius_clip) {
+  float pc[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    pc[i] = cam.R[i][0] * p[0] + cam.R[i][1] * p[1] + cam.R[i][2] * p[2] + cam.t[i];
+  if (pc[2] < near_plane || pc[2] > far_plane) return false;
+  m3 Rc;
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) Rc.m[i][j] = cam.R[i][j];
+  const m3 Sc = m3_mul_bt(m3_mul(Rc, Sigma), Rc);
+  const float x = pc[0], y = pc[1], z = pc[2];
+  const float lim_x = 1.3f * (0.5f * (float)W / cam.fx);
+  const float lim_y = 1.3f * (0.5f * (float)H / cam.fy);
+  const float rz = 1.f / z, rz2 = rz * rz;
+  const float tx = z * fminf(lim_x, fmaxf(-lim_x, x * rz));
+  const float ty = z * fminf(lim_y, fmaxf(-lim_y, y * rz));
+  const float J00 = cam.fx * rz, J02 = -cam.fx * tx * rz2;
+  const float J11 = cam.fy * rz, J12 = -cam.fy * ty * rz2;
+  float JS0[3], JS1[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    JS0[k] = J00 * Sc.m[0][k] + J02 * Sc.m[2][k];
+    JS1[k] = J11 * Sc.m[1][k] + J12 * Sc.m[2][k];
+  }
+  const float a = JS0[0] * J00 + JS0[2] * J02 + eps2d;
+  const float b = JS0[1] * J11 + JS0[2] * J12;
+  const float d = JS1[1] * J11 + JS1[2] * J12 + eps2d;
+  const float det = a * d - b * b;
+  if (det <= 0.f) return false;
+  const float bb = 0.5f * (a + d);
+  const float s = sqrtf(fmaxf(0.1f, bb * bb - det));
+  const float radius = ceilf(3.f * sqrtf(fmaxf(bb + s, bb - s)));
+  if (radius <= radius_clip) return false;
+  const float mx = cam.fx * x * rz + cam.cx;
+  const float my = cam.fy * y * rz + cam.cy;
+  if (mx + radius <= 0.f || mx - radius >= (float)W || my + radius <= 0.f ||
+      my - radius >= (float)H)
+    return false;
+  return true;
+}
+
+__device__ __forceinline__ m3 row_covariance(const float* __restrict__ row) {
+  const float s[3] = {expf(row[3]), expf(row[4]), expf(row[5])};
+  float qn[4], inv;
+  normalize4(row + 6, qn, inv);
+  return covar_from_quat_scale(qn, s);
+}
+
+// ---------------------------------------------------------------------------
+// Visibility + per-block counts.  counts layout (uint32, block-minor):
+//   [c * nb + b]        visible rows of camera c in block b   (c < C)
+//   [C * nb + b]        touched rows in block b
+//   [(C+1) * nb + b]    visits (sum of popcount(mask)) in block b
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(VIS_THREADS) tide_visibility_kernel(
+    uint64_t n_rows, const float* __restrict__ params, TideCams tc, int W, int H, float eps2d,
+    float near_plane, float far_plane, float radius_clip, uint32_t* __restrict__ masks,
+    uint32_t* __restrict__ counts) {
+  __shared__ CamLDS s_cam;
+  __shared__ uint32_t s_cnt[TIDE_MAX_CAMS + 2];
+  load_cams_lds(tc, s_cam);
+  if (threadIdx.x < TIDE_MAX_CAMS + 2) s_cnt[threadIdx.x] = 0;
+  __syncthreads();
+  const uint64_t n = (uint64_t)blockIdx.x * VIS_THREADS + threadIdx.x;
+  const uint32_t nb = gridDim.x;
+  uint32_t mask = 0;
+  if (n < n_rows) {
+    const float* row = params + n * TIDE_ROW;
+    const float p[3] = {row[0], row[1], row[2]};
+    const m3 Sigma = row_covariance(row);
+    for (uint32_t c = 0; c < tc.C; ++c)
+      if (packed_visible(p, Sigma, s_cam.cam[c], W, H, eps2d, near_plane, far_plane, radius_clip))
+        mask |= 1u << c;
+    masks[n] = mask;
+  }
+  const int lane = threadIdx.x & 63;
+  for (uint32_t c = 0; c < tc.C; ++c) {
+    const uint32_t cnt = (uint32_t)__popcll(tgs_ballot((mask >> c) & 1u));
+    if (lane == 0 && cnt) atomicAdd(&s_cnt[c], cnt);
+  }
+  const uint32_t tcnt = (uint32_t)__popcll(tgs_ballot(mask != 0));
+  if (lane == 0 && tcnt) atomicAdd(&s_cnt[tc.C], tcnt);
+  atomicAdd(&s_cnt[tc.C + 1], (uint32_t)__popc(mask));
+  __syncthreads();
+  if (threadIdx.x < tc.C + 2) counts[(uint64_t)threadIdx.x * nb + blockIdx.x] = s_cnt[threadIdx.x];
+}
+
+// offs = exclusive scan of counts (same layout).  Writes:
+//   entries[base_c + rank] = row          (camera lists, concatenated, ascending rows)
+//   touched[t] = row, visit_base[t] = first visit of row t (visit_base[T] = total)
+//   visits[visit_base[t] + j] = entry of the j-th camera (ascending) seeing row t
+//   totals[0..C-1] = V_c, totals[C] = T, totals[C+1] = sum_c V_c
+__global__ void __launch_bounds__(VIS_THREADS) tide_compact_kernel(
+    uint64_t n_rows, uint32_t C, const uint32_t* __restrict__ masks,
+    const uint32_t* __restrict__ offs, int32_t* __restrict__ entries,
+    int32_t* __restrict__ touched, int32_t* __restrict__ visit_base,
+    int32_t* __restrict__ visits, uint32_t* __restrict__ totals) {
+  __shared__ uint32_t s_wave[VIS_THREADS / 64][TIDE_MAX_CAMS + 2];
+  const uint32_t nb = gridDim.x;
+  const uint64_t n = (uint64_t)blockIdx.x * VIS_THREADS + threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const uint32_t mask = n < n_rows ? masks[n] : 0u;
+  const uint32_t total_entries = offs[(uint64_t)C * nb];  // sum of V_c
+  const uint32_t total_touched = offs[(uint64_t)(C + 1) * nb] - total_entries;
+
+  // per-wave ranks and counts: cameras, touched, visits
+  uint32_t rank[TIDE_MAX_CAMS];
+#pragma unroll
+  for (uint32_t c = 0; c < TIDE_MAX_CAMS; ++c) {
+    if (c < C) {
+      const uint64_t b = tgs_ballot((mask >> c) & 1u);
+      rank[c] = (uint32_t)__popcll(b & lt);
+      if (lane == 0) s_wave[wave][c] = (uint32_t)__popcll(b);
+    }
+  }
+  const uint64_t tb = tgs_ballot(mask != 0);
+  const uint32_t trank = (uint32_t)__popcll(tb & lt);
+  if (lane == 0) s_wave[wave][C] = (uint32_t)__popcll(tb);
+  // inclusive wave scan of popcount(mask)
+  const uint32_t pc = (uint32_t)__popc(mask);
+  uint32_t inc = pc;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += o;
+  }
+  if (lane == 63) s_wave[wave][C + 1] = inc;
+  __syncthreads();
+  if (n >= n_rows || mask == 0) return;
+
+  auto wave_prefix = [&](uint32_t k) {
+    uint32_t s = 0;
+    for (int w = 0; w < wave; ++w) s += s_wave[w][k];
+    return s;
+  };
+  const uint32_t t = offs[(uint64_t)C * nb + blockIdx.x] - total_entries + wave_prefix(C) + trank;
+  const uint32_t vbase = offs[(uint64_t)(C + 1) * nb + blockIdx.x] - total_entries -
+                         total_touched + wave_prefix(C + 1) + (inc - pc);
+  touched[t] = (int32_t)n;
+  visit_base[t] = (int32_t)vbase;
+  uint32_t j = 0;
+  for (uint32_t c = 0; c < C; ++c) {
+    if ((mask >> c) & 1u) {
+      const uint32_t e = offs[(uint64_t)c * nb + blockIdx.x] + wave_prefix(c) + rank[c];
+      entries[e] = (int32_t)n;
+      visits[vbase + j] = (int32_t)e;
+      ++j;
+    }
+  }
+  (void)totals;
+}
+
+__global__ void tide_totals_kernel(uint32_t C, uint32_t nb, const uint32_t* __restrict__ counts,
+                                   const uint32_t* __restrict__ offs,
+                                   uint32_t* __restrict__ totals,
+                                   int32_t* __restrict__ cam_offsets,
+                                   int32_t* __restrict__ visit_base) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const uint64_t last = (uint64_t)(C + 2) * nb - 1;
+  const uint32_t grand = offs[last] + counts[last];
+  const uint32_t ents = offs[(uint64_t)C * nb];
+  const uint32_t tch = offs[(uint64_t)(C + 1) * nb] - ents;
+  for (uint32_t c = 0; c < C; ++c) {
+    const uint32_t lo = offs[(uint64_t)c * nb];
+    const uint32_t hi = offs[(uint64_t)(c + 1) * nb];
+    totals[c] = hi - lo;
+    cam_offsets[c] = (int32_t)lo;
+  }
+  cam_offsets[C] = (int32_t)ents;
+  totals[C] = tch;
+  totals[C + 1] = ents;
+  totals[C + 2] = grand - ents - tch;  // visits (== ents)
+  visit_base[tch] = (int32_t)ents;
+}
+
+// ---------------------------------------------------------------------------
+// Forward projection + SH for every entry -> packed splat records.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t entry_camera(const int32_t* s_off, uint32_t C, uint32_t e) {
+  uint32_t c = 0;
+  while (c + 1 < C && (uint32_t)s_off[c + 1] <= e) ++c;
+  return c;
+}
+
+__global__ void __launch_bounds__(256) tide_project_fwd_kernel(
+    uint32_t n_entries, const int32_t* __restrict__ entries, const int32_t* __restrict__ cam_offsets,
+    TideCams tc, const float* __restrict__ params, int W, int H, float eps2d, float near_plane,
+    float far_plane, float radius_clip, int sh_degree, uint32_t tile_size, uint32_t tw,
+    uint32_t th, float4* __restrict__ splats, int32_t* __restrict__ tiles_per_entry) {
+  __shared__ CamLDS s_cam;
+  __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
+  load_cams_lds(tc, s_cam);
+  if (threadIdx.x <= tc.C) s_off[threadIdx.x] = cam_offsets[threadIdx.x];
+  __syncthreads();
+  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n_entries) return;
+  const uint32_t c = entry_camera(s_off, tc.C, e);
+  const float* row = params + (uint64_t)entries[e] * TIDE_ROW;
+  const float p[3] = {row[0], row[1], row[2]};
+  const m3 Sigma = row_covariance(row);
+  const ProjResult r = project_forward(p, Sigma, s_cam.cam[c], W, H, eps2d, near_plane,
+                                       far_plane, radius_clip);
+  float4* out = splats + (uint64_t)e * 3;
+  if (r.radius <= 0) {
+    out[0] = make_float4(0.f, 0.f, 0.f, 0.f);
+    out[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    out[2] = make_float4(0.f, 0.f, 0.f, 0.f);
+    tiles_per_entry[e] = 0;
+    return;
+  }
+  float col[3];
+  sh_eval3(sh_degree, p[0] - s_cam.campos[c][0], p[1] - s_cam.campos[c][1],
+           p[2] - s_cam.campos[c][2], row + 11, col);
+  const float opac = sigmoidf_(row[10]);
+  out[0] = make_float4(r.mean2d[0], r.mean2d[1], opac, r.depth);
+  out[1] = make_float4(r.conic[0], r.conic[1], r.conic[2], (float)r.radius);
+  out[2] = make_float4(fmaxf(col[0] + 0.5f, 0.f), fmaxf(col[1] + 0.5f, 0.f),
+                       fmaxf(col[2] + 0.5f, 0.f), 0.f);
+  // tile count (isect_tiles.cu:55-70)
+  const float ts = (float)tile_size;
+  const float trd = (float)r.radius / ts;
+  const float txx = r.mean2d[0] / ts, tyy = r.mean2d[1] / ts;
+  auto clampu = [](float v, uint32_t lim) -> uint32_t {
+    if (!(v > 0.f)) return 0u;
+    if (v >= (float)lim) return lim;
+    return (uint32_t)v;
+  };
+  const uint32_t x0 = clampu(floorf(txx - trd), tw), x1 = clampu(ceilf(txx + trd), tw);
+  const uint32_t y0 = clampu(floorf(tyy - trd), th), y1 = clampu(ceilf(tyy + trd), th);
+  tiles_per_entry[e] = (int32_t)((x1 > x0 ? x1 - x0 : 0u) * (y1 > y0 ? y1 - y0 : 0u));
+}
+
+__global__ void __launch_bounds__(256) tide_isect_emit_kernel(
+    uint32_t n_entries, const int32_t* __restrict__ cam_offsets, uint32_t C,
+    const float4* __restrict__ splats, const int64_t* __restrict__ cum_tiles, uint32_t tile_size,
+    uint32_t tw, uint32_t th, uint32_t tile_n_bits, int64_t* __restrict__ isect_ids,
+    int32_t* __restrict__ flatten_ids) {
+  __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
+  if (threadIdx.x <= C) s_off[threadIdx.x] = cam_offsets[threadIdx.x];
+  __syncthreads();
+  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n_entries) return;
+  const float4 r0 = splats[(uint64_t)e * 3 + 0];
+  const float4 r1 = splats[(uint64_t)e * 3 + 1];
+  const int32_t radius = (int32_t)r1.w;
+  if (radius <= 0) return;
+  const uint32_t c = entry_camera(s_off, C, e);
+  const float ts = (float)tile_size;
+  const float trd = (float)radius / ts;
+  const float txx = r0.x / ts, tyy = r0.y / ts;
+  auto clampu = [](float v, uint32_t lim) -> uint32_t {
+    if (!(v > 0.f)) return 0u;
+    if (v >= (float)lim) return lim;
+    return (uint32_t)v;
+  };
+  const uint32_t x0 = clampu(floorf(txx - trd), tw), x1 = clampu(ceilf(txx + trd), tw);
+  const uint32_t y0 = clampu(floorf(tyy - trd), th), y1 = clampu(ceilf(tyy + trd), th);
+  const int64_t cam_enc = (int64_t)c << (32 + tile_n_bits);
+  const int64_t depth_enc = (int64_t)__float_as_int(r0.w);
+  int64_t cur = e == 0 ? 0 : cum_tiles[e - 1];
+  for (uint32_t y = y0; y < y1; ++y)
+    for (uint32_t x = x0; x < x1; ++x) {
+      isect_ids[cur] = cam_enc | (((int64_t)y * tw + x) << 32) | depth_enc;
+      flatten_ids[cur] = (int32_t)e;
+      ++cur;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: one thread per touched row.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) tide_project_bwd_kernel(
+    uint32_t n_touched, const int32_t* __restrict__ touched,
+    const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
+    const int32_t* __restrict__ cam_offsets, TideCams tc, const float* __restrict__ params,
+    int W, int H, float eps2d, int sh_degree, const float4* __restrict__ splats,
+    const float* __restrict__ splat_grads, float* __restrict__ grads) {
+  __shared__ CamLDS s_cam;
+  __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
+  load_cams_lds(tc, s_cam);
+  if (threadIdx.x <= tc.C) s_off[threadIdx.x] = cam_offsets[threadIdx.x];
+  __syncthreads();
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_touched) return;
+  const float* row = params + (uint64_t)touched[t] * TIDE_ROW;
+  const float p[3] = {row[0], row[1], row[2]};
+  const float s[3] = {expf(row[3]), expf(row[4]), expf(row[5])};
+  float qn[4], qinv;
+  normalize4(row + 6, qn, qinv);
+  const m3 Sigma = covar_from_quat_scale(qn, s);
+  const float opac = sigmoidf_(row[10]);
+  float sh[48];
+#pragma unroll
+  for (int k = 0; k < 48; ++k) sh[k] = row[11 + k];
+
+  float v_sh[48];
+#pragma unroll
+  for (int k = 0; k < 48; ++k) v_sh[k] = 0.f;
+  float v_p[3] = {0.f, 0.f, 0.f};
+  m3 v_S;
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) v_S.m[i][j] = 0.f;
+  float v_op = 0.f;
+
+  const int32_t v0 = visit_base[t], v1 = visit_base[t + 1];
+  for (int32_t v = v0; v < v1; ++v) {
+    const uint32_t e = (uint32_t)visits[v];
+    const float4 r1 = splats[(uint64_t)e * 3 + 1];
+    if (r1.w <= 0.f) continue;  // culled by the render projection: zero gradient
+    const uint32_t c = entry_camera(s_off, tc.C, e);
+    const float* g = splat_grads + (uint64_t)e * 9;
+    const float vm[2] = {g[0], g[1]};
+    const float vc[3] = {g[2], g[3], g[4]};
+    float vcol[3] = {g[5], g[6], g[7]};
+    v_op += g[8];
+    // colour = clamp_min(SH + 0.5, 0): gradient passes where SH + 0.5 >= 0
+    const float dx = p[0] - s_cam.campos[c][0], dy = p[1] - s_cam.campos[c][1],
+                dz = p[2] - s_cam.campos[c][2];
+    float col[3];
+    sh_eval3(sh_degree, dx, dy, dz, sh, col);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) vcol[k] = (col[k] + 0.5f >= 0.f) ? vcol[k] : 0.f;
+    float vdir[3];
+    sh_vjp3<true>(sh_degree, dx, dy, dz, sh, vcol, v_sh, true, vdir);
+    const float conic[3] = {r1.x, r1.y, r1.z};
+    ProjGrad pg;
+    project_backward(p, Sigma, s_cam.cam[c], W, H, eps2d, conic, 0.f, vm, 0.f, vc, false, 0.f,
+                     false, pg);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) v_p[k] += pg.v_p[k] + vdir[k];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) v_S.m[i][j] += pg.v_Sigma.m[i][j];
+  }
+  // Sigma(q_n, s) -> (v_qn, v_s); then the activation VJPs:
+  // exp: v_logscale = v_s * s; normalize: v_q = (v_qn - (v_qn.qn) qn) / max(|q|, eps);
+  // sigmoid: v_logit = v_op * o * (1 - o).
+  float vq[4], vs[3];
+  covar_vjp_quat_scale(qn, s, v_S, vq, vs);
+  const float dot = vq[0] * qn[0] + vq[1] * qn[1] + vq[2] * qn[2] + vq[3] * qn[3];
+  float* out = grads + (uint64_t)t * TIDE_ROW;
+  out[0] = v_p[0];
+  out[1] = v_p[1];
+  out[2] = v_p[2];
+  out[3] = vs[0] * s[0];
+  out[4] = vs[1] * s[1];
+  out[5] = vs[2] * s[2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) out[6 + k] = (vq[k] - dot * qn[k]) * qinv;
+  out[10] = v_op * (1.f - opac) * opac;
+#pragma unroll
+  for (int k = 0; k < 48; ++k) out[11 + k] = v_sh[k];
+}
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+static int check_cams(uint32_t C) {
+  TGS_CHECK_ARG(C >= 1 && C <= TIDE_MAX_CAMS, "tide step: 1..%d cameras per batch (got %u)",
+                TIDE_MAX_CAMS, C);
+  return TGS_OK;
+}
+
+extern "C" uint32_t tgs_tide_row_blocks(uint64_t n_rows) {
+  return (uint32_t)((n_rows + VIS_THREADS - 1) / VIS_THREADS);
+}
+
+extern "C" int tgs_tide_visibility(uint64_t n_rows, const float* params, uint32_t C,
+                                   const float* viewmats, const float* Ks, const float* campos,
+                                   int32_t W, int32_t H, float eps2d, float near_plane,
+                                   float far_plane, float radius_clip, uint32_t* masks,
+                                   uint32_t* counts, hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  if (n_rows == 0) return TGS_OK;
+  TGS_CHECK_ARG(params && viewmats && Ks && campos && masks && counts, "tide_visibility: null");
+  TGS_CHECK_ARG(n_rows < (1ull << 31), "tide_visibility: at most 2^31-1 rows");
+  TideCams tc{viewmats, Ks, campos, C};
+  hipLaunchKernelGGL(tide_visibility_kernel, dim3(tgs_tide_row_blocks(n_rows)), dim3(VIS_THREADS),
+                     0, stream, n_rows, params, tc, W, H, eps2d, near_plane, far_plane,
+                     radius_clip, masks, counts);
+  TGS_RETURN_LAUNCH("tgs_tide_visibility");
+}
+
+extern "C" int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* masks,
+                                const uint32_t* counts, const uint32_t* offs, int32_t* entries,
+                                int32_t* touched, int32_t* visit_base, int32_t* visits,
+                                uint32_t* totals, int32_t* cam_offsets, hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  if (n_rows == 0) return TGS_OK;
+  TGS_CHECK_ARG(masks && counts && offs && entries && touched && visit_base && visits && totals &&
+                    cam_offsets,
+                "tide_compact: null");
+  const uint32_t nb = tgs_tide_row_blocks(n_rows);
+  hipLaunchKernelGGL(tide_compact_kernel, dim3(nb), dim3(VIS_THREADS), 0, stream, n_rows, C,
+                     masks, offs, entries, touched, visit_base, visits, totals);
+  TGS_LAUNCH_CHECK("tgs_tide_compact");
+  hipLaunchKernelGGL(tide_totals_kernel, dim3(1), dim3(64), 0, stream, C, nb, counts, offs,
+                     totals, cam_offsets, visit_base);
+  TGS_RETURN_LAUNCH("tgs_tide_compact");
+}
+
+extern "C" int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries,
+                                    const int32_t* cam_offsets, uint32_t C, const float* params,
+                                    const float* viewmats, const float* Ks, const float* campos,
+                                    int32_t W, int32_t H, float eps2d, float near_plane,
+                                    float far_plane, float radius_clip, int32_t sh_degree,
+                                    uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
+                                    float* splats, int32_t* tiles_per_entry, hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  if (n_entries == 0) return TGS_OK;
+  TGS_CHECK_ARG(entries && cam_offsets && params && viewmats && Ks && campos && splats &&
+                    tiles_per_entry,
+                "tide_project_fwd: null");
+  TGS_CHECK_ARG(sh_degree >= 0 && sh_degree <= 3, "tide step: sh_degree must be in [0,3]");
+  TGS_CHECK_ARG(((uintptr_t)splats & 15) == 0, "tide_project_fwd: splats must be 16-byte aligned");
+  TideCams tc{viewmats, Ks, campos, C};
+  hipLaunchKernelGGL(tide_project_fwd_kernel, dim3(tgs_blocks(n_entries, 256)), dim3(256), 0,
+                     stream, n_entries, entries, cam_offsets, tc, params, W, H, eps2d, near_plane,
+                     far_plane, radius_clip, sh_degree, tile_size, tile_width, tile_height,
+                     (float4*)splats, tiles_per_entry);
+  TGS_RETURN_LAUNCH("tgs_tide_project_fwd");
+}
+
+extern "C" int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,
+                                   const float* splats, const int64_t* cum_tiles,
+                                   uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
+                                   uint32_t tile_n_bits, int64_t* isect_ids, int32_t* flatten_ids,
+                                   hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  if (n_entries == 0) return TGS_OK;
+  TGS_CHECK_ARG(cam_offsets && splats && cum_tiles && isect_ids && flatten_ids,
+                "tide_isect_emit: null");
+  hipLaunchKernelGGL(tide_isect_emit_kernel, dim3(tgs_blocks(n_entries, 256)), dim3(256), 0,
+                     stream, n_entries, cam_offsets, C, (const float4*)splats, cum_tiles,
+                     tile_size, tile_width, tile_height, tile_n_bits, isect_ids, flatten_ids);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_emit");
+}
+
+extern "C" int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const float* backgrounds,
+                                      uint32_t W, uint32_t H, uint32_t tile_width,
+                                      uint32_t tile_height, const int32_t* tile_offsets,
+                                      const int32_t* flatten_ids, uint32_t n_isects,
+                                      float* images, float* alphas, int32_t* last_ids,
+                                      hipStream_t stream) {
+  if (C == 0 || W == 0 || H == 0) return TGS_OK;
+  TGS_CHECK_ARG(tile_offsets && images && alphas && last_ids, "tide_rasterize_fwd: null");
+  TGS_CHECK_ARG(n_isects == 0 || (splats && flatten_ids), "tide_rasterize_fwd: null splats");
+  TGS_CHECK_ARG(tile_width * 16 >= W && tile_height * 16 >= H, "tide_rasterize_fwd: tile grid");
+  const RasterGeom G{C, W, H, tile_width, tile_height, n_isects};
+  hipLaunchKernelGGL((raster_fwd_kernel<3, 16, PackedSplats>), dim3(C, tile_height, tile_width),
+                     dim3(256), 0, stream, G, PackedSplats{(const float4*)splats}, backgrounds,
+                     tile_offsets, flatten_ids, images, alphas, last_ids);
+  TGS_RETURN_LAUNCH("tgs_tide_rasterize_fwd");
+}
+
+extern "C" int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const float* backgrounds,
+                                      uint32_t W, uint32_t H, uint32_t tile_width,
+                                      uint32_t tile_height, const int32_t* tile_offsets,
+                                      const int32_t* flatten_ids, uint32_t n_isects,
+                                      const float* alphas, const int32_t* last_ids,
+                                      const float* v_images, float* splat_grads,
+                                      hipStream_t stream) {
+  if (C == 0 || W == 0 || H == 0 || n_isects == 0) return TGS_OK;
+  TGS_CHECK_ARG(splats && tile_offsets && flatten_ids && alphas && last_ids && v_images &&
+                    splat_grads,
+                "tide_rasterize_bwd: null");
+  TGS_CHECK_ARG(tile_width * 16 >= W && tile_height * 16 >= H, "tide_rasterize_bwd: tile grid");
+  const RasterGeom G{C, W, H, tile_width, tile_height, n_isects};
+  hipLaunchKernelGGL((raster_bwd_kernel<3, 16, PackedSplats, PackedGrads>),
+                     dim3(C, tile_height, tile_width), dim3(256), 0, stream, G,
+                     PackedSplats{(const float4*)splats}, PackedGrads{splat_grads}, backgrounds,
+                     tile_offsets, flatten_ids, alphas, last_ids, v_images, (const float*)nullptr);
+  TGS_RETURN_LAUNCH("tgs_tide_rasterize_bwd");
+}
+
+extern "C" int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched,
+                                    const int32_t* visit_base, const int32_t* visits,
+                                    const int32_t* cam_offsets, uint32_t C, const float* params,
+                                    const float* viewmats, const float* Ks, const float* campos,
+                                    int32_t W, int32_t H, float eps2d, int32_t sh_degree,
+                                    const float* splats, const float* splat_grads, float* grads,
+                                    hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  if (n_touched == 0) return TGS_OK;
+  TGS_CHECK_ARG(touched && visit_base && visits && cam_offsets && params && viewmats && Ks &&
+                    campos && splats && splat_grads && grads,
+                "tide_project_bwd: null");
+  TGS_CHECK_ARG(sh_degree >= 0 && sh_degree <= 3, "tide step: sh_degree must be in [0,3]");
+  TideCams tc{viewmats, Ks, campos, C};
+  hipLaunchKernelGGL(tide_project_bwd_kernel, dim3(tgs_blocks(n_touched, 256)), dim3(256), 0,
+                     stream, n_touched, touched, visit_base, visits, cam_offsets, tc, params, W,
+                     H, eps2d, sh_degree, (const float4*)splats, splat_grads, grads);
+  TGS_RETURN_LAUNCH("tgs_tide_project_bwd");
+}

@@ -283,6 +283,9 @@ class GPUResidentAdam:
             strides[3 * k + 0], strides[3 * k + 1], strides[3 * k + 2] = ps, gs, self.TOTAL_WIDTH
             lrs[k] = component_lrs[name]
         self._error_flag.zero_()
+        hooks = getattr(self, "kernel_hooks", None)
+        if hooks:
+            hooks[0]()
         if kernel == "tgs_resident_adam_step":
             args = (n_rows, N.ptr(local_rows), index_is_i64, N.ptr(starts), N.ptr(ends), N.ptr(slots),
                     n_layout, self.block_size, N.ptr(self._bias_correction1),
@@ -293,6 +296,8 @@ class GPUResidentAdam:
                     n_layout, self.block_size, n, params_p, grads_p, m_p, v_p, widths, strides, lrs,
                     *extra_args, N.ptr(self._error_flag), N.stream_handle(self.device))
         N.call(kernel, *args)
+        if hooks:
+            hooks[1]()
 
     def _prepare(self, iteration, gaussians, sparse_grad_local_ids, sparse_grad_components):
         manager = getattr(gaussians, "gpu_working_set_manager", None)

@@ -1,0 +1,330 @@
+"""Fused per-batch TideGS training step on a resident ``[N, 59]`` table.
+
+One call of :meth:`TideStep.step` does what a TideGS batch does on the GPU
+(``strategies/tide_engine/engine.py:1435-2737`` + ``runtime.py:1741-1791``):
+per-camera visibility filters (packed-projection rule), the touched-row set,
+projection + SH colours, tile intersection and sort, alpha compositing, the
+L1 + SSIM loss (``base_engine.py:464-488``), the full backward into compact
+``[T, 59]`` row gradients, and the resident Adam (or Sophia) update of the
+touched rows.  Every stage is a HIP kernel from ``libtidegs_amd.so``; this
+module only sequences them and owns the buffers.
+
+The per-camera loop of the reference becomes one launch per stage over the
+whole batch: parameters do not change between the cameras of a batch, so the
+gradients are the same, and each touched row accumulates its cameras in the
+reference's camera order.
+
+Host synchronisations per step: the visibility totals, the intersection
+count, and the per-block touch counts of the optimizer (the reference has the
+same three kinds, ``isect_tiles.cu:166``, ``base_engine.py:407``,
+``gpu_resident_optimizer.py:296``).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import types
+from dataclasses import dataclass, field
+from typing import Dict, Optional
+
+import torch
+
+from . import _native as N
+from .resident_optim import GPUResidentAdam, GPUResidentSophia
+
+ROW = 59
+# CACHE-order column slices of the optimizer components (unified names)
+_CACHE_COLS = {
+    "xyz": (0, 3),
+    "scaling": (3, 6),
+    "rotation": (6, 10),
+    "opacity": (10, 11),
+    "features_dc": (11, 14),
+    "features_rest": (14, 59),
+}
+
+
+class _Manager:
+    """Working-set view expected by GPUResidentAdam: all blocks resident."""
+
+    def __init__(self, n_rows: int, block_size: int, device):
+        n_blocks = -(-n_rows // block_size)
+        self.loaded_blocks = list(range(n_blocks))
+        self.block_to_gpu_slice = {
+            b: slice(b * block_size, min(n_rows, (b + 1) * block_size)) for b in range(n_blocks)
+        }
+        self.local_to_global_idx = torch.empty(0, device=device)  # identity mapping
+
+
+class _TableGaussians:
+    """Component attributes as column views of the CACHE-order table."""
+
+    def __init__(self, table, manager, columns_lr, betas, eps):
+        self.gpu_working_set_manager = manager
+        for name, (a, b) in _CACHE_COLS.items():
+            setattr(self, "_" + name, table[:, a:b])
+        self.optimizer = types.SimpleNamespace(columns_lr=columns_lr,
+                                               param_groups=[{"betas": betas, "eps": eps}])
+
+
+@dataclass
+class StepStats:
+    n_cameras: int
+    visible_per_camera: list
+    touched_rows: int
+    entries: int
+    n_isects: int
+    loss_sums: torch.Tensor = field(repr=False)  # [C, 2] double on device
+    optimizer: dict = field(default_factory=dict)
+
+    def losses(self, width: int, height: int, lambda_dssim: float = 0.2):
+        s = self.loss_sums.double().cpu()
+        n = 3.0 * width * height
+        return [float((1 - lambda_dssim) * s[c, 0] / n + lambda_dssim * (1 - s[c, 1] / n))
+                for c in range(s.shape[0])]
+
+
+class TideStep:
+    """Fused TideGS batch step (forward, backward, resident optimizer) on one GPU."""
+
+    TILE = 16
+
+    def __init__(self, params: torch.Tensor, width: int, height: int, batch_size: int,
+                 block_size: int = 4096, sh_degree: int = 3, columns_lr=None,
+                 betas=(0.9, 0.999), eps: float = 1e-15, lr_scale_mode: str = "sqrt",
+                 eps2d: float = 0.3, near_plane: float = 0.01, far_plane: float = 1e10,
+                 radius_clip: float = 0.0, lambda_dssim: float = 0.2,
+                 backgrounds: Optional[torch.Tensor] = None, optimizer: str = "adam",
+                 sophia_rho: float = 0.04, gt_div: float = 255.0):
+        if params.dim() != 2 or params.shape[1] != ROW or params.dtype != torch.float32:
+            raise ValueError("params must be a float32 [N, 59] table (CACHE column order)")
+        if not params.is_cuda or not params.is_contiguous():
+            raise ValueError("params must be a contiguous GPU tensor")
+        self.params = params
+        self.device = params.device
+        self.W, self.H = int(width), int(height)
+        self.tw = -(-self.W // self.TILE)
+        self.th = -(-self.H // self.TILE)
+        self.bsz = int(batch_size)
+        self.sh_degree = int(sh_degree)
+        self.eps2d, self.near, self.far = float(eps2d), float(near_plane), float(far_plane)
+        self.radius_clip = float(radius_clip)
+        self.lambda_dssim = float(lambda_dssim)
+        self.gt_div = float(gt_div)
+        self.backgrounds = backgrounds
+        n = params.shape[0]
+        # TideGS hyper-parameter scaling (gaussian_model.py:855-888)
+        if columns_lr is None:
+            columns_lr = [1.6e-4, 0.05, 5e-3, 1e-3, 2.5e-3, 2.5e-3 / 20.0]
+        cols = torch.tensor(columns_lr, dtype=torch.float32)
+        if lr_scale_mode == "sqrt":
+            scale = math.sqrt(self.bsz)
+            cols = cols * scale
+            eps = eps / scale
+            betas = tuple(b ** self.bsz for b in betas)
+        elif lr_scale_mode == "linear":
+            cols = cols * self.bsz
+        self.manager = _Manager(n, block_size, self.device)
+        self.gaussians = _TableGaussians(params, self.manager, cols, betas, eps)
+        opt_cls = GPUResidentSophia if optimizer == "sophia" else GPUResidentAdam
+        kw = {"rho": sophia_rho} if optimizer == "sophia" else {}
+        self.optimizer = opt_cls(batch_size=self.bsz, block_size=block_size,
+                                 capacity_blocks=len(self.manager.loaded_blocks),
+                                 device=str(self.device), **kw)
+        self.optimizer.set_resident_blocks(self.manager.loaded_blocks)
+        self._iteration = 0
+        self._bufs: Dict[str, torch.Tensor] = {}
+        self.last: Dict[str, torch.Tensor] = {}
+        self._timing = False
+        self._events = []
+        self.stage_ms: Dict[str, float] = {}
+        self.last_visible_entries = 0
+
+    # ---- stage timing (HIP events on the launch stream) ----------------------
+    def _begin(self, name: str):
+        if self._timing:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self._events.append([name, ev, None])
+
+    def _end(self):
+        if self._timing:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self._events[-1][2] = ev
+
+    def _collect(self):
+        torch.cuda.synchronize(self.device)
+        out: Dict[str, float] = {}
+        for name, a, b in self._events:
+            out[name] = out.get(name, 0.0) + a.elapsed_time(b)
+        self._events = []
+        self.stage_ms = out
+
+    # ---- buffers ----------------------------------------------------------
+    def _buf(self, name: str, numel: int, dtype) -> torch.Tensor:
+        b = self._bufs.get(name)
+        if b is None or b.numel() < numel or b.dtype != dtype:
+            b = torch.empty(max(1, int(numel * 1.25) if b is not None else numel), dtype=dtype,
+                            device=self.device)
+            self._bufs[name] = b
+        return b[:numel]
+
+    # ---- stages -----------------------------------------------------------
+    def forward_backward(self, viewmats: torch.Tensor, Ks: torch.Tensor, gt: torch.Tensor):
+        """Everything up to the compact gradients; returns (touched, grads, stats)."""
+        C = viewmats.shape[0]
+        if not 1 <= C <= 32:
+            raise ValueError("1..32 cameras per batch")
+        s = N.stream_handle(self.device)
+        P = self.params
+        n = P.shape[0]
+        W, H, tw, th = self.W, self.H, self.tw, self.th
+        viewmats = viewmats.to(self.device, torch.float32).contiguous()
+        Ks = Ks.to(self.device, torch.float32).contiguous()
+        campos = torch.linalg.inv(viewmats)[:, :3, 3].contiguous()
+        gt = gt.to(self.device, torch.float32).contiguous()
+        lib = N.load()
+
+        # 1. visibility masks + per-block counts, scan, compaction
+        nb = lib.tgs_tide_row_blocks(n)
+        masks = self._buf("masks", n, torch.int32)
+        counts = self._buf("counts", (C + 2) * nb, torch.int32)
+        self._begin("visibility")
+        N.call("tgs_tide_visibility", n, N.ptr(P), C, N.ptr(viewmats), N.ptr(Ks), N.ptr(campos),
+               W, H, self.eps2d, self.near, self.far, self.radius_clip, N.ptr(masks),
+               N.ptr(counts), s)
+        offs = self._buf("offs", (C + 2) * nb, torch.int32)
+        ws = self._buf("scan_ws", lib.tgs_scan_workspace_size((C + 2) * nb), torch.uint8)
+        N.call("tgs_exclusive_scan_u32", N.ptr(counts), N.ptr(offs), (C + 2) * nb, N.ptr(ws),
+               ws.numel(), s)
+        entries = self._buf("entries", C * n, torch.int32)
+        visits = self._buf("visits", C * n, torch.int32)
+        touched = self._buf("touched", n, torch.int32)
+        visit_base = self._buf("visit_base", n + 1, torch.int32)
+        totals = self._buf("totals", C + 3, torch.int32)
+        cam_offsets = self._buf("cam_offsets", C + 1, torch.int32)
+        N.call("tgs_tide_compact", n, C, N.ptr(masks), N.ptr(counts), N.ptr(offs), N.ptr(entries),
+               N.ptr(touched), N.ptr(visit_base), N.ptr(visits), N.ptr(totals),
+               N.ptr(cam_offsets), s)
+        self._end()
+        tot = totals.cpu().tolist()  # sync 1
+        V = tot[C + 1]
+        T = tot[C]
+
+        # 2. projection + SH colours for every (camera, visible row)
+        splats = self._buf("splats", max(V, 1) * 12, torch.float32)
+        tiles = self._buf("tiles", max(V, 1), torch.int32)
+        self._begin("project_fwd")
+        N.call("tgs_tide_project_fwd", V, N.ptr(entries), N.ptr(cam_offsets), C, N.ptr(P),
+               N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H, self.eps2d, self.near, self.far,
+               0.0, self.sh_degree, self.TILE, tw, th, N.ptr(splats), N.ptr(tiles), s)
+        self._end()
+
+        # 3. intersections: count scan, emit, one sort for the batch, offsets
+        cum = self._buf("cum", max(V, 1), torch.int64)
+        ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(max(V, 1)), torch.uint8)
+        n_isects = 0
+        self._begin("isect_scan")
+        if V:
+            N.call("tgs_inclusive_scan_i32_i64", N.ptr(tiles), N.ptr(cum), V, N.ptr(ws),
+                   ws.numel(), s)
+        self._end()
+        if V:
+            n_isects = int(cum[V - 1].item())  # sync 2
+        tile_bits = (tw * th).bit_length()
+        cam_bits = C.bit_length()
+        keys = self._buf("keys", max(n_isects, 1), torch.int64)
+        fids = self._buf("fids", max(n_isects, 1), torch.int32)
+        keys2 = self._buf("keys2", max(n_isects, 1), torch.int64)
+        fids2 = self._buf("fids2", max(n_isects, 1), torch.int32)
+        self._begin("isect_sort")
+        if n_isects:
+            N.call("tgs_tide_isect_emit", V, N.ptr(cam_offsets), C, N.ptr(splats), N.ptr(cum),
+                   self.TILE, tw, th, tile_bits, N.ptr(keys), N.ptr(fids), s)
+            sws = self._buf("sort_ws", lib.tgs_radix_sort_workspace_size(n_isects), torch.uint8)
+            sel = ctypes.c_int(0)
+            N.call("tgs_radix_sort_pairs", N.ptr(keys), N.ptr(fids), N.ptr(keys2), N.ptr(fids2),
+                   n_isects, 0, 32 + tile_bits + cam_bits, N.ptr(sws), sws.numel(),
+                   ctypes.byref(sel), s)
+            if sel.value:
+                keys, fids = keys2, fids2
+        offsets = self._buf("offsets", C * th * tw, torch.int32)
+        N.call("tgs_isect_offset_encode", n_isects, N.ptr(keys), C, tw, th, N.ptr(offsets), s)
+        self._end()
+
+        # 4. rasterize, loss, loss backward, rasterize backward
+        images = self._buf("images", C * H * W * 3, torch.float32)
+        alphas = self._buf("alphas", C * H * W, torch.float32)
+        last_ids = self._buf("last_ids", C * H * W, torch.int32)
+        bg = self.backgrounds
+        self._begin("raster_fwd")
+        N.call("tgs_tide_rasterize_fwd", C, N.ptr(splats), N.ptr(bg), W, H, tw, th,
+               N.ptr(offsets), N.ptr(fids), n_isects, N.ptr(images), N.ptr(alphas),
+               N.ptr(last_ids), s)
+        self._end()
+        parts = self._buf("loss_parts", 3 * C * 3 * H * W, torch.float32)
+        plane = C * 3 * H * W
+        sums = self._buf("loss_sums", 2 * C, torch.float64)
+        self._begin("loss")
+        N.call("tgs_fill_u32", N.ptr(sums), 4 * C, 0, s)
+        N.call("tgs_tide_loss_fwd", C, H, W, N.ptr(images), N.ptr(gt), self.gt_div,
+               N.ptr(parts), N.ptr(parts[plane:]), N.ptr(parts[2 * plane:]), N.ptr(sums), s)
+        v_images = self._buf("v_images", C * H * W * 3, torch.float32)
+        N.call("tgs_tide_loss_bwd", C, H, W, N.ptr(images), N.ptr(gt), self.gt_div,
+               self.lambda_dssim, N.ptr(parts), N.ptr(parts[plane:]), N.ptr(parts[2 * plane:]),
+               N.ptr(v_images), s)
+        self._end()
+        sgrads = self._buf("splat_grads", max(V, 1) * 9, torch.float32)
+        N.call("tgs_fill_u32", N.ptr(sgrads), max(V, 1) * 9, 0, s)
+        self._begin("raster_bwd")
+        N.call("tgs_tide_rasterize_bwd", C, N.ptr(splats), N.ptr(bg), W, H, tw, th,
+               N.ptr(offsets), N.ptr(fids), n_isects, N.ptr(alphas), N.ptr(last_ids),
+               N.ptr(v_images), N.ptr(sgrads), s)
+        self._end()
+
+        # 5. per touched row: projection + SH + activation backward
+        grads = self._buf("grads", max(T, 1) * ROW, torch.float32).view(-1, ROW)[:T]
+        self._begin("project_bwd")
+        N.call("tgs_tide_project_bwd", T, N.ptr(touched), N.ptr(visit_base), N.ptr(visits),
+               N.ptr(cam_offsets), C, N.ptr(P), N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H,
+               self.eps2d, self.sh_degree, N.ptr(splats), N.ptr(sgrads), N.ptr(grads), s)
+        self._end()
+        if self._timing:
+            self.last_visible_entries = int((splats[: V * 12].view(-1, 12)[:, 7] > 0).sum())
+        self.last = dict(masks=masks, entries=entries[:V], cam_offsets=cam_offsets,
+                         touched=touched[:T], visit_base=visit_base[:T + 1], visits=visits[:V],
+                         splats=splats[: V * 12].view(-1, 12), isect_ids=keys[:n_isects],
+                         flatten_ids=fids[:n_isects], offsets=offsets.view(C, th, tw),
+                         images=images.view(C, H, W, 3), alphas=alphas.view(C, H, W),
+                         last_ids=last_ids.view(C, H, W), v_images=v_images.view(C, H, W, 3),
+                         splat_grads=sgrads[: V * 9].view(-1, 9), grads=grads, campos=campos)
+        stats = StepStats(n_cameras=C, visible_per_camera=tot[:C], touched_rows=T, entries=V,
+                          n_isects=n_isects, loss_sums=sums.view(C, 2))
+        return touched[:T], grads, stats
+
+    def optimizer_step(self, touched: torch.Tensor, grads: torch.Tensor) -> dict:
+        self._iteration += 1
+        comps = {name: grads[:, a:b] for name, (a, b) in _CACHE_COLS.items()}
+        return self.optimizer.step(self._iteration, self.gaussians, touched, comps)
+
+    def step(self, viewmats: torch.Tensor, Ks: torch.Tensor, gt: torch.Tensor,
+             timing: bool = False) -> StepStats:
+        """One batch: forward, backward and the resident optimizer update.
+
+        With ``timing`` the stages are bracketed by HIP events on the launch
+        stream and their times (ms) are left in ``self.stage_ms``.
+        """
+        self._timing = bool(timing)
+        self._events = []
+        try:
+            touched, grads, stats = self.forward_backward(viewmats, Ks, gt)
+            if self._timing:
+                self.optimizer.kernel_hooks = (lambda: self._begin("adam"), self._end)
+            stats.optimizer = self.optimizer_step(touched, grads) if touched.numel() else {}
+            if self._timing:
+                self._collect()
+        finally:
+            self._timing = False
+            self.optimizer.kernel_hooks = None
+        return stats
