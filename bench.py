@@ -37,7 +37,7 @@ BYTES = {
 }
 
 
-def cpu_baseline(width, height, frac_a=1 / 128, frac_b=1 / 64, seed=0):
+def cpu_baseline(width, height, frac_a=1 / 16, frac_b=1 / 8, seed=0):
     """Time the CPU oracle on one camera of the same workload with a random
     subset of the Gaussians at two subset sizes, fit t = t_pix + f * t_gauss,
     and extrapolate to 16 cameras x 4M Gaussians (single thread)."""
