@@ -239,6 +239,15 @@ int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries, const int32
                          float far_plane, float radius_clip, int32_t sh_degree,
                          uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
                          float* splats, int32_t* tiles_per_entry, tgs_stream_t stream);
+/* Per-bucket depth sort of the fused step: after a stable radix sort of the
+ * camera|tile key bits [32, 32+tile_bits+cam_bits) (tgs_radix_sort_pairs)
+ * and tgs_isect_offset_encode, sorts each (camera, tile) bucket of
+ * isect_ids / flatten_ids in place by (depth bits, flatten id) -- the order
+ * of the reference's full-key sort (isect_tiles.cu:189-227).  tmp and
+ * scratch: [n_isects] u64 (used for buckets above 8192 intersections). */
+int tgs_tide_bucket_sort(uint32_t n_buckets, uint32_t n_isects, const int32_t* bucket_offsets,
+                         int64_t* isect_ids, int32_t* flatten_ids, uint64_t* tmp,
+                         uint64_t* scratch, tgs_stream_t stream);
 /* Batched isect emission (isect_tiles.cu:73-98 with camera ids). */
 int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,
                         const float* splats, const int64_t* cum_tiles, uint32_t tile_size,

@@ -58,7 +58,8 @@ def test_tide_step_grads_match_oracle(gpu, with_bg):
 def test_tide_step_isect_bit_exact(gpu):
     announce("tide step isect")
     sc = _scene(seed=2)
-    ts = TideStep(sc.params.to(gpu).contiguous(), sc.width, sc.height, batch_size=sc.n_cams)
+    ts = TideStep(sc.params.to(gpu).contiguous(), sc.width, sc.height, batch_size=sc.n_cams,
+                  keep_isect_ids=True)
     ts.forward_backward(sc.viewmats, sc.Ks, sc.gt)
     sp = to_np(ts.last["splats"])
     offs = to_np(ts.last["cam_offsets"])

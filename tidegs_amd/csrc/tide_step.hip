@@ -345,6 +345,126 @@ __global__ void __launch_bounds__(256) tide_isect_emit_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Per-bucket depth sort (fused path).  The order the reference's radix sort
+// gives camera|tile|depth keys (isect_tiles.cu:189-227) is ascending in
+// (camera*n_tiles + tile, depth bits, entry), a total order.  The fused step
+// radix-sorts only the camera|tile bits (stable, so each bucket keeps entry
+// order) and this kernel then sorts every bucket by (depth bits, entry) in
+// LDS -- bitonic up to 8192 intersections, merge-path passes beyond.
+// ---------------------------------------------------------------------------
+#define BSORT_THREADS 512
+#define BSORT_CAP 8192  // 64 KB of 64-bit keys in LDS
+
+__device__ __forceinline__ void bitonic_lds(uint64_t* s, uint32_t p) {
+  for (uint32_t k = 2; k <= p; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      for (uint32_t h = threadIdx.x; h < (p >> 1); h += blockDim.x) {
+        const uint32_t lo = 2 * h - (h & (j - 1));  // h = q j + r -> 2 q j + r
+        const uint32_t hi = lo + j;
+        const bool asc = (lo & k) == 0;
+        const uint64_t a = s[lo], b = s[hi];
+        if ((a > b) == asc) {
+          s[lo] = b;
+          s[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Merge two sorted runs src[lo,mid) and src[mid,hi) into dst[lo,hi) with the
+// whole block (merge-path partition per thread, then a sequential merge).
+__device__ __forceinline__ void block_merge(const uint64_t* __restrict__ src,
+                                            uint64_t* __restrict__ dst, uint32_t lo,
+                                            uint32_t mid, uint32_t hi) {
+  const uint32_t n = hi - lo;
+  const uint32_t step = (n + blockDim.x - 1) / blockDim.x;
+  const uint32_t d0 = min(n, threadIdx.x * step);
+  const uint32_t d1 = min(n, d0 + step);
+  if (d0 >= d1) return;
+  const uint32_t na = mid - lo, nb = hi - mid;
+  // first output diagonal d0: find i (taken from A) with i + j = d0
+  auto split = [&](uint32_t d) {
+    uint32_t a_lo = d > nb ? d - nb : 0u, a_hi = min(d, na);
+    while (a_lo < a_hi) {
+      const uint32_t i = (a_lo + a_hi) >> 1;
+      // take i from A, d - i from B: valid if A[i] > B[d-i-1]
+      if (src[lo + i] <= src[mid + d - i - 1])
+        a_lo = i + 1;
+      else
+        a_hi = i;
+    }
+    return a_lo;
+  };
+  uint32_t i = split(d0), j = d0 - i;
+  for (uint32_t d = d0; d < d1; ++d) {
+    const bool take_a = j >= nb || (i < na && src[lo + i] <= src[mid + j]);
+    dst[lo + d] = take_a ? src[lo + i++] : src[mid + j++];
+  }
+}
+
+__global__ void __launch_bounds__(BSORT_THREADS) tide_bucket_sort_kernel(
+    uint32_t n_buckets, uint32_t n_isects, const int32_t* __restrict__ bucket_offsets,
+    int64_t* __restrict__ keys, int32_t* __restrict__ fids, uint64_t* __restrict__ tmp,
+    uint64_t* __restrict__ scratch) {
+  __shared__ uint64_t s[BSORT_CAP];
+  const uint32_t b = blockIdx.x;
+  const uint32_t start = (uint32_t)bucket_offsets[b];
+  const uint32_t end = b + 1 < n_buckets ? (uint32_t)bucket_offsets[b + 1] : n_isects;
+  const uint32_t n = end - start;
+  if (n <= 1) return;
+  // composite (depth bits, entry): ascending order = the reference's order
+  // inside one (camera, tile) bucket
+  auto comp = [&](uint32_t k) {
+    return ((uint64_t)(uint32_t)keys[start + k] << 32) | (uint32_t)fids[start + k];
+  };
+  const uint64_t* result;
+  if (n <= BSORT_CAP) {
+    uint32_t p = 2;
+    while (p < n) p <<= 1;
+    for (uint32_t k = threadIdx.x; k < p; k += blockDim.x) s[k] = k < n ? comp(k) : ~0ull;
+    __syncthreads();
+    bitonic_lds(s, p);
+    result = s;
+  } else {
+    for (uint32_t r0 = 0; r0 < n; r0 += BSORT_CAP) {
+      const uint32_t m = min(BSORT_CAP, n - r0);
+      for (uint32_t k = threadIdx.x; k < BSORT_CAP; k += blockDim.x)
+        s[k] = k < m ? comp(r0 + k) : ~0ull;
+      __syncthreads();
+      bitonic_lds(s, BSORT_CAP);
+      for (uint32_t k = threadIdx.x; k < m; k += blockDim.x) tmp[start + r0 + k] = s[k];
+      __syncthreads();
+    }
+    uint64_t* src = tmp + start;
+    uint64_t* dst = scratch + start;
+    for (uint32_t w = BSORT_CAP; w < n; w <<= 1) {
+      for (uint32_t lo = 0; lo < n; lo += 2 * w) {
+        const uint32_t mid = min(n, lo + w), hi = min(n, lo + 2 * w);
+        if (mid >= hi) {
+          for (uint32_t k = lo + threadIdx.x; k < hi; k += blockDim.x) dst[k] = src[k];
+        } else {
+          block_merge(src, dst, lo, mid, hi);
+        }
+        __syncthreads();
+      }
+      uint64_t* t = src;
+      src = dst;
+      dst = t;
+    }
+    result = src;
+  }
+  __syncthreads();
+  const int64_t hi_bits = keys[start] & ~(int64_t)0xffffffffll;
+  for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
+    const uint64_t v = result[k];
+    fids[start + k] = (int32_t)(uint32_t)(v & 0xffffffffu);
+    keys[start + k] = hi_bits | (int64_t)(int32_t)(uint32_t)(v >> 32);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Backward: one thread per touched row.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
@@ -503,6 +623,19 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries,
                      far_plane, radius_clip, sh_degree, tile_size, tile_width, tile_height,
                      (float4*)splats, tiles_per_entry);
   TGS_RETURN_LAUNCH("tgs_tide_project_fwd");
+}
+
+
+extern "C" int tgs_tide_bucket_sort(uint32_t n_buckets, uint32_t n_isects,
+                                    const int32_t* bucket_offsets, int64_t* isect_ids,
+                                    int32_t* flatten_ids, uint64_t* tmp, uint64_t* scratch,
+                                    hipStream_t stream) {
+  if (n_buckets == 0 || n_isects == 0) return TGS_OK;
+  TGS_CHECK_ARG(bucket_offsets && isect_ids && flatten_ids && tmp && scratch,
+                "tide_bucket_sort: null");
+  hipLaunchKernelGGL(tide_bucket_sort_kernel, dim3(n_buckets), dim3(BSORT_THREADS), 0, stream,
+                     n_buckets, n_isects, bucket_offsets, isect_ids, flatten_ids, tmp, scratch);
+  TGS_RETURN_LAUNCH("tgs_tide_bucket_sort");
 }
 
 extern "C" int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,

@@ -95,7 +95,7 @@ class TideStep:
                  eps2d: float = 0.3, near_plane: float = 0.01, far_plane: float = 1e10,
                  radius_clip: float = 0.0, lambda_dssim: float = 0.2,
                  backgrounds: Optional[torch.Tensor] = None, optimizer: str = "adam",
-                 sophia_rho: float = 0.04, gt_div: float = 255.0):
+                 sophia_rho: float = 0.04, gt_div: float = 255.0, keep_isect_ids: bool = False):
         if params.dim() != 2 or params.shape[1] != ROW or params.dtype != torch.float32:
             raise ValueError("params must be a float32 [N, 59] table (CACHE column order)")
         if not params.is_cuda or not params.is_contiguous():
@@ -112,6 +112,7 @@ class TideStep:
         self.lambda_dssim = float(lambda_dssim)
         self.gt_div = float(gt_div)
         self.backgrounds = backgrounds
+        self.keep_isect_ids = bool(keep_isect_ids)  # materialise gsplat's isect keys (tests)
         n = params.shape[0]
         # TideGS hyper-parameter scaling (gaussian_model.py:855-888)
         if columns_lr is None:
@@ -212,7 +213,8 @@ class TideStep:
         V = tot[C + 1]
         T = tot[C]
 
-        # 2. projection + SH colours for every (camera, visible row)
+        # 2. projection + SH colours for every (camera, visible row), tiles per entry
+        n_buckets = C * th * tw
         splats = self._buf("splats", max(V, 1) * 12, torch.float32)
         tiles = self._buf("tiles", max(V, 1), torch.int32)
         self._begin("project_fwd")
@@ -221,37 +223,43 @@ class TideStep:
                0.0, self.sh_degree, self.TILE, tw, th, N.ptr(splats), N.ptr(tiles), s)
         self._end()
 
-        # 3. intersections: count scan, emit, one sort for the batch, offsets
-        cum = self._buf("cum", max(V, 1), torch.int64)
+        # 3. intersections: emit camera|tile|depth keys in entry order, stable radix
+        #    sort of the camera|tile bits only, bucket offsets, per-bucket depth sort
+        cum = self._buf("cum_tiles", max(V, 1), torch.int64)
         ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(max(V, 1)), torch.uint8)
-        n_isects = 0
         self._begin("isect_scan")
         if V:
             N.call("tgs_inclusive_scan_i32_i64", N.ptr(tiles), N.ptr(cum), V, N.ptr(ws),
                    ws.numel(), s)
         self._end()
-        if V:
-            n_isects = int(cum[V - 1].item())  # sync 2
+        n_isects = int(cum[V - 1].item()) if V else 0  # sync 2
         tile_bits = (tw * th).bit_length()
         cam_bits = C.bit_length()
-        keys = self._buf("keys", max(n_isects, 1), torch.int64)
-        fids = self._buf("fids", max(n_isects, 1), torch.int32)
-        keys2 = self._buf("keys2", max(n_isects, 1), torch.int64)
-        fids2 = self._buf("fids2", max(n_isects, 1), torch.int32)
+        cap = max(n_isects, 1)
+        keys = self._buf("keys", cap, torch.int64)
+        keys2 = self._buf("keys2", cap, torch.int64)
+        fids = self._buf("fids", cap, torch.int32)
+        fids2 = self._buf("fids2", cap, torch.int32)
+        tmp = self._buf("bsort_tmp", cap, torch.int64)
+        scratch = self._buf("bsort_scratch", cap, torch.int64)
+        rws = self._buf("radix_ws", max(1, lib.tgs_radix_sort_workspace_size(cap)), torch.uint8)
+        offsets = self._buf("offsets", n_buckets, torch.int32)
         self._begin("isect_sort")
         if n_isects:
             N.call("tgs_tide_isect_emit", V, N.ptr(cam_offsets), C, N.ptr(splats), N.ptr(cum),
                    self.TILE, tw, th, tile_bits, N.ptr(keys), N.ptr(fids), s)
-            sws = self._buf("sort_ws", lib.tgs_radix_sort_workspace_size(n_isects), torch.uint8)
             sel = ctypes.c_int(0)
             N.call("tgs_radix_sort_pairs", N.ptr(keys), N.ptr(fids), N.ptr(keys2), N.ptr(fids2),
-                   n_isects, 0, 32 + tile_bits + cam_bits, N.ptr(sws), sws.numel(),
+                   n_isects, 32, 32 + tile_bits + cam_bits, N.ptr(rws), rws.numel(),
                    ctypes.byref(sel), s)
             if sel.value:
-                keys, fids = keys2, fids2
-        offsets = self._buf("offsets", C * th * tw, torch.int32)
+                keys, keys2, fids, fids2 = keys2, keys, fids2, fids
         N.call("tgs_isect_offset_encode", n_isects, N.ptr(keys), C, tw, th, N.ptr(offsets), s)
+        if n_isects:
+            N.call("tgs_tide_bucket_sort", n_buckets, n_isects, N.ptr(offsets), N.ptr(keys),
+                   N.ptr(fids), N.ptr(tmp), N.ptr(scratch), s)
         self._end()
+        isect_ids = keys if self.keep_isect_ids else None
 
         # 4. rasterize, loss, loss backward, rasterize backward
         images = self._buf("images", C * H * W * 3, torch.float32)
@@ -294,8 +302,9 @@ class TideStep:
             self.last_visible_entries = int((splats[: V * 12].view(-1, 12)[:, 7] > 0).sum())
         self.last = dict(masks=masks, entries=entries[:V], cam_offsets=cam_offsets,
                          touched=touched[:T], visit_base=visit_base[:T + 1], visits=visits[:V],
-                         splats=splats[: V * 12].view(-1, 12), isect_ids=keys[:n_isects],
-                         flatten_ids=fids[:n_isects], offsets=offsets.view(C, th, tw),
+                         splats=splats[: V * 12].view(-1, 12),
+                         isect_ids=isect_ids[:n_isects] if isect_ids is not None else None,
+                         flatten_ids=fids[:n_isects], offsets=offsets[:n_buckets].view(C, th, tw),
                          images=images.view(C, H, W, 3), alphas=alphas.view(C, H, W),
                          last_ids=last_ids.view(C, H, W), v_images=v_images.view(C, H, W, 3),
                          splat_grads=sgrads[: V * 9].view(-1, 9), grads=grads, campos=campos)
