@@ -107,6 +107,18 @@ size_t tgs_radix_sort_workspace_size(uint64_t n);
 int tgs_radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
                          uint64_t n, int begin_bit, int end_bit, void* workspace,
                          size_t workspace_bytes, int* selector, tgs_stream_t stream);
+/* Segmented stable sort of uint32 keys with 4- or 8-byte values (the
+ * camera-grouped sorts of the fused step; a plain sort is one segment): each
+ * segment [seg_offsets[s], seg_offsets[s+1]) is sorted on key bits
+ * [begin_bit, end_bit) on its own.  seg_offsets is a HOST array of
+ * n_segments+1 (<= 65) non-decreasing offsets from 0 to n.  Double-buffered
+ * like tgs_radix_sort_pairs. */
+size_t tgs_segmented_sort_workspace_size(uint64_t n, uint32_t n_segments);
+int tgs_segmented_sort_pairs_u32(uint32_t* keys, void* vals, uint32_t* keys_alt, void* vals_alt,
+                                 uint32_t value_bytes, uint64_t n, uint32_t n_segments,
+                                 const uint32_t* seg_offsets, int begin_bit, int end_bit,
+                                 void* workspace, size_t workspace_bytes, int* selector,
+                                 tgs_stream_t stream);
 /* Replaces isect_offset_encode_tensor (isect_tiles.cu:234-301); offsets [C,th,tw]. */
 int tgs_isect_offset_encode(uint64_t n_isects, const int64_t* isect_ids, uint32_t C,
                             uint32_t tile_width, uint32_t tile_height, int32_t* offsets,
@@ -232,27 +244,42 @@ int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* masks, const u
                      int32_t* cam_offsets, tgs_stream_t stream);
 /* Projection + SH colour + activations per entry (engine.py:458-512 with
  * base_gaussian_model.py:35-50) -> splats [V,12] (3 x float4:
- * {x,y,opacity,depth},{a,b,c,radius},{r,g,b,0}) and tile counts [V]. */
+ * {x,y,opacity,depth},{a,b,c,radius},{r,g,b,0}), depth_keys [V] (float bits
+ * of the depth; 0xffffffff when culled) and entry_rects [V] (tile rectangle
+ * x0|x1<<8|y0<<16|y1<<24 in the high word, entry index in the low word;
+ * isect_tiles.cu:55-70).  Tile grid at most 255 x 255. */
 int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries, const int32_t* cam_offsets,
                          uint32_t C, const float* params, const float* viewmats, const float* Ks,
                          const float* campos, int32_t W, int32_t H, float eps2d, float near_plane,
                          float far_plane, float radius_clip, int32_t sh_degree,
                          uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
-                         float* splats, int32_t* tiles_per_entry, tgs_stream_t stream);
-/* Per-bucket depth sort of the fused step: after a stable radix sort of the
- * camera|tile key bits [32, 32+tile_bits+cam_bits) (tgs_radix_sort_pairs)
- * and tgs_isect_offset_encode, sorts each (camera, tile) bucket of
- * isect_ids / flatten_ids in place by (depth bits, flatten id) -- the order
- * of the reference's full-key sort (isect_tiles.cu:189-227).  tmp and
- * scratch: [n_isects] u64 (used for buckets above 8192 intersections). */
-int tgs_tide_bucket_sort(uint32_t n_buckets, uint32_t n_isects, const int32_t* bucket_offsets,
-                         int64_t* isect_ids, int32_t* flatten_ids, uint64_t* tmp,
-                         uint64_t* scratch, tgs_stream_t stream);
-/* Batched isect emission (isect_tiles.cu:73-98 with camera ids). */
+                         float* splats, uint32_t* depth_keys, uint64_t* entry_rects,
+                         tgs_stream_t stream);
+/* Intersections of the batch in the order of the reference's sort
+ * (isect_tiles.cu:73-98,189-227: camera, tile, depth bits, entry).  After
+ * tgs_segmented_sort_pairs_u32 of (depth_keys, entry_rects) per camera:
+ *   tgs_tide_isect_count     tiles [V] of the depth-ordered entries;
+ *   (tgs_inclusive_scan_i32_i64 -> cum_tiles)
+ *   tgs_tide_isect_segments  seg [C+1]: first intersection of each camera
+ *                            (seg[C] = n_isects);
+ *   tgs_tide_isect_emit      keys [n_isects] = camera << tile_n_bits | tile,
+ *                            flatten_ids = entry index, in depth order;
+ *   (tgs_segmented_sort_pairs_u32 of the tile bits per camera)
+ *   tgs_tide_offset_encode   offsets [C,th,tw] as tgs_isect_offset_encode;
+ *   tgs_tide_isect_ids       the reference's int64 ids (inspection only). */
+int tgs_tide_isect_count(uint32_t n_entries, const uint64_t* entry_rects, int32_t* tiles,
+                         tgs_stream_t stream);
+int tgs_tide_isect_segments(uint32_t C, const int32_t* cam_offsets, const int64_t* cum_tiles,
+                            uint32_t* seg, tgs_stream_t stream);
 int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,
-                        const float* splats, const int64_t* cum_tiles, uint32_t tile_size,
-                        uint32_t tile_width, uint32_t tile_height, uint32_t tile_n_bits,
-                        int64_t* isect_ids, int32_t* flatten_ids, tgs_stream_t stream);
+                        const uint64_t* entry_rects, const int64_t* cum_tiles,
+                        uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
+                        int32_t* flatten_ids, tgs_stream_t stream);
+int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, uint32_t C,
+                           uint32_t tile_width, uint32_t tile_height, uint32_t tile_n_bits,
+                           int32_t* offsets, tgs_stream_t stream);
+int tgs_tide_isect_ids(uint32_t n_isects, const uint32_t* keys, const int32_t* flatten_ids,
+                       const float* splats, int64_t* isect_ids, tgs_stream_t stream);
 /* Rasterize forward/backward over packed splats (tile 16, 3 channels);
  * images / v_images [C,H,W,3], alphas [C,H,W], last_ids [C,H,W];
  * splat_grads [V,9] accumulated (zero first): {mean2d 2, conic 3, color 3, opacity}. */

@@ -186,6 +186,45 @@ def test_radix_sort_pairs_stable(gpu, n, begin, end):
     np.testing.assert_array_equal(to_np(k), keys[order])
 
 
+@pytest.mark.parametrize("segs,bits,vbytes", [
+    ([0, 5000], 13, 4),
+    ([0, 0, 4096, 4097, 4097, 90_000], 13, 4),   # empty segments, a one-key segment
+    ([0, 1, 2, 3000, 3000], 32, 8),
+    ([0, 300_000, 300_001, 1_000_000], 32, 8),
+    ([0, 8192, 8192, 8192], 7, 4),
+])
+def test_segmented_sort_pairs_u32(gpu, segs, bits, vbytes):
+    """Each segment sorted stably on its own (numpy argsort kind='stable')."""
+    import ctypes
+    from tidegs_amd import _native as N
+    announce(f"segmented sort segs={segs} bits={bits} vbytes={vbytes}")
+    n = segs[-1]
+    rng = np.random.default_rng(n + bits)
+    keys = rng.integers(0, 2 ** 32, size=n, dtype=np.uint64).astype(np.uint32)
+    keys[: n // 3] = keys[n // 3: 2 * (n // 3)]  # duplicates exercise stability
+    vdt = np.int32 if vbytes == 4 else np.int64
+    vals = (np.arange(n, dtype=np.int64) * 3 + (1 << 40 if vbytes == 8 else 0)).astype(vdt)
+    k = torch.from_numpy(keys.view(np.int32)).to(gpu)
+    v = torch.from_numpy(vals).to(gpu)
+    k2, v2 = torch.empty_like(k), torch.empty_like(v)
+    lib = N.load()
+    ws = torch.empty(lib.tgs_segmented_sort_workspace_size(n, len(segs) - 1), dtype=torch.uint8,
+                     device=gpu)
+    sel = ctypes.c_int(0)
+    host = (ctypes.c_uint32 * len(segs))(*segs)
+    N.call("tgs_segmented_sort_pairs_u32", N.ptr(k), N.ptr(v), N.ptr(k2), N.ptr(v2), vbytes, n,
+           len(segs) - 1, host, 0, bits, N.ptr(ws), ws.numel(), ctypes.byref(sel),
+           N.stream_handle())
+    ko, vo = (k2, v2) if sel.value else (k, v)
+    ko = to_np(ko).view(np.uint32)
+    vo = to_np(vo)
+    mask = np.uint32((1 << bits) - 1) if bits < 32 else np.uint32(0xffffffff)
+    for a, b in zip(segs[:-1], segs[1:]):
+        order = np.argsort(keys[a:b] & mask, kind="stable") + a
+        np.testing.assert_array_equal(ko[a:b], keys[order])
+        np.testing.assert_array_equal(vo[a:b], vals[order])
+
+
 def _raster_case(gpu, seed, C=2, D=3, W=200, H=120, tile=16, packed=False):
     sc, radii, m2d, depths, conics, opac = _projected(gpu, seed=seed, C=C, W=W, H=H)
     tw, th = -(-W // tile), -(-H // tile)

@@ -54,6 +54,12 @@ SIGNATURES = {
         ctypes.c_int,
         [P, P, P, P, U64, ctypes.c_int, ctypes.c_int, P, SZ, ctypes.POINTER(ctypes.c_int), P],
     ),
+    "tgs_segmented_sort_workspace_size": (SZ, [U64, U32]),
+    "tgs_segmented_sort_pairs_u32": (
+        ctypes.c_int,
+        [P, P, P, P, U32, U64, U32, P, ctypes.c_int, ctypes.c_int, P, SZ,
+         ctypes.POINTER(ctypes.c_int), P],
+    ),
     "tgs_isect_offset_encode": (ctypes.c_int, [U64, P, U32, U32, U32, P, P]),
     "tgs_rasterize_supported_channels": (ctypes.c_int, [ctypes.POINTER(I32), I32]),
     "tgs_selftest_wave_reduce": (ctypes.c_int, [P, P, P]),
@@ -78,9 +84,13 @@ SIGNATURES = {
     "tgs_tide_compact": (ctypes.c_int, [U64, U32, P, P, P, P, P, P, P, P, P, P]),
     "tgs_tide_project_fwd": (
         ctypes.c_int,
-        [U32, P, P, U32, P, P, P, P, I32, I32, F32, F32, F32, F32, I32, U32, U32, U32, P, P, P]),
-    "tgs_tide_bucket_sort": (ctypes.c_int, [U32, U32, P, P, P, P, P, P]),
-    "tgs_tide_isect_emit": (ctypes.c_int, [U32, P, U32, P, P, U32, U32, U32, U32, P, P, P]),
+        [U32, P, P, U32, P, P, P, P, I32, I32, F32, F32, F32, F32, I32, U32, U32, U32, P, P, P,
+         P]),
+    "tgs_tide_isect_count": (ctypes.c_int, [U32, P, P, P]),
+    "tgs_tide_isect_segments": (ctypes.c_int, [U32, P, P, P, P]),
+    "tgs_tide_isect_emit": (ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P]),
+    "tgs_tide_offset_encode": (ctypes.c_int, [U32, P, U32, U32, U32, U32, P, P]),
+    "tgs_tide_isect_ids": (ctypes.c_int, [U32, P, P, P, P, P]),
     "tgs_tide_rasterize_fwd": (ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P]),
     "tgs_tide_rasterize_bwd": (
         ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, P]),

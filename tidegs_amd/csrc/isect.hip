@@ -11,8 +11,6 @@
 //              empty tiles take the next run's start; trailing tiles take n.
 #include "tgs_common.cuh"
 
-extern "C" int tgs_fill_u32(void* ptr, uint64_t n_words, uint32_t value, hipStream_t stream);
-
 struct TileRect {
   uint32_t x0, y0, x1, y1;
 };

@@ -10,12 +10,11 @@
 //
 // Scan: reduce-then-scan in three kernels (block sums, one-block scan of the
 // sums, per-block rescan), no inter-block spin-waits.
-// Radix pass (8-bit digit, 4096-key tiles of 256 threads x 16 keys):
-//   upsweep   per-tile digit histogram -> hist[digit * n_tiles + tile]
+// Radix pass (<= 8-bit digit, 4096-key tiles of 256 threads x 16 keys):
+//   hist      per-tile digit histogram -> hist[segment][digit][tile]
 //   scan      exclusive scan of hist (digit-major => global digit offsets)
-//   downsweep per-tile stable ranking: 8 ballots give each lane the set of
-//             lanes in its wave holding the same digit; per-wave counts in LDS
-//             give the offsets of earlier waves and rounds.
+//   scatter   per-tile stable ranking (ballot matching + per-wave counters),
+//             LDS reorder, coalesced write of each digit run.
 #include "tgs_common.cuh"
 
 #define SCAN_THREADS 256
@@ -26,6 +25,7 @@
 #define SORT_ITEMS 16
 #define SORT_TILE (SORT_THREADS * SORT_ITEMS)
 #define SORT_BINS 256
+#define RADIX_MAX_SEGS 64
 
 // ---------------------------------------------------------------------------
 // Block-level exclusive scan of one value per thread (256 threads, 4 waves).
@@ -168,53 +168,118 @@ extern "C" int tgs_exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint64_
 
 // ---------------------------------------------------------------------------
 // Radix sort
+//
+// Segmented LSD passes: the key range [0, n) is split into segments (one for
+// a plain sort; one per camera for the fused step, where entries and
+// intersections are already grouped by camera) and tiles never straddle a
+// segment, so one pass sorts every segment independently.  The histogram is
+// laid out [segment][digit][tile of segment]; its exclusive scan is then the
+// absolute output offset of (segment, digit, tile).
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ uint32_t digit_of(uint64_t key, int shift, uint32_t mask) {
+struct RadixSegs {
+  uint32_t n;                             // number of segments (>= 1)
+  uint32_t key_off[RADIX_MAX_SEGS + 1];   // key_off[0] = 0, key_off[n] = n_keys
+  uint32_t tile_base[RADIX_MAX_SEGS + 1]; // first tile of each segment
+};
+
+struct TileRange {
+  uint32_t start, count;  // keys [start, start + count)
+  uint32_t hbase, stride; // hist index of digit d: hbase + d * stride
+};
+
+__device__ __forceinline__ TileRange radix_tile(const RadixSegs& sg, uint32_t b) {
+  uint32_t lo = 0, hi = sg.n;  // largest s with tile_base[s] <= b
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (sg.tile_base[mid] <= b) lo = mid;
+    else hi = mid;
+  }
+  const uint32_t t = b - sg.tile_base[lo];
+  const uint32_t nts = sg.tile_base[lo + 1] - sg.tile_base[lo];
+  TileRange r;
+  r.start = sg.key_off[lo] + t * SORT_TILE;
+  const uint32_t end = sg.key_off[lo + 1];
+  r.count = end > r.start ? min((uint32_t)SORT_TILE, end - r.start) : 0u;
+  r.hbase = sg.tile_base[lo] * SORT_BINS + t;
+  r.stride = nts;
+  return r;
+}
+
+template <typename K>
+__device__ __forceinline__ uint32_t digit_of(K key, int shift, uint32_t mask) {
   return (uint32_t)(key >> shift) & mask;
 }
 
-__global__ void __launch_bounds__(SORT_THREADS) radix_upsweep_kernel(
-    const uint64_t* __restrict__ keys, uint64_t n, int shift, uint32_t mask, uint32_t n_tiles,
-    uint32_t* __restrict__ hist) {
-  __shared__ uint32_t s_hist[SORT_BINS];
-  s_hist[threadIdx.x] = 0;
+template <typename K>
+__global__ void __launch_bounds__(SORT_THREADS) radix_hist_kernel(const K* __restrict__ keys,
+                                                                  RadixSegs sg, int shift,
+                                                                  uint32_t mask,
+                                                                  uint32_t* __restrict__ hist) {
+  __shared__ uint32_t s_h[SORT_THREADS / 64][SORT_BINS];
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int w = 0; w < SORT_THREADS / 64; ++w) s_h[w][threadIdx.x] = 0;
   __syncthreads();
-  const uint64_t base = (uint64_t)blockIdx.x * SORT_TILE;
+  const TileRange tr = radix_tile(sg, blockIdx.x);
 #pragma unroll 4
   for (int r = 0; r < SORT_ITEMS; ++r) {
-    const uint64_t i = base + (uint64_t)r * SORT_THREADS + threadIdx.x;
-    if (i < n) atomicAdd(&s_hist[digit_of(keys[i], shift, mask)], 1u);
+    const uint32_t i = (uint32_t)r * SORT_THREADS + threadIdx.x;
+    if (i < tr.count) atomicAdd(&s_h[wave][digit_of(keys[tr.start + i], shift, mask)], 1u);
   }
   __syncthreads();
-  hist[(uint64_t)threadIdx.x * n_tiles + blockIdx.x] = s_hist[threadIdx.x];
+  uint32_t c = 0;
+#pragma unroll
+  for (int w = 0; w < SORT_THREADS / 64; ++w) c += s_h[w][threadIdx.x];
+  hist[tr.hbase + threadIdx.x * tr.stride] = c;
 }
 
-__global__ void __launch_bounds__(SORT_THREADS) radix_downsweep_kernel(
-    const uint64_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint64_t n,
-    int shift, uint32_t mask, uint32_t n_tiles, const uint32_t* __restrict__ hist_scan,
-    uint64_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
-  __shared__ uint32_t s_base[SORT_BINS];                       // global offset of digit
-  __shared__ uint32_t s_wave[SORT_THREADS / 64][SORT_BINS];    // per-wave counts this round
+// One tile of 4096 keys per block.  Wave w owns keys [w*1024, (w+1)*1024) of
+// the tile in rounds of 64; for each round 8 ballots give a lane the lanes of
+// its wave with the same digit, and a per-wave digit counter in LDS carries
+// the count of earlier rounds.  The tile is then scattered into LDS in
+// (digit, position) order and written out by consecutive threads, so each
+// digit's run of the tile is one contiguous store.
+template <typename K, typename V>
+__global__ void __launch_bounds__(SORT_THREADS) radix_scatter_kernel(
+    const K* __restrict__ keys_in, const V* __restrict__ vals_in, RadixSegs sg, int shift,
+    uint32_t mask, const uint32_t* __restrict__ hist_scan, K* __restrict__ keys_out,
+    V* __restrict__ vals_out) {
+  constexpr int WAVES = SORT_THREADS / 64;
+  __shared__ K s_k[SORT_TILE];
+  __shared__ V s_v[SORT_TILE];
+  __shared__ uint32_t s_wh[WAVES][SORT_BINS];
+  __shared__ uint32_t s_start[SORT_BINS];
+  __shared__ uint32_t s_gofs[SORT_BINS];
+  __shared__ uint32_t s_scan[WAVES];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  s_base[threadIdx.x] = hist_scan[(uint64_t)threadIdx.x * n_tiles + blockIdx.x];
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  const TileRange tr = radix_tile(sg, blockIdx.x);
 #pragma unroll
-  for (int w = 0; w < SORT_THREADS / 64; ++w) s_wave[w][threadIdx.x] = 0;
+  for (int w = 0; w < WAVES; ++w) s_wh[w][threadIdx.x] = 0;
   __syncthreads();
 
-  const uint64_t base = (uint64_t)blockIdx.x * SORT_TILE;
+  K k[SORT_ITEMS];
+  V v[SORT_ITEMS];
+  uint32_t rk[SORT_ITEMS];
+  const uint32_t wbase = (uint32_t)wave * 64u * SORT_ITEMS;
+#pragma unroll
   for (int r = 0; r < SORT_ITEMS; ++r) {
-    const uint64_t i = base + (uint64_t)r * SORT_THREADS + threadIdx.x;
-    const bool valid = i < n;
-    uint64_t key = 0;
-    uint32_t val = 0;
-    if (valid) {
-      key = keys_in[i];
-      val = vals_in[i];
+    const uint32_t li = wbase + (uint32_t)r * 64u + lane;
+    if (li < tr.count) {
+      k[r] = keys_in[tr.start + li];
+      v[r] = vals_in[tr.start + li];
+    } else {
+      k[r] = 0;
+      v[r] = 0;
     }
-    const uint32_t d = digit_of(key, shift, mask);
+  }
+#pragma unroll
+  for (int r = 0; r < SORT_ITEMS; ++r) {
+    const uint32_t li = wbase + (uint32_t)r * 64u + lane;
+    const bool valid = li < tr.count;
+    const uint32_t d = digit_of(k[r], shift, mask);
     uint64_t peers = tgs_ballot(valid);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -222,39 +287,104 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_downsweep_kernel(
       const uint64_t m = tgs_ballot(bit);
       peers &= bit ? m : ~m;
     }
-    const uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
-    const uint32_t cnt = (uint32_t)__popcll(peers);
-    // The highest peer lane publishes the wave's count for this digit.
-    const bool leader = valid && ((peers >> lane) == 1ull);
-    if (leader) s_wave[wave][d] = cnt;
-    __syncthreads();
-    if (valid) {
-      uint32_t off = s_base[d] + rank;
-      for (int w = 0; w < wave; ++w) off += s_wave[w][d];
-      keys_out[off] = key;
-      vals_out[off] = val;
-    }
-    __syncthreads();
-    // Thread t owns digit t: fold this round's counts into the base and clear.
-    uint32_t add = 0;
+    const uint32_t before = s_wh[wave][d];
+    __builtin_amdgcn_wave_barrier();
+    // the highest lane of each digit group advances the wave's counter
+    if (valid && (peers >> lane) == 1ull) s_wh[wave][d] = before + (uint32_t)__popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+    rk[r] = before + (uint32_t)__popcll(peers & lt_mask);
+  }
+  __syncthreads();
+  // thread t owns digit t: per-wave exclusive offsets, tile total, tile start
+  uint32_t tot = 0;
 #pragma unroll
-    for (int w = 0; w < SORT_THREADS / 64; ++w) {
-      add += s_wave[w][threadIdx.x];
-      s_wave[w][threadIdx.x] = 0;
+  for (int w = 0; w < WAVES; ++w) {
+    const uint32_t c = s_wh[w][threadIdx.x];
+    s_wh[w][threadIdx.x] = tot;
+    tot += c;
+  }
+  uint32_t all;
+  const uint32_t st = block_exclusive_scan<uint32_t>(tot, s_scan, all);
+  s_start[threadIdx.x] = st;
+  s_gofs[threadIdx.x] = hist_scan[tr.hbase + threadIdx.x * tr.stride] - st;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < SORT_ITEMS; ++r) {
+    const uint32_t li = wbase + (uint32_t)r * 64u + lane;
+    if (li < tr.count) {
+      const uint32_t d = digit_of(k[r], shift, mask);
+      const uint32_t pos = s_start[d] + s_wh[wave][d] + rk[r];
+      s_k[pos] = k[r];
+      s_v[pos] = v[r];
     }
-    s_base[threadIdx.x] += add;
-    __syncthreads();
+  }
+  __syncthreads();
+  for (uint32_t j = threadIdx.x; j < tr.count; j += SORT_THREADS) {
+    const K kk = s_k[j];
+    const uint32_t o = s_gofs[digit_of(kk, shift, mask)] + j;
+    keys_out[o] = kk;
+    vals_out[o] = s_v[j];
   }
 }
 
 static uint64_t sort_tiles(uint64_t n) { return (n + SORT_TILE - 1) / SORT_TILE; }
 
-extern "C" size_t tgs_radix_sort_workspace_size(uint64_t n) {
-  const uint64_t tiles = sort_tiles(n);
+static size_t radix_workspace(uint64_t tiles) {
   const uint64_t hist = tiles * SORT_BINS;
   // hist + scanned hist + scan block sums, each 256-byte aligned.
   auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
   return (size_t)(al(hist * 4) * 2 + al(tgs_scan_workspace_size(hist)));
+}
+
+extern "C" size_t tgs_radix_sort_workspace_size(uint64_t n) { return radix_workspace(sort_tiles(n)); }
+
+extern "C" size_t tgs_segmented_sort_workspace_size(uint64_t n, uint32_t n_segments) {
+  return radix_workspace(sort_tiles(n) + n_segments);
+}
+
+// Runs the passes over key bits [begin_bit, end_bit), splitting the range
+// into the fewest passes of at most 8 bits with widths as even as possible.
+template <typename K, typename V>
+static int radix_passes(K* keys, V* vals, K* keys_alt, V* vals_alt, const RadixSegs& sg,
+                        int begin_bit, int end_bit, void* workspace, int* selector,
+                        hipStream_t stream) {
+  const uint64_t tiles = sg.tile_base[sg.n];
+  const uint64_t hist_n = tiles * SORT_BINS;
+  auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
+  uint8_t* ws = (uint8_t*)workspace;
+  uint32_t* hist = (uint32_t*)ws;
+  uint32_t* hist_scan = (uint32_t*)(ws + al(hist_n * 4));
+  void* scan_ws = ws + 2 * al(hist_n * 4);
+  K* kin = keys;
+  V* vin = vals;
+  K* kout = keys_alt;
+  V* vout = vals_alt;
+  int sel = 0;
+  int shift = begin_bit;
+  int passes = (end_bit - begin_bit + 7) / 8;
+  while (shift < end_bit) {
+    const int bits = (end_bit - shift + passes - 1) / passes;
+    const uint32_t mask = (1u << bits) - 1u;
+    hipLaunchKernelGGL((radix_hist_kernel<K>), dim3((unsigned)tiles), dim3(SORT_THREADS), 0,
+                       stream, kin, sg, shift, mask, hist);
+    TGS_LAUNCH_CHECK("radix_hist");
+    int rc = exclusive_scan_u32(hist, hist_scan, hist_n, scan_ws, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL((radix_scatter_kernel<K, V>), dim3((unsigned)tiles), dim3(SORT_THREADS), 0,
+                       stream, kin, vin, sg, shift, mask, hist_scan, kout, vout);
+    TGS_LAUNCH_CHECK("radix_scatter");
+    K* tk = kin;
+    kin = kout;
+    kout = tk;
+    V* tv = vin;
+    vin = vout;
+    vout = tv;
+    sel ^= 1;
+    shift += bits;
+    --passes;
+  }
+  *selector = sel;
+  return TGS_OK;
 }
 
 // Stable ascending sort of (keys, vals) on key bits [begin_bit, end_bit).
@@ -270,44 +400,64 @@ extern "C" int tgs_radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* ke
   if (n <= 1 || end_bit <= begin_bit) return TGS_OK;
   TGS_CHECK_ARG(keys && vals && keys_alt && vals_alt && workspace, "radix_sort: null pointer");
   TGS_CHECK_ARG(begin_bit >= 0 && end_bit <= 64, "radix_sort: bit range out of [0,64]");
-  TGS_CHECK_ARG(n < (1ull << 32), "radix_sort: n must be < 2^32");
+  TGS_CHECK_ARG(n < (1ull << 32) - SORT_TILE, "radix_sort: n too large");
   if (workspace_bytes < tgs_radix_sort_workspace_size(n)) {
     tgs_set_error("radix_sort: workspace %zu < %zu", workspace_bytes,
                   tgs_radix_sort_workspace_size(n));
     return TGS_ERR_WORKSPACE;
   }
-  const uint64_t tiles = sort_tiles(n);
-  const uint64_t hist_n = tiles * SORT_BINS;
-  auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
-  uint8_t* ws = (uint8_t*)workspace;
-  uint32_t* hist = (uint32_t*)ws;
-  uint32_t* hist_scan = (uint32_t*)(ws + al(hist_n * 4));
-  void* scan_ws = ws + 2 * al(hist_n * 4);
+  RadixSegs sg{};
+  sg.n = 1;
+  sg.key_off[0] = 0;
+  sg.key_off[1] = (uint32_t)n;
+  sg.tile_base[0] = 0;
+  sg.tile_base[1] = (uint32_t)sort_tiles(n);
+  return radix_passes<uint64_t, uint32_t>(keys, vals, keys_alt, vals_alt, sg, begin_bit, end_bit,
+                                          workspace, selector, stream);
+}
 
-  uint64_t* kin = keys;
-  uint32_t* vin = vals;
-  uint64_t* kout = keys_alt;
-  uint32_t* vout = vals_alt;
-  int sel = 0;
-  for (int shift = begin_bit; shift < end_bit; shift += 8) {
-    const int bits = (end_bit - shift) < 8 ? (end_bit - shift) : 8;
-    const uint32_t mask = (1u << bits) - 1u;
-    hipLaunchKernelGGL(radix_upsweep_kernel, dim3((unsigned)tiles), dim3(SORT_THREADS), 0, stream,
-                       kin, n, shift, mask, (uint32_t)tiles, hist);
-    TGS_LAUNCH_CHECK("radix_upsweep");
-    int rc = exclusive_scan_u32(hist, hist_scan, hist_n, scan_ws, stream);
-    if (rc) return rc;
-    hipLaunchKernelGGL(radix_downsweep_kernel, dim3((unsigned)tiles), dim3(SORT_THREADS), 0,
-                       stream, kin, vin, n, shift, mask, (uint32_t)tiles, hist_scan, kout, vout);
-    TGS_LAUNCH_CHECK("radix_downsweep");
-    uint64_t* tk = kin;
-    kin = kout;
-    kout = tk;
-    uint32_t* tv = vin;
-    vin = vout;
-    vout = tv;
-    sel ^= 1;
+// Segmented stable sort of uint32 keys with 4- or 8-byte values: each segment
+// [seg_offsets[s], seg_offsets[s+1]) is sorted on its own.  seg_offsets is a
+// HOST array of n_segments+1 non-decreasing offsets from 0 to n.
+extern "C" int tgs_segmented_sort_pairs_u32(uint32_t* keys, void* vals, uint32_t* keys_alt,
+                                            void* vals_alt, uint32_t value_bytes, uint64_t n,
+                                            uint32_t n_segments, const uint32_t* seg_offsets,
+                                            int begin_bit, int end_bit, void* workspace,
+                                            size_t workspace_bytes, int* selector,
+                                            hipStream_t stream) {
+  TGS_CHECK_ARG(selector != nullptr, "segmented_sort: null selector");
+  *selector = 0;
+  if (n <= 1 || end_bit <= begin_bit) return TGS_OK;
+  TGS_CHECK_ARG(keys && vals && keys_alt && vals_alt && workspace && seg_offsets,
+                "segmented_sort: null pointer");
+  TGS_CHECK_ARG(value_bytes == 4 || value_bytes == 8, "segmented_sort: value_bytes must be 4 or 8");
+  TGS_CHECK_ARG(begin_bit >= 0 && end_bit <= 32, "segmented_sort: bit range out of [0,32]");
+  TGS_CHECK_ARG(n < (1ull << 32) - (uint64_t)SORT_TILE * (RADIX_MAX_SEGS + 1),
+                "segmented_sort: n too large");
+  TGS_CHECK_ARG(n_segments >= 1 && n_segments <= RADIX_MAX_SEGS,
+                "segmented_sort: n_segments must be in [1, 64]");
+  TGS_CHECK_ARG(seg_offsets[0] == 0 && seg_offsets[n_segments] == n,
+                "segmented_sort: segments must cover [0, n)");
+  RadixSegs sg{};
+  sg.n = n_segments;
+  uint32_t tiles = 0;
+  for (uint32_t s = 0; s < n_segments; ++s) {
+    TGS_CHECK_ARG(seg_offsets[s + 1] >= seg_offsets[s], "segmented_sort: offsets decrease");
+    sg.key_off[s] = seg_offsets[s];
+    sg.tile_base[s] = tiles;
+    tiles += (uint32_t)sort_tiles(seg_offsets[s + 1] - seg_offsets[s]);
   }
-  *selector = sel;
-  return TGS_OK;
+  sg.key_off[n_segments] = (uint32_t)n;
+  sg.tile_base[n_segments] = tiles;
+  if (workspace_bytes < tgs_segmented_sort_workspace_size(n, n_segments)) {
+    tgs_set_error("segmented_sort: workspace %zu < %zu", workspace_bytes,
+                  tgs_segmented_sort_workspace_size(n, n_segments));
+    return TGS_ERR_WORKSPACE;
+  }
+  if (tiles == 0) return TGS_OK;
+  if (value_bytes == 4)
+    return radix_passes<uint32_t, uint32_t>(keys, (uint32_t*)vals, keys_alt, (uint32_t*)vals_alt,
+                                            sg, begin_bit, end_bit, workspace, selector, stream);
+  return radix_passes<uint32_t, uint64_t>(keys, (uint64_t*)vals, keys_alt, (uint64_t*)vals_alt, sg,
+                                          begin_bit, end_bit, workspace, selector, stream);
 }

@@ -21,6 +21,9 @@ enum {
 // Per-thread last-error text for the host wrapper (reentrant across threads).
 void tgs_set_error(const char* fmt, ...);
 
+// Word fill kernel launch (abi_common.hip), used instead of hipMemsetAsync.
+extern "C" int tgs_fill_u32(void* ptr, uint64_t n_words, uint32_t value, hipStream_t stream);
+
 #define TGS_CHECK_ARG(cond, ...)          \
   do {                                    \
     if (!(cond)) {                        \

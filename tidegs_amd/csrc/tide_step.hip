@@ -260,11 +260,22 @@ __device__ __forceinline__ uint32_t entry_camera(const int32_t* s_off, uint32_t 
   return c;
 }
 
+// Tile rectangle [x0,x1) x [y0,y1) of one entry, 8 bits per bound (grids up
+// to 255 x 255 tiles), carried through the depth sort beside the entry index.
+__device__ __forceinline__ uint32_t pack_rect(uint32_t x0, uint32_t x1, uint32_t y0, uint32_t y1) {
+  return x0 | (x1 << 8) | (y0 << 16) | (y1 << 24);
+}
+__device__ __forceinline__ uint32_t rect_tiles(uint32_t rc) {
+  const uint32_t x0 = rc & 255u, x1 = (rc >> 8) & 255u, y0 = (rc >> 16) & 255u, y1 = rc >> 24;
+  return (x1 > x0 ? x1 - x0 : 0u) * (y1 > y0 ? y1 - y0 : 0u);
+}
+
 __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
     uint32_t n_entries, const int32_t* __restrict__ entries, const int32_t* __restrict__ cam_offsets,
     TideCams tc, const float* __restrict__ params, int W, int H, float eps2d, float near_plane,
     float far_plane, float radius_clip, int sh_degree, uint32_t tile_size, uint32_t tw,
-    uint32_t th, float4* __restrict__ splats, int32_t* __restrict__ tiles_per_entry) {
+    uint32_t th, float4* __restrict__ splats, uint32_t* __restrict__ depth_keys,
+    uint64_t* __restrict__ entry_rects) {
   __shared__ CamLDS s_cam;
   __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
   load_cams_lds(tc, s_cam);
@@ -283,7 +294,8 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
     out[0] = make_float4(0.f, 0.f, 0.f, 0.f);
     out[1] = make_float4(0.f, 0.f, 0.f, 0.f);
     out[2] = make_float4(0.f, 0.f, 0.f, 0.f);
-    tiles_per_entry[e] = 0;
+    depth_keys[e] = 0xffffffffu;
+    entry_rects[e] = (uint64_t)e;  // empty rectangle
     return;
   }
   float col[3];
@@ -305,163 +317,90 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
   };
   const uint32_t x0 = clampu(floorf(txx - trd), tw), x1 = clampu(ceilf(txx + trd), tw);
   const uint32_t y0 = clampu(floorf(tyy - trd), th), y1 = clampu(ceilf(tyy + trd), th);
-  tiles_per_entry[e] = (int32_t)((x1 > x0 ? x1 - x0 : 0u) * (y1 > y0 ? y1 - y0 : 0u));
+  // depth > near_plane > 0, so the float bits order like the depths
+  depth_keys[e] = __float_as_uint(r.depth);
+  entry_rects[e] = ((uint64_t)pack_rect(x0, x1, y0, y1) << 32) | e;
+}
+
+// ---------------------------------------------------------------------------
+// Intersections in the reference's order (isect_tiles.cu:73-98,189-227).
+// The reference emits camera|tile|depth keys in (camera, entry) order and
+// stable-sorts them, i.e. orders intersections by (camera, tile, depth bits,
+// entry).  Here entries are first stable-sorted by depth bits within each
+// camera (carrying their tile rectangles), intersections are emitted in that
+// order with camera|tile keys, and a stable sort of the tile bits within each
+// camera gives the same total order.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) tide_isect_count_kernel(
+    uint32_t n_entries, const uint64_t* __restrict__ rects, int32_t* __restrict__ tiles) {
+  const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n_entries) return;
+  tiles[j] = (int32_t)rect_tiles((uint32_t)(rects[j] >> 32));
+}
+
+__global__ void tide_isect_segments_kernel(uint32_t C, const int32_t* __restrict__ cam_offsets,
+                                           const int64_t* __restrict__ cum_tiles,
+                                           uint32_t* __restrict__ seg) {
+  const uint32_t c = threadIdx.x;
+  if (c > C) return;
+  const int32_t o = cam_offsets[c];
+  seg[c] = o > 0 ? (uint32_t)cum_tiles[o - 1] : 0u;
 }
 
 __global__ void __launch_bounds__(256) tide_isect_emit_kernel(
     uint32_t n_entries, const int32_t* __restrict__ cam_offsets, uint32_t C,
-    const float4* __restrict__ splats, const int64_t* __restrict__ cum_tiles, uint32_t tile_size,
-    uint32_t tw, uint32_t th, uint32_t tile_n_bits, int64_t* __restrict__ isect_ids,
-    int32_t* __restrict__ flatten_ids) {
+    const uint64_t* __restrict__ rects, const int64_t* __restrict__ cum_tiles, uint32_t tw,
+    uint32_t tile_n_bits, uint32_t* __restrict__ keys, int32_t* __restrict__ flatten_ids) {
   __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
   if (threadIdx.x <= C) s_off[threadIdx.x] = cam_offsets[threadIdx.x];
   __syncthreads();
-  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n_entries) return;
-  const float4 r0 = splats[(uint64_t)e * 3 + 0];
-  const float4 r1 = splats[(uint64_t)e * 3 + 1];
-  const int32_t radius = (int32_t)r1.w;
-  if (radius <= 0) return;
-  const uint32_t c = entry_camera(s_off, C, e);
-  const float ts = (float)tile_size;
-  const float trd = (float)radius / ts;
-  const float txx = r0.x / ts, tyy = r0.y / ts;
-  auto clampu = [](float v, uint32_t lim) -> uint32_t {
-    if (!(v > 0.f)) return 0u;
-    if (v >= (float)lim) return lim;
-    return (uint32_t)v;
-  };
-  const uint32_t x0 = clampu(floorf(txx - trd), tw), x1 = clampu(ceilf(txx + trd), tw);
-  const uint32_t y0 = clampu(floorf(tyy - trd), th), y1 = clampu(ceilf(tyy + trd), th);
-  const int64_t cam_enc = (int64_t)c << (32 + tile_n_bits);
-  const int64_t depth_enc = (int64_t)__float_as_int(r0.w);
-  int64_t cur = e == 0 ? 0 : cum_tiles[e - 1];
+  const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n_entries) return;
+  const uint64_t v = rects[j];
+  const uint32_t rc = (uint32_t)(v >> 32);
+  const uint32_t x0 = rc & 255u, x1 = (rc >> 8) & 255u, y0 = (rc >> 16) & 255u, y1 = rc >> 24;
+  const uint32_t cam_enc = entry_camera(s_off, C, j) << tile_n_bits;
+  const int32_t e = (int32_t)(uint32_t)v;
+  uint32_t cur = j == 0 ? 0u : (uint32_t)cum_tiles[j - 1];
   for (uint32_t y = y0; y < y1; ++y)
     for (uint32_t x = x0; x < x1; ++x) {
-      isect_ids[cur] = cam_enc | (((int64_t)y * tw + x) << 32) | depth_enc;
-      flatten_ids[cur] = (int32_t)e;
+      keys[cur] = cam_enc | (y * tw + x);
+      flatten_ids[cur] = e;
       ++cur;
     }
 }
 
-// ---------------------------------------------------------------------------
-// Per-bucket depth sort (fused path).  The order the reference's radix sort
-// gives camera|tile|depth keys (isect_tiles.cu:189-227) is ascending in
-// (camera*n_tiles + tile, depth bits, entry), a total order.  The fused step
-// radix-sorts only the camera|tile bits (stable, so each bucket keeps entry
-// order) and this kernel then sorts every bucket by (depth bits, entry) in
-// LDS -- bitonic up to 8192 intersections, merge-path passes beyond.
-// ---------------------------------------------------------------------------
-#define BSORT_THREADS 512
-#define BSORT_CAP 8192  // 64 KB of 64-bit keys in LDS
-
-__device__ __forceinline__ void bitonic_lds(uint64_t* s, uint32_t p) {
-  for (uint32_t k = 2; k <= p; k <<= 1) {
-    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-      for (uint32_t h = threadIdx.x; h < (p >> 1); h += blockDim.x) {
-        const uint32_t lo = 2 * h - (h & (j - 1));  // h = q j + r -> 2 q j + r
-        const uint32_t hi = lo + j;
-        const bool asc = (lo & k) == 0;
-        const uint64_t a = s[lo], b = s[hi];
-        if ((a > b) == asc) {
-          s[lo] = b;
-          s[hi] = a;
-        }
-      }
-      __syncthreads();
-    }
+// isect_offset_encode (isect_tiles.cu:234-301) over camera|tile keys.
+__global__ void __launch_bounds__(256) tide_offset_encode_kernel(
+    uint32_t n_isects, const uint32_t* __restrict__ keys, uint32_t C, uint32_t n_tiles,
+    uint32_t tile_n_bits, int32_t* __restrict__ offsets) {
+  const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n_isects) return;
+  const uint32_t total = C * n_tiles;
+  auto bucket = [&](uint32_t k) {
+    const uint32_t b = (k >> tile_n_bits) * n_tiles + (k & ((1u << tile_n_bits) - 1u));
+    return b < total ? b : total - 1;
+  };
+  const uint32_t cur = bucket(keys[idx]);
+  if (idx == 0)
+    for (uint32_t i = 0; i <= cur; ++i) offsets[i] = 0;
+  if (idx == n_isects - 1)
+    for (uint32_t i = cur + 1; i < total; ++i) offsets[i] = (int32_t)n_isects;
+  if (idx > 0) {
+    const uint32_t prev = bucket(keys[idx - 1]);
+    for (uint32_t i = prev + 1; i <= cur; ++i) offsets[i] = (int32_t)idx;
   }
 }
 
-// Merge two sorted runs src[lo,mid) and src[mid,hi) into dst[lo,hi) with the
-// whole block (merge-path partition per thread, then a sequential merge).
-__device__ __forceinline__ void block_merge(const uint64_t* __restrict__ src,
-                                            uint64_t* __restrict__ dst, uint32_t lo,
-                                            uint32_t mid, uint32_t hi) {
-  const uint32_t n = hi - lo;
-  const uint32_t step = (n + blockDim.x - 1) / blockDim.x;
-  const uint32_t d0 = min(n, threadIdx.x * step);
-  const uint32_t d1 = min(n, d0 + step);
-  if (d0 >= d1) return;
-  const uint32_t na = mid - lo, nb = hi - mid;
-  // first output diagonal d0: find i (taken from A) with i + j = d0
-  auto split = [&](uint32_t d) {
-    uint32_t a_lo = d > nb ? d - nb : 0u, a_hi = min(d, na);
-    while (a_lo < a_hi) {
-      const uint32_t i = (a_lo + a_hi) >> 1;
-      // take i from A, d - i from B: valid if A[i] > B[d-i-1]
-      if (src[lo + i] <= src[mid + d - i - 1])
-        a_lo = i + 1;
-      else
-        a_hi = i;
-    }
-    return a_lo;
-  };
-  uint32_t i = split(d0), j = d0 - i;
-  for (uint32_t d = d0; d < d1; ++d) {
-    const bool take_a = j >= nb || (i < na && src[lo + i] <= src[mid + j]);
-    dst[lo + d] = take_a ? src[lo + i++] : src[mid + j++];
-  }
-}
-
-__global__ void __launch_bounds__(BSORT_THREADS) tide_bucket_sort_kernel(
-    uint32_t n_buckets, uint32_t n_isects, const int32_t* __restrict__ bucket_offsets,
-    int64_t* __restrict__ keys, int32_t* __restrict__ fids, uint64_t* __restrict__ tmp,
-    uint64_t* __restrict__ scratch) {
-  __shared__ uint64_t s[BSORT_CAP];
-  const uint32_t b = blockIdx.x;
-  const uint32_t start = (uint32_t)bucket_offsets[b];
-  const uint32_t end = b + 1 < n_buckets ? (uint32_t)bucket_offsets[b + 1] : n_isects;
-  const uint32_t n = end - start;
-  if (n <= 1) return;
-  // composite (depth bits, entry): ascending order = the reference's order
-  // inside one (camera, tile) bucket
-  auto comp = [&](uint32_t k) {
-    return ((uint64_t)(uint32_t)keys[start + k] << 32) | (uint32_t)fids[start + k];
-  };
-  const uint64_t* result;
-  if (n <= BSORT_CAP) {
-    uint32_t p = 2;
-    while (p < n) p <<= 1;
-    for (uint32_t k = threadIdx.x; k < p; k += blockDim.x) s[k] = k < n ? comp(k) : ~0ull;
-    __syncthreads();
-    bitonic_lds(s, p);
-    result = s;
-  } else {
-    for (uint32_t r0 = 0; r0 < n; r0 += BSORT_CAP) {
-      const uint32_t m = min(BSORT_CAP, n - r0);
-      for (uint32_t k = threadIdx.x; k < BSORT_CAP; k += blockDim.x)
-        s[k] = k < m ? comp(r0 + k) : ~0ull;
-      __syncthreads();
-      bitonic_lds(s, BSORT_CAP);
-      for (uint32_t k = threadIdx.x; k < m; k += blockDim.x) tmp[start + r0 + k] = s[k];
-      __syncthreads();
-    }
-    uint64_t* src = tmp + start;
-    uint64_t* dst = scratch + start;
-    for (uint32_t w = BSORT_CAP; w < n; w <<= 1) {
-      for (uint32_t lo = 0; lo < n; lo += 2 * w) {
-        const uint32_t mid = min(n, lo + w), hi = min(n, lo + 2 * w);
-        if (mid >= hi) {
-          for (uint32_t k = lo + threadIdx.x; k < hi; k += blockDim.x) dst[k] = src[k];
-        } else {
-          block_merge(src, dst, lo, mid, hi);
-        }
-        __syncthreads();
-      }
-      uint64_t* t = src;
-      src = dst;
-      dst = t;
-    }
-    result = src;
-  }
-  __syncthreads();
-  const int64_t hi_bits = keys[start] & ~(int64_t)0xffffffffll;
-  for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) {
-    const uint64_t v = result[k];
-    fids[start + k] = (int32_t)(uint32_t)(v & 0xffffffffu);
-    keys[start + k] = hi_bits | (int64_t)(int32_t)(uint32_t)(v >> 32);
-  }
+// The reference's int64 intersection ids (camera|tile << 32 | depth bits,
+// isect_tiles.cu:89-94), rebuilt from the sorted keys for inspection.
+__global__ void __launch_bounds__(256) tide_isect_ids_kernel(
+    uint32_t n_isects, const uint32_t* __restrict__ keys, const int32_t* __restrict__ fids,
+    const float4* __restrict__ splats, int64_t* __restrict__ isect_ids) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_isects) return;
+  const float depth = splats[(uint64_t)fids[i] * 3].w;
+  isect_ids[i] = ((int64_t)keys[i] << 32) | (int64_t)__float_as_int(depth);
 }
 
 // ---------------------------------------------------------------------------
@@ -608,50 +547,86 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries,
                                     int32_t W, int32_t H, float eps2d, float near_plane,
                                     float far_plane, float radius_clip, int32_t sh_degree,
                                     uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
-                                    float* splats, int32_t* tiles_per_entry, hipStream_t stream) {
+                                    float* splats, uint32_t* depth_keys, uint64_t* entry_rects,
+                                    hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;
   if (n_entries == 0) return TGS_OK;
   TGS_CHECK_ARG(entries && cam_offsets && params && viewmats && Ks && campos && splats &&
-                    tiles_per_entry,
+                    depth_keys && entry_rects,
                 "tide_project_fwd: null");
+  TGS_CHECK_ARG(tile_width >= 1 && tile_width <= 255 && tile_height >= 1 && tile_height <= 255,
+                "tide step: tile grid must be at most 255 x 255 tiles (got %u x %u)", tile_width,
+                tile_height);
   TGS_CHECK_ARG(sh_degree >= 0 && sh_degree <= 3, "tide step: sh_degree must be in [0,3]");
   TGS_CHECK_ARG(((uintptr_t)splats & 15) == 0, "tide_project_fwd: splats must be 16-byte aligned");
   TideCams tc{viewmats, Ks, campos, C};
   hipLaunchKernelGGL(tide_project_fwd_kernel, dim3(tgs_blocks(n_entries, 256)), dim3(256), 0,
                      stream, n_entries, entries, cam_offsets, tc, params, W, H, eps2d, near_plane,
                      far_plane, radius_clip, sh_degree, tile_size, tile_width, tile_height,
-                     (float4*)splats, tiles_per_entry);
+                     (float4*)splats, depth_keys, entry_rects);
   TGS_RETURN_LAUNCH("tgs_tide_project_fwd");
 }
 
 
-extern "C" int tgs_tide_bucket_sort(uint32_t n_buckets, uint32_t n_isects,
-                                    const int32_t* bucket_offsets, int64_t* isect_ids,
-                                    int32_t* flatten_ids, uint64_t* tmp, uint64_t* scratch,
-                                    hipStream_t stream) {
-  if (n_buckets == 0 || n_isects == 0) return TGS_OK;
-  TGS_CHECK_ARG(bucket_offsets && isect_ids && flatten_ids && tmp && scratch,
-                "tide_bucket_sort: null");
-  hipLaunchKernelGGL(tide_bucket_sort_kernel, dim3(n_buckets), dim3(BSORT_THREADS), 0, stream,
-                     n_buckets, n_isects, bucket_offsets, isect_ids, flatten_ids, tmp, scratch);
-  TGS_RETURN_LAUNCH("tgs_tide_bucket_sort");
+extern "C" int tgs_tide_isect_count(uint32_t n_entries, const uint64_t* entry_rects,
+                                    int32_t* tiles, hipStream_t stream) {
+  if (n_entries == 0) return TGS_OK;
+  TGS_CHECK_ARG(entry_rects && tiles, "tide_isect_count: null");
+  hipLaunchKernelGGL(tide_isect_count_kernel, dim3(tgs_blocks(n_entries, 256)), dim3(256), 0,
+                     stream, n_entries, entry_rects, tiles);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_count");
+}
+
+extern "C" int tgs_tide_isect_segments(uint32_t C, const int32_t* cam_offsets,
+                                       const int64_t* cum_tiles, uint32_t* seg,
+                                       hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  TGS_CHECK_ARG(cam_offsets && cum_tiles && seg, "tide_isect_segments: null");
+  hipLaunchKernelGGL(tide_isect_segments_kernel, dim3(1), dim3(64), 0, stream, C, cam_offsets,
+                     cum_tiles, seg);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_segments");
 }
 
 extern "C" int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,
-                                   const float* splats, const int64_t* cum_tiles,
-                                   uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
-                                   uint32_t tile_n_bits, int64_t* isect_ids, int32_t* flatten_ids,
-                                   hipStream_t stream) {
+                                   const uint64_t* entry_rects, const int64_t* cum_tiles,
+                                   uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
+                                   int32_t* flatten_ids, hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;
   if (n_entries == 0) return TGS_OK;
-  TGS_CHECK_ARG(cam_offsets && splats && cum_tiles && isect_ids && flatten_ids,
+  TGS_CHECK_ARG(cam_offsets && entry_rects && cum_tiles && keys && flatten_ids,
                 "tide_isect_emit: null");
+  TGS_CHECK_ARG(tile_n_bits <= 16, "tide_isect_emit: tile_n_bits must be <= 16");
   hipLaunchKernelGGL(tide_isect_emit_kernel, dim3(tgs_blocks(n_entries, 256)), dim3(256), 0,
-                     stream, n_entries, cam_offsets, C, (const float4*)splats, cum_tiles,
-                     tile_size, tile_width, tile_height, tile_n_bits, isect_ids, flatten_ids);
+                     stream, n_entries, cam_offsets, C, entry_rects, cum_tiles, tile_width,
+                     tile_n_bits, keys, flatten_ids);
   TGS_RETURN_LAUNCH("tgs_tide_isect_emit");
+}
+
+extern "C" int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, uint32_t C,
+                                      uint32_t tile_width, uint32_t tile_height,
+                                      uint32_t tile_n_bits, int32_t* offsets,
+                                      hipStream_t stream) {
+  const uint64_t total = (uint64_t)C * tile_width * tile_height;
+  if (total == 0) return TGS_OK;
+  TGS_CHECK_ARG(offsets && (n_isects == 0 || keys), "tide_offset_encode: null");
+  TGS_CHECK_ARG(total < (1ull << 31), "tide_offset_encode: too many buckets");
+  if (n_isects == 0) return tgs_fill_u32(offsets, total, 0u, stream);
+  hipLaunchKernelGGL(tide_offset_encode_kernel, dim3(tgs_blocks(n_isects, 256)), dim3(256), 0,
+                     stream, n_isects, keys, C, tile_width * tile_height, tile_n_bits, offsets);
+  TGS_RETURN_LAUNCH("tgs_tide_offset_encode");
+}
+
+extern "C" int tgs_tide_isect_ids(uint32_t n_isects, const uint32_t* keys,
+                                  const int32_t* flatten_ids, const float* splats,
+                                  int64_t* isect_ids, hipStream_t stream) {
+  if (n_isects == 0) return TGS_OK;
+  TGS_CHECK_ARG(keys && flatten_ids && splats && isect_ids, "tide_isect_ids: null");
+  hipLaunchKernelGGL(tide_isect_ids_kernel, dim3(tgs_blocks(n_isects, 256)), dim3(256), 0, stream,
+                     n_isects, keys, flatten_ids, (const float4*)splats, isect_ids);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_ids");
 }
 
 extern "C" int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const float* backgrounds,

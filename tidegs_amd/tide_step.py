@@ -84,6 +84,11 @@ class StepStats:
                 for c in range(s.shape[0])]
 
 
+def _segments(offsets) -> "ctypes.Array":
+    """Host uint32 array of segment offsets for tgs_segmented_sort_pairs_u32."""
+    return (ctypes.c_uint32 * len(offsets))(*[int(o) for o in offsets])
+
+
 class TideStep:
     """Fused TideGS batch step (forward, backward, resident optimizer) on one GPU."""
 
@@ -213,53 +218,74 @@ class TideStep:
         V = tot[C + 1]
         T = tot[C]
 
-        # 2. projection + SH colours for every (camera, visible row), tiles per entry
+        # 2. projection + SH colours for every (camera, visible row); depth keys
+        #    and tile rectangles for the intersection sort
         n_buckets = C * th * tw
         splats = self._buf("splats", max(V, 1) * 12, torch.float32)
-        tiles = self._buf("tiles", max(V, 1), torch.int32)
+        dkeys = self._buf("depth_keys", max(V, 1), torch.int32)
+        rects = self._buf("entry_rects", max(V, 1), torch.int64)
         self._begin("project_fwd")
         N.call("tgs_tide_project_fwd", V, N.ptr(entries), N.ptr(cam_offsets), C, N.ptr(P),
                N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H, self.eps2d, self.near, self.far,
-               0.0, self.sh_degree, self.TILE, tw, th, N.ptr(splats), N.ptr(tiles), s)
+               0.0, self.sh_degree, self.TILE, tw, th, N.ptr(splats), N.ptr(dkeys), N.ptr(rects),
+               s)
         self._end()
 
-        # 3. intersections: emit camera|tile|depth keys in entry order, stable radix
-        #    sort of the camera|tile bits only, bucket offsets, per-bucket depth sort
+        # 3. intersections in the reference's (camera, tile, depth, entry) order:
+        #    depth sort of the entries per camera, count + scan, emission in depth
+        #    order, stable sort of the tile bits per camera, bucket offsets
+        cam_segs = _segments([sum(tot[:c]) for c in range(C + 1)])
+        dkeys2 = self._buf("depth_keys2", max(V, 1), torch.int32)
+        rects2 = self._buf("entry_rects2", max(V, 1), torch.int64)
+        tiles = self._buf("tiles", max(V, 1), torch.int32)
         cum = self._buf("cum_tiles", max(V, 1), torch.int64)
+        seg = self._buf("isect_segs", C + 1, torch.int32)
         ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(max(V, 1)), torch.uint8)
         self._begin("isect_scan")
         if V:
+            sel = ctypes.c_int(0)
+            dws = self._buf("sort_ws", lib.tgs_segmented_sort_workspace_size(V, C), torch.uint8)
+            N.call("tgs_segmented_sort_pairs_u32", N.ptr(dkeys), N.ptr(rects), N.ptr(dkeys2),
+                   N.ptr(rects2), 8, V, C, cam_segs, 0, 32, N.ptr(dws), dws.numel(),
+                   ctypes.byref(sel), s)
+            if sel.value:
+                rects = rects2
+            N.call("tgs_tide_isect_count", V, N.ptr(rects), N.ptr(tiles), s)
             N.call("tgs_inclusive_scan_i32_i64", N.ptr(tiles), N.ptr(cum), V, N.ptr(ws),
                    ws.numel(), s)
+            N.call("tgs_tide_isect_segments", C, N.ptr(cam_offsets), N.ptr(cum), N.ptr(seg), s)
+        else:
+            seg.zero_()
         self._end()
-        n_isects = int(cum[V - 1].item()) if V else 0  # sync 2
+        isect_segs = seg.cpu().tolist()  # sync 2
+        n_isects = isect_segs[C]
         tile_bits = (tw * th).bit_length()
-        cam_bits = C.bit_length()
         cap = max(n_isects, 1)
-        keys = self._buf("keys", cap, torch.int64)
-        keys2 = self._buf("keys2", cap, torch.int64)
+        keys = self._buf("keys", cap, torch.int32)
+        keys2 = self._buf("keys2", cap, torch.int32)
         fids = self._buf("fids", cap, torch.int32)
         fids2 = self._buf("fids2", cap, torch.int32)
-        tmp = self._buf("bsort_tmp", cap, torch.int64)
-        scratch = self._buf("bsort_scratch", cap, torch.int64)
-        rws = self._buf("radix_ws", max(1, lib.tgs_radix_sort_workspace_size(cap)), torch.uint8)
         offsets = self._buf("offsets", n_buckets, torch.int32)
         self._begin("isect_sort")
         if n_isects:
-            N.call("tgs_tide_isect_emit", V, N.ptr(cam_offsets), C, N.ptr(splats), N.ptr(cum),
-                   self.TILE, tw, th, tile_bits, N.ptr(keys), N.ptr(fids), s)
+            N.call("tgs_tide_isect_emit", V, N.ptr(cam_offsets), C, N.ptr(rects), N.ptr(cum), tw,
+                   tile_bits, N.ptr(keys), N.ptr(fids), s)
             sel = ctypes.c_int(0)
-            N.call("tgs_radix_sort_pairs", N.ptr(keys), N.ptr(fids), N.ptr(keys2), N.ptr(fids2),
-                   n_isects, 32, 32 + tile_bits + cam_bits, N.ptr(rws), rws.numel(),
-                   ctypes.byref(sel), s)
+            tws = self._buf("sort_ws2", lib.tgs_segmented_sort_workspace_size(n_isects, C),
+                            torch.uint8)
+            N.call("tgs_segmented_sort_pairs_u32", N.ptr(keys), N.ptr(fids), N.ptr(keys2),
+                   N.ptr(fids2), 4, n_isects, C, _segments(isect_segs), 0, tile_bits,
+                   N.ptr(tws), tws.numel(), ctypes.byref(sel), s)
             if sel.value:
-                keys, keys2, fids, fids2 = keys2, keys, fids2, fids
-        N.call("tgs_isect_offset_encode", n_isects, N.ptr(keys), C, tw, th, N.ptr(offsets), s)
-        if n_isects:
-            N.call("tgs_tide_bucket_sort", n_buckets, n_isects, N.ptr(offsets), N.ptr(keys),
-                   N.ptr(fids), N.ptr(tmp), N.ptr(scratch), s)
+                keys, fids = keys2, fids2
+        N.call("tgs_tide_offset_encode", n_isects, N.ptr(keys), C, tw, th, tile_bits,
+               N.ptr(offsets), s)
         self._end()
-        isect_ids = keys if self.keep_isect_ids else None
+        isect_ids = None
+        if self.keep_isect_ids:
+            isect_ids = self._buf("isect_ids", cap, torch.int64)
+            N.call("tgs_tide_isect_ids", n_isects, N.ptr(keys), N.ptr(fids), N.ptr(splats),
+                   N.ptr(isect_ids), s)
 
         # 4. rasterize, loss, loss backward, rasterize backward
         images = self._buf("images", C * H * W * 3, torch.float32)
