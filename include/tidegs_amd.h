@@ -127,10 +127,6 @@ int tgs_isect_offset_encode(uint64_t n_isects, const int64_t* isect_ids, uint32_
 /* ---- rasterization ---------------------------------------------------- */
 /* Channel counts with an instantiated kernel; returns their number. */
 int tgs_rasterize_supported_channels(int32_t* out, int32_t cap);
-/* Self-test of the backward's wavefront reduce-scatter (no reference
- * counterpart): in [10*64] (value k of lane l at k*64+l) -> out [128]:
- * out[l] = total held by lane l's quad, out[64+l] = the value index it holds. */
-int tgs_selftest_wave_reduce(const float* in, float* out, tgs_stream_t stream);
 /* Replaces rasterize_to_pixels_fwd_tensor (rasterize_to_pixels_fwd.cu:236-284).
  * means2d/conics/colors/opacities [C,N,*] or packed [nnz,*]; backgrounds
  * [C,channels] or null; render_colors [C,H,W,ch], render_alphas [C,H,W,1],

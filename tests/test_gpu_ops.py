@@ -330,23 +330,3 @@ def test_tide_loss_kernels(gpu):
     loss = 0.8 * sums[0] / n + 0.2 * (1 - sums[1] / n)
     assert abs(loss - loss_ref) < 1e-6
     assert rel_l2(to_np(v).transpose(2, 0, 1), grad_ref) < 1e-5
-
-
-def test_wave_reduce_scatter_lane_layout(gpu):
-    """The backward's permlane/DPP reduce-scatter leaves value k's wave total in
-    every lane of the quad that rs_value_of_quad maps to k."""
-    announce("wave reduce-scatter selftest")
-    from tidegs_amd import _native as N
-
-    g = torch.Generator().manual_seed(0)
-    x = torch.randn((10, 64), generator=g)
-    out = torch.empty(128, device=gpu)
-    N.call("tgs_selftest_wave_reduce", N.ptr(x.to(gpu).contiguous()), N.ptr(out), N.stream_handle())
-    out = to_np(out)
-    totals, which = out[:64], out[64:].astype(int)
-    q = np.arange(64) // 4
-    expect_map = 8 * (q & 1) + 4 * ((q >> 1) & 1) + np.array([0, 2, 1, 3])[q >> 2]
-    np.testing.assert_array_equal(which, expect_map)
-    sums = np.concatenate([x.sum(1).numpy(), np.zeros(6)])
-    np.testing.assert_allclose(totals, sums[which], rtol=1e-5, atol=1e-5)
-    assert sorted(set(which.tolist())) == list(range(16))

@@ -62,7 +62,6 @@ SIGNATURES = {
     ),
     "tgs_isect_offset_encode": (ctypes.c_int, [U64, P, U32, U32, U32, P, P]),
     "tgs_rasterize_supported_channels": (ctypes.c_int, [ctypes.POINTER(I32), I32]),
-    "tgs_selftest_wave_reduce": (ctypes.c_int, [P, P, P]),
     "tgs_rasterize_to_pixels_fwd": (
         ctypes.c_int,
         [U32, U32, P, P, P, P, P, U32, U32, U32, U32, U32, P, P, U32, P, P, P, P],

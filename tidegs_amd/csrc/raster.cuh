@@ -19,13 +19,12 @@
 //     (0.5 d^T Q d <= ln(255 opacity)), which is exact: pixels outside it
 //     are skipped by the reference too.
 // Every wavefront then compacts the batch to the Gaussians whose box meets its
-// own 16x4 pixel strip and loops only over those.
-// In the backward each wavefront reduces a Gaussian's nine gradient values
-// with a reduce-scatter (v_permlane32_swap / v_permlane16_swap / DPP) that
-// leaves each value's total in one quad, then one atomic instruction adds all
-// nine (lane 4q handles value of quad q).  The pixel-side products are
-// accumulated as moments (sum v_sigma dx, dx^2, ...) and turned into mean2d /
-// conic / opacity gradients once per Gaussian after the reduction.
+// own 16x4 pixel strip; each lane marks which of those reach its pixel and
+// walks only its own marks (lane-compacted iteration, below).
+// In the backward each lane leaves its per-(Gaussian, pixel) terms in LDS and
+// owner lanes sum them per Gaussian as moments (sum v_sigma dx, dx^2, ...),
+// turned into mean2d / conic / opacity gradients once per Gaussian and
+// wavefront.
 //
 // The splat source/gradient sink are policies so the same kernels serve
 // gsplat's SoA tensors (drop-in op) and the packed 48-byte splat records of the
@@ -124,7 +123,7 @@ struct RasterGeom {
 // ---------------------------------------------------------------------------
 struct StagedGeo {
   float4 g0;   // x, y, A = -0.5 log2e a, B = -log2e b
-  float4 g1;   // C = -0.5 log2e c, L = log2(opacity), 0, 0
+  float2 g1;   // C = -0.5 log2e c, L = log2(opacity)
   float4 box;  // x_lo, x_hi, y_lo, y_hi of the alpha >= 1/255 ellipse
 };
 
@@ -133,7 +132,7 @@ __device__ __forceinline__ StagedGeo stage_geo(const SplatData<CDIM>& s) {
   StagedGeo o;
   o.g0 = make_float4(s.x, s.y, -0.5f * RS_LOG2E * s.a, -RS_LOG2E * s.b);
   const float L = __builtin_amdgcn_logf(s.op);  // log2; -inf for 0, NaN for < 0
-  o.g1 = make_float4(-0.5f * RS_LOG2E * s.c, s.op > 0.f ? L : -INFINITY, 0.f, 0.f);
+  o.g1 = make_float2(-0.5f * RS_LOG2E * s.c, s.op > 0.f ? L : -INFINITY);
   // alpha >= 1/255 needs sigma <= t = ln(255 op).  On {0.5 d^T Q d <= t} the
   // extents are |dx| <= sqrt(2 t c / det), |dy| <= sqrt(2 t a / det).
   const float t = logf(255.f * s.op);
@@ -151,8 +150,14 @@ __device__ __forceinline__ StagedGeo stage_geo(const SplatData<CDIM>& s) {
   return o;
 }
 
+// Conic (a, b, c) and 1/opacity recovered from the staged coefficients.
+__device__ __forceinline__ float4 staged_conic_rop(const float4& g0, const float2& g1) {
+  constexpr float k = 1.f / RS_LOG2E;
+  return make_float4(-2.f * k * g0.z, -k * g0.w, -2.f * k * g1.x, __builtin_amdgcn_exp2f(-g1.y));
+}
+
 // power = log2(op) - sigma log2(e) at offset (dx, dy) = mean - pixel.
-__device__ __forceinline__ float raster_power(const float4& g0, const float4& g1, float dx,
+__device__ __forceinline__ float raster_power(const float4& g0, const float2& g1, float dx,
                                               float dy) {
   const float t2 = fmaf(g0.z, dx, g0.w * dy);
   const float s = fmaf(g1.x * dy, dy, g1.y);
@@ -185,65 +190,43 @@ __device__ __forceinline__ int build_wave_list(const float4* s_box, uint8_t* s_l
 }
 
 // ---------------------------------------------------------------------------
-// Reduce-scatter of up to 10 wave values (gfx950).  Afterwards every lane of
-// quad q (lanes 4q..4q+3) holds the wave total of value rs_value_of_quad(q);
-// values >= the caller's count are zero padding.
-//   step A  v_permlane32_swap: value 2j in lanes 0-31, 2j+1 in lanes 32-63
-//   step B  v_permlane16_swap: each 16-lane row holds one value
-//   step C  select + DPP row_ror:8: each 8-lane half row holds one value
-//   step D  select + DPP row_half_mirror: each quad holds one value
-//   step E  DPP quad_perm adds
+// Lane-compacted iteration.  A wavefront's list holds every Gaussian whose box
+// meets its strip, but a small Gaussian covers only a few of its 64 pixels,
+// so looping over the list with one pixel per lane leaves most lanes idle.
+// Instead every lane first records, in a bitmask over list positions, which
+// Gaussians actually reach its pixel (the cheap alpha test), and then walks
+// only its own set bits in list order: the wavefront iterates
+// max_lane(|own set|) times instead of |list| times.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int rs_value_of_quad(int q) {
-  const int rmap = (0x3120 >> (4 * (q >> 2))) & 0xF;  // [0,2,1,3][q>>2]
-  return 8 * (q & 1) + 4 * ((q >> 1) & 1) + rmap;
-}
+template <int BLOCK>
+struct LaneMask {
+  static constexpr int WORDS = BLOCK / 32;
+  uint32_t w[WORDS];
+};
 
-__device__ __forceinline__ void rs_swap32(float a, float b, float& x, float& y) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
-                                                  false);
-  x = __uint_as_float(r[0]);
-  y = __uint_as_float(r[1]);
-}
-
-__device__ __forceinline__ void rs_swap16(float a, float b, float& x, float& y) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false,
-                                                  false);
-  x = __uint_as_float(r[0]);
-  y = __uint_as_float(r[1]);
-}
-
-__device__ __forceinline__ float rs_reduce10(const float v[10]) {
-  const int lane = threadIdx.x & 63;
-  float R[5];
+// Bit li of the mask is set iff list entry li passes the pixel test of
+// rasterize_to_pixels_{fwd,bwd}.cu (sigma >= 0 and alpha >= 1/255) and, in
+// the backward, its batch index is not behind the pixel's last contributor.
+template <int BLOCK>
+__device__ __forceinline__ void lane_masks(LaneMask<BLOCK>& m, const uint8_t* list, int n_list,
+                                           const float4* s_g0, const float2* s_g1, float px,
+                                           float py, bool active, int t_min) {
 #pragma unroll
-  for (int j = 0; j < 5; ++j) {
-    float x, y;
-    rs_swap32(v[2 * j], v[2 * j + 1], x, y);
-    R[j] = x + y;
+  for (int W = 0; W < LaneMask<BLOCK>::WORDS; ++W) {
+    uint32_t mw = 0;
+    if (W * 32 < n_list) {
+      const int lim = min(32, n_list - W * 32);
+      for (int bb = 0; bb < lim; ++bb) {
+        const int t = list[W * 32 + bb];
+        const float4 g0 = s_g0[t];
+        const float2 g1 = s_g1[t];
+        const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
+        const bool ok = t >= t_min && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
+        mw |= (ok ? 1u : 0u) << bb;
+      }
+    }
+    m.w[W] = active ? mw : 0u;
   }
-  float S[3];
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    float x, y;
-    rs_swap16(R[2 * j], (2 * j + 1 < 5) ? R[2 * j + 1] : 0.f, x, y);
-    S[j] = x + y;
-  }
-  const int l16 = lane & 15;
-  auto split8 = [&](float x, float y) {
-    const float keep = l16 < 8 ? x : y;
-    const float send = l16 < 8 ? y : x;
-    return keep + tgs_dpp<0x128>(send);  // row_ror:8
-  };
-  const float U0 = split8(S[0], S[1]);
-  const float U1 = split8(S[2], 0.f);
-  const int l8 = lane & 7;
-  const float keep = l8 < 4 ? U0 : U1;
-  const float send = l8 < 4 ? U1 : U0;
-  float V = keep + tgs_dpp<0x141>(send);  // row_half_mirror
-  V += tgs_dpp<0xB1>(V);                  // quad_perm [1,0,3,2]
-  V += tgs_dpp<0x4E>(V);                  // quad_perm [2,3,0,1]
-  return V;
 }
 
 // ---------------------------------------------------------------------------
@@ -259,7 +242,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
   constexpr int WAVES = BLOCK / 64;
   constexpr int ROWS = 64 / TILE;  // pixel rows per wavefront
   __shared__ float4 s_g0[BLOCK];
-  __shared__ float4 s_g1[BLOCK];
+  __shared__ float2 s_g1[BLOCK];
   __shared__ float4 s_box[BLOCK];
   __shared__ float s_col[BLOCK][CDIM];
   __shared__ uint8_t s_list[WAVES][BLOCK];
@@ -311,27 +294,35 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
     int n_list = 0;
     if (tgs_ballot(!done))
       n_list = build_wave_list<BLOCK>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1);
-    for (int li = 0; li < n_list; ++li) {
-      if (!tgs_ballot(!done)) break;
-      const int t = s_list[wave][li];
-      if (done) continue;
-      const float4 g0 = s_g0[t];
-      const float4 g1 = s_g1[t];
-      const float dx = g0.x - px, dy = g0.y - py;
-      const float power = raster_power(g0, g1, dx, dy);
-      // sigma < 0  <=>  power > log2(op);  alpha < 1/255  <=>  power < log2(1/255)
-      if (power > g1.y || power < RS_LOG2_MIN_ALPHA) continue;
-      const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
-      const float next_T = T * (1.f - alpha);
-      if (next_T <= 1e-4f) {
-        done = true;
-        continue;
-      }
-      const float vis = alpha * T;
+    LaneMask<BLOCK> m;
+    lane_masks<BLOCK>(m, s_list[wave], n_list, s_g0, s_g1, px, py, !done, 0);
 #pragma unroll
-      for (int k = 0; k < CDIM; ++k) pix[k] += s_col[t][k] * vis;
-      cur_idx = (uint32_t)(batch_start + t);
-      T = next_T;
+    for (int W = 0; W < LaneMask<BLOCK>::WORDS; ++W) {
+      if (W * 32 >= n_list) break;
+      uint32_t mw = m.w[W];
+      while (true) {
+        const bool act = mw != 0u && !done;
+        if (!tgs_ballot(act)) break;
+        if (act) {
+          const int bit = __builtin_ctz(mw);
+          mw &= mw - 1u;
+          const int t = s_list[wave][W * 32 + bit];
+          const float4 g0 = s_g0[t];
+          const float2 g1 = s_g1[t];
+          const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
+          const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
+          const float next_T = T * (1.f - alpha);
+          if (next_T <= 1e-4f) {
+            done = true;
+          } else {
+            const float vis = alpha * T;
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k) pix[k] += s_col[t][k] * vis;
+            cur_idx = (uint32_t)(batch_start + t);
+            T = next_T;
+          }
+        }
+      }
     }
   }
   if (inside) {
@@ -346,8 +337,25 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Backward
+// Backward.  Per batch and wavefront the list is processed in chunks of CH
+// entries, all within the wavefront (no block barriers):
+//   1. test     lane bit e = list entry e reaches my pixel; the wavefront's
+//               ballot of it is the entry's pixel mask (LDS);
+//   2. pixels   each lane walks its own entries back to front (T, colour
+//               buffer) and leaves (alpha T, v_sigma) for (entry, pixel) in a
+//               per-wavefront LDS pair buffer;
+//   3. owners   lanes 4e..4e+3 own entry e, each summing the moments
+//               (v_sigma dx, dy, dx^2, dx dy, dy^2, v_sigma, colour terms,
+//               |v_mean2d|) over the pixels of its 16-lane quarter from the
+//               pair buffer; a quad DPP sum gives the entry's totals, turned
+//               into mean2d / conic / opacity gradients with its constants;
+//   4. flush    (entry, value) pairs in value-fastest order, so each atomic
+//               instruction covers a few Gaussians' contiguous records.
+// Every pixel-side term is one product per (entry, pixel), so no lane ever
+// adds to a shared location: no LDS atomics and no per-entry wave reduction.
 // ---------------------------------------------------------------------------
+#define RB_CH 8  // list entries per chunk (8 owner lanes each)
+
 template <int CDIM, int TILE, class Src, class Sink>
 __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
     RasterGeom G, Src src, Sink sink, const float* __restrict__ backgrounds,
@@ -359,14 +367,21 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   constexpr int ROWS = 64 / TILE;
   // value slots: 0,1 mean2d; 2..4 conic; 5.. color; 5+CDIM opacity; then |mean2d|
   constexpr int NV = 6 + CDIM;
-  constexpr bool FAST = NV <= 10;  // reduce-scatter path
+  constexpr int NA = NV + 2;
   __shared__ float4 s_g0[BLOCK];
-  __shared__ float4 s_g1[BLOCK];
-  __shared__ float4 s_box[BLOCK];
-  __shared__ float4 s_abc[BLOCK];  // a, b, c, 1/op
+  __shared__ float2 s_g1[BLOCK];
   __shared__ float s_col[BLOCK][CDIM];
+  __shared__ float s_vrc[BLOCK][CDIM];  // dL/dcolor of each pixel
   __shared__ int32_t s_id[BLOCK];
   __shared__ uint8_t s_list[WAVES][BLOCK];
+  // boxes are dead once the lists are built (barrier), then the pair buffer
+  // (alpha T, v_sigma) per (entry, lane) takes their place
+  __shared__ union {
+    float4 box[BLOCK];
+    float2 pair[WAVES][RB_CH][64];
+  } s_u;
+  __shared__ uint64_t s_emask[WAVES][RB_CH];
+  __shared__ float s_stage[WAVES][RB_CH * NA];
 
   const uint32_t cam = blockIdx.x;
   const uint32_t ty = blockIdx.y, tx = blockIdx.z;
@@ -398,6 +413,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   for (int k = 0; k < CDIM; ++k) {
     buffer[k] = 0.f;
     v_rc[k] = v_render_colors[pid * CDIM + k];
+    s_vrc[tr][k] = v_rc[k];
   }
   const float v_ra = v_render_alphas ? v_render_alphas[pid] : 0.f;
   float bg_dot = 0.f;
@@ -410,6 +426,10 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   const int32_t bin_final = inside ? last_ids[pid] : 0;
   const int32_t wave_bin_final = tgs_wave_max_i32(bin_final);
   const bool absg = sink.absgrad();
+  const int nval = absg ? NA : NV;
+
+  // owner role: entry oe of a chunk, pixel lanes [8 oq, 8 oq + 8) of the wave
+  const int oe = lane >> 3, oq = lane & 7;
 
   for (int32_t b = 0; b < n_batches; ++b) {
     __syncthreads();
@@ -423,8 +443,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
       const StagedGeo sg = stage_geo<CDIM>(s);
       s_g0[tr] = sg.g0;
       s_g1[tr] = sg.g1;
-      s_box[tr] = sg.box;
-      s_abc[tr] = make_float4(s.a, s.b, s.c, 1.f / s.op);
+      s_u.box[tr] = sg.box;
       s_id[tr] = g;
 #pragma unroll
       for (int k = 0; k < CDIM; ++k) s_col[tr][k] = s.col[k];
@@ -433,94 +452,125 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
     // entries with global index > wave_bin_final contribute to no pixel of this wave
     const int j_lo = max(0, batch_end - wave_bin_final);
     const int n_list =
-        build_wave_list<BLOCK>(s_box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1);
-    for (int li = 0; li < n_list; ++li) {
-      const int t = s_list[wave][li];
-      bool valid = inside && (batch_end - t <= bin_final);
-      const float4 g0 = s_g0[t];
-      const float4 g1 = s_g1[t];
-      const float dx = g0.x - px, dy = g0.y - py;
-      const float power = raster_power(g0, g1, dx, dy);
-      if (power > g1.y || power < RS_LOG2_MIN_ALPHA) valid = false;
-      if (!tgs_ballot(valid)) continue;
-
-      // per-pixel values: 0 sum v_sigma dx, 1 sum v_sigma dy, 2 v_sigma dx^2,
-      // 3 v_sigma dx dy, 4 v_sigma dy^2, 5.. color, 5+CDIM v_sigma, then |v_xy|
-      float vals[NV + 2];
+        build_wave_list<BLOCK>(s_u.box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1);
+    __syncthreads();
+    // batch entry t is global index batch_end - t: at or before bin_final
+    const int t_min = batch_end - bin_final;
+    for (int c0 = 0; c0 < n_list; c0 += RB_CH) {
+      const int cn = min(RB_CH, n_list - c0);
+      const uint8_t* list = s_list[wave] + c0;
+      // 1. test
+      uint32_t m = 0;
+      for (int e = 0; e < cn; ++e) {
+        const int t = list[e];
+        const float4 g0 = s_g0[t];
+        const float2 g1 = s_g1[t];
+        const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
+        const bool ok =
+            inside && t >= t_min && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
+        m |= (ok ? 1u : 0u) << e;
+        const uint64_t em = tgs_ballot(ok);
+        if (lane == 0) s_emask[wave][e] = em;
+      }
+      // 2. per-pixel walk, back to front
+      while (tgs_ballot(m != 0u)) {
+        if (m != 0u) {
+          const int e = __builtin_ctz(m);
+          m &= m - 1u;
+          const int t = list[e];
+          const float4 g0 = s_g0[t];
+          const float2 g1 = s_g1[t];
+          const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
+          const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
+          const float alpha = fminf(0.999f, raw);
+          const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
+          T *= ra;
+          const float fac = alpha * T;
+          float v_alpha = ra * tf_term;
 #pragma unroll
-      for (int k = 0; k < NV + 2; ++k) vals[k] = 0.f;
-      if (valid) {
-        const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
-        const float alpha = fminf(0.999f, raw);
-        const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
-        T *= ra;
-        const float fac = alpha * T;
-        float v_alpha = ra * tf_term;
-#pragma unroll
-        for (int k = 0; k < CDIM; ++k) {
-          const float ck = s_col[t][k];
-          vals[5 + k] = fac * v_rc[k];
-          v_alpha += (ck * T - buffer[k] * ra) * v_rc[k];
-          buffer[k] += ck * fac;
+          for (int k = 0; k < CDIM; ++k) {
+            const float ck = s_col[t][k];
+            v_alpha += (ck * T - buffer[k] * ra) * v_rc[k];
+            buffer[k] += ck * fac;
+          }
+          // reference: the sigma terms only where alpha was not clamped
+          const float v_sigma = raw <= 0.999f ? -raw * v_alpha : 0.f;
+          s_u.pair[wave][e][lane] = make_float2(fac, v_sigma);
         }
-        if (raw <= 0.999f) {
-          const float v_sigma = -raw * v_alpha;
-          const float mx = v_sigma * dx, my = v_sigma * dy;
-          vals[0] = mx;
-          vals[1] = my;
-          vals[2] = mx * dx;
-          vals[3] = mx * dy;
-          vals[4] = my * dy;
-          vals[5 + CDIM] = v_sigma;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // 3. owners
+      float acc[NA];
+#pragma unroll
+      for (int k = 0; k < NA; ++k) acc[k] = 0.f;
+      float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (oe < cn) {
+        const int t = list[oe];
+        const float4 g0 = s_g0[t];
+        q = staged_conic_rop(g0, s_g1[t]);
+        uint32_t pm = (uint32_t)(s_emask[wave][oe] >> (8 * oq)) & 0xffu;
+        while (pm != 0u) {
+          const int pl = 8 * oq + __builtin_ctz(pm);
+          pm &= pm - 1u;
+          const float2 pr = s_u.pair[wave][oe][pl];
+          const int pix = wave * 64 + pl;
+          const float dx = g0.x - ((float)(tx * TILE + pix % TILE) + 0.5f);
+          const float dy = g0.y - ((float)(ty * TILE + pix / TILE) + 0.5f);
+          const float vs = pr.y;
+          const float mx = vs * dx, my = vs * dy;
+          acc[0] += mx;
+          acc[1] += my;
+          acc[2] += mx * dx;
+          acc[3] += mx * dy;
+          acc[4] += my * dy;
+#pragma unroll
+          for (int k = 0; k < CDIM; ++k) acc[5 + k] += pr.x * s_vrc[pix][k];
+          acc[5 + CDIM] += vs;
           if (absg) {
-            const float4 q = s_abc[t];
-            vals[NV] = fabsf(v_sigma * (q.x * dx + q.y * dy));
-            vals[NV + 1] = fabsf(v_sigma * (q.y * dx + q.z * dy));
+            acc[NV] += fabsf(q.x * mx + q.y * my);
+            acc[NV + 1] += fabsf(q.y * mx + q.z * my);
           }
         }
       }
-      // wave totals -> final gradient values of this Gaussian
-      const float4 q = s_abc[t];
-      const int32_t gid = s_id[t];
-      if (FAST && !absg) {
-        float v10[10];
 #pragma unroll
-        for (int k = 0; k < 10; ++k) v10[k] = k < NV ? vals[k] : 0.f;
-        const float tot = rs_reduce10(v10);
-        // lane 4q owns value k = rs_value_of_quad(q); the moments are turned into
-        // gradients with the Gaussian's constants (mean2d: Q m; conic: halves).
-        const int quad = lane >> 2;
-        const int k = rs_value_of_quad(quad);
-        // neighbour totals needed for mean2d: fetch via readlane of the quads
-        // holding values 0 and 1 (quads 0 and 8).
-        const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 0));
-        const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 32));
-        float out = tot;
-        if (k == 0) out = q.x * m0 + q.y * m1;
-        else if (k == 1) out = q.y * m0 + q.z * m1;
-        else if (k == 2 || k == 4) out = 0.5f * tot;
-        else if (k == 5 + CDIM) out = -tot * q.w;
-        if ((lane & 3) == 0 && k < NV) tgs_atomic_add(sink.ptr(gid, k), out);
-      } else {
-        float mine = 0.f;
-        float tot[NV + 2];
-#pragma unroll
-        for (int k = 0; k < NV + 2; ++k) tot[k] = 0.f;
-#pragma unroll
-        for (int k = 0; k < NV + 2; ++k)
-          if (k < NV || absg) tot[k] = tgs_wave_sum(vals[k]);
-        const int nv = absg ? NV + 2 : NV;
-#pragma unroll
-        for (int k = 0; k < NV + 2; ++k) {
-          float o = tot[k];
-          if (k == 0) o = q.x * tot[0] + q.y * tot[1];
-          else if (k == 1) o = q.y * tot[0] + q.z * tot[1];
-          else if (k == 2 || k == 4) o = 0.5f * tot[k];
-          else if (k == 5 + CDIM) o = -tot[k] * q.w;
-          if (lane == k) mine = o;
+      for (int k = 0; k < NA; ++k) {
+        if (k < NV || absg) {
+          acc[k] += tgs_dpp<0xB1>(acc[k]);   // quad_perm [1,0,3,2]
+          acc[k] += tgs_dpp<0x4E>(acc[k]);   // quad_perm [2,3,0,1]
+          acc[k] += tgs_dpp<0x141>(acc[k]);  // row_half_mirror: 8-lane sum
         }
-        if (lane < nv) tgs_atomic_add(sink.ptr(gid, lane), mine);
       }
+      if (oq == 0 && oe < cn) {
+        float* st = s_stage[wave] + oe * nval;
+        st[0] = q.x * acc[0] + q.y * acc[1];
+        st[1] = q.y * acc[0] + q.z * acc[1];
+        st[2] = 0.5f * acc[2];
+        st[3] = acc[3];
+        st[4] = 0.5f * acc[4];
+#pragma unroll
+        for (int k = 0; k < CDIM; ++k) st[5 + k] = acc[5 + k];
+        st[5 + CDIM] = -acc[5 + CDIM] * q.w;
+        if (absg) {
+          st[NV] = acc[NV];
+          st[NV + 1] = acc[NV + 1];
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // 4. flush
+      const int total = cn * nval;
+      for (int L = lane; L < total; L += 64) {
+        const int e = absg ? L / NA : L / NV;
+        const int k = L - e * nval;
+        const float v = s_stage[wave][L];
+        if (v != 0.f) tgs_atomic_add(sink.ptr(s_id[list[e]], k), v);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 }

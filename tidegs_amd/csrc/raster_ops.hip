@@ -67,24 +67,6 @@ static int dispatch_bwd(uint32_t tile_size, const RasterGeom& G, const float* me
 
 #define TGS_CHANNEL_CASES(X) X(1) X(2) X(3) X(4) X(8) X(16) X(32)
 
-// Lane-layout self-test of the backward's reduce-scatter: one wavefront,
-// in[k*64 + lane] is value k of lane; out[lane] = the total its quad holds.
-__global__ void __launch_bounds__(64) selftest_reduce_kernel(const float* __restrict__ in,
-                                                             float* __restrict__ out) {
-  const int lane = threadIdx.x;
-  float v[10];
-#pragma unroll
-  for (int k = 0; k < 10; ++k) v[k] = in[k * 64 + lane];
-  out[lane] = rs_reduce10(v);
-  out[64 + lane] = (float)rs_value_of_quad(lane >> 2);
-}
-
-extern "C" int tgs_selftest_wave_reduce(const float* in, float* out, hipStream_t stream) {
-  TGS_CHECK_ARG(in && out, "selftest_wave_reduce: null pointer");
-  hipLaunchKernelGGL(selftest_reduce_kernel, dim3(1), dim3(64), 0, stream, in, out);
-  TGS_RETURN_LAUNCH("tgs_selftest_wave_reduce");
-}
-
 extern "C" int tgs_rasterize_supported_channels(int32_t* out, int32_t cap) {
   const int32_t list[] = {1, 2, 3, 4, 8, 16, 32};
   const int32_t n = (int32_t)(sizeof(list) / sizeof(list[0]));
