@@ -29,7 +29,7 @@ METRIC = "ms/train-step (fwd+bwd+Adam) at 4M Gaussians, 16×1080p; bwd HBM GB/s"
 # Algorithmic bytes per unit of work (fp32), see DESIGN.md "Measurement".
 BYTES = {
     "visibility": lambda s: 40 * s["N"] + 4 * s["N"],
-    "project_fwd": lambda s: s["V"] * (4 + 44 + 4 + 48 + 4) + s["Vvis"] * 192,
+    "project_fwd": lambda s: s["T"] * (4 + 4 + 4 + 236) + s["V"] * (4 + 48 + 4 + 8),
     "raster_fwd": lambda s: s["C"] * s["P"] * 20 + s["I"] * 52,
     "raster_bwd": lambda s: s["C"] * s["P"] * 20 + s["I"] * 52 + s["V"] * 36,
     "project_bwd": lambda s: s["T"] * (4 + 4 + 236 + 236) + s["V"] * (4 + 16 + 36),

@@ -239,13 +239,16 @@ int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* masks, const u
                      int32_t* visit_base, int32_t* visits, uint32_t* totals,
                      int32_t* cam_offsets, tgs_stream_t stream);
 /* Projection + SH colour + activations per entry (engine.py:458-512 with
- * base_gaussian_model.py:35-50) -> splats [V,12] (3 x float4:
- * {x,y,opacity,depth},{a,b,c,radius},{r,g,b,0}), depth_keys [V] (float bits
- * of the depth; 0xffffffff when culled) and entry_rects [V] (tile rectangle
- * x0|x1<<8|y0<<16|y1<<24 in the high word, entry index in the low word;
- * isect_tiles.cu:55-70).  Tile grid at most 255 x 255. */
-int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries, const int32_t* cam_offsets,
-                         uint32_t C, const float* params, const float* viewmats, const float* Ks,
+ * base_gaussian_model.py:35-50), one thread per touched row over its visits
+ * (entries of the cameras in its visibility mask, camera order) ->
+ * splats [V,12] (3 x float4: {x,y,opacity,depth},{a,b,c,radius},{r,g,b,0}),
+ * depth_keys [V] (float bits of the depth; 0xffffffff when culled) and
+ * entry_rects [V] (tile rectangle x0|x1<<8|y0<<16|y1<<24 in the high word,
+ * entry index in the low word; isect_tiles.cu:55-70).  Tile grid at most
+ * 255 x 255. */
+int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched, const int32_t* visit_base,
+                         const int32_t* visits, const uint32_t* masks, uint32_t C,
+                         const float* params, const float* viewmats, const float* Ks,
                          const float* campos, int32_t W, int32_t H, float eps2d, float near_plane,
                          float far_plane, float radius_clip, int32_t sh_degree,
                          uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,

@@ -373,7 +373,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   __shared__ float s_col[BLOCK][CDIM];
   __shared__ float s_vrc[BLOCK][CDIM];  // dL/dcolor of each pixel
   __shared__ int32_t s_id[BLOCK];
-  __shared__ uint8_t s_list[WAVES][BLOCK];
+  __shared__ __align__(16) uint8_t s_list[WAVES][BLOCK];
   // boxes are dead once the lists are built (barrier), then the pair buffer
   // (alpha T, v_sigma) per (entry, lane) takes their place
   __shared__ union {
@@ -458,16 +458,19 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
     const int t_min = batch_end - bin_final;
     for (int c0 = 0; c0 < n_list; c0 += RB_CH) {
       const int cn = min(RB_CH, n_list - c0);
-      const uint8_t* list = s_list[wave] + c0;
+      // the chunk's batch indices, eight bytes of the (8-byte aligned) list
+      const uint64_t l8 = *reinterpret_cast<const uint64_t*>(s_list[wave] + c0);
+      auto entry = [&](int e) { return (int)((l8 >> (8 * e)) & (uint64_t)(BLOCK - 1)); };
       // 1. test
       uint32_t m = 0;
-      for (int e = 0; e < cn; ++e) {
-        const int t = list[e];
+#pragma unroll
+      for (int e = 0; e < RB_CH; ++e) {
+        const int t = entry(e);
         const float4 g0 = s_g0[t];
         const float2 g1 = s_g1[t];
         const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
-        const bool ok =
-            inside && t >= t_min && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
+        const bool ok = e < cn && inside && t >= t_min &&
+                        !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
         m |= (ok ? 1u : 0u) << e;
         const uint64_t em = tgs_ballot(ok);
         if (lane == 0) s_emask[wave][e] = em;
@@ -477,7 +480,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
         if (m != 0u) {
           const int e = __builtin_ctz(m);
           m &= m - 1u;
-          const int t = list[e];
+          const int t = entry(e);
           const float4 g0 = s_g0[t];
           const float2 g1 = s_g1[t];
           const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
@@ -507,7 +510,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
       for (int k = 0; k < NA; ++k) acc[k] = 0.f;
       float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
       if (oe < cn) {
-        const int t = list[oe];
+        const int t = entry(oe);
         const float4 g0 = s_g0[t];
         q = staged_conic_rop(g0, s_g1[t]);
         uint32_t pm = (uint32_t)(s_emask[wave][oe] >> (8 * oq)) & 0xffu;
@@ -566,7 +569,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
         const int e = absg ? L / NA : L / NV;
         const int k = L - e * nval;
         const float v = s_stage[wave][L];
-        if (v != 0.f) tgs_atomic_add(sink.ptr(s_id[list[e]], k), v);
+        if (v != 0.f) tgs_atomic_add(sink.ptr(s_id[entry(e)], k), v);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();

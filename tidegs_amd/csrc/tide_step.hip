@@ -270,25 +270,16 @@ __device__ __forceinline__ uint32_t rect_tiles(uint32_t rc) {
   return (x1 > x0 ? x1 - x0 : 0u) * (y1 > y0 ? y1 - y0 : 0u);
 }
 
-__global__ void __launch_bounds__(256) tide_project_fwd_kernel(
-    uint32_t n_entries, const int32_t* __restrict__ entries, const int32_t* __restrict__ cam_offsets,
-    TideCams tc, const float* __restrict__ params, int W, int H, float eps2d, float near_plane,
-    float far_plane, float radius_clip, int sh_degree, uint32_t tile_size, uint32_t tw,
-    uint32_t th, float4* __restrict__ splats, uint32_t* __restrict__ depth_keys,
+// Projection + SH colour of one (camera, row) entry e into the packed splat
+// record, its depth key and its tile rectangle.
+__device__ __forceinline__ void project_entry(
+    const float p[3], const m3& Sigma, float opac, const float* sh, const Cam& cam,
+    const float* campos, int W, int H, float eps2d, float near_plane, float far_plane,
+    float radius_clip, int sh_degree, uint32_t tile_size, uint32_t tw, uint32_t th, uint32_t e,
+    float4* __restrict__ splats, uint32_t* __restrict__ depth_keys,
     uint64_t* __restrict__ entry_rects) {
-  __shared__ CamLDS s_cam;
-  __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
-  load_cams_lds(tc, s_cam);
-  if (threadIdx.x <= tc.C) s_off[threadIdx.x] = cam_offsets[threadIdx.x];
-  __syncthreads();
-  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n_entries) return;
-  const uint32_t c = entry_camera(s_off, tc.C, e);
-  const float* row = params + (uint64_t)entries[e] * TIDE_ROW;
-  const float p[3] = {row[0], row[1], row[2]};
-  const m3 Sigma = row_covariance(row);
-  const ProjResult r = project_forward(p, Sigma, s_cam.cam[c], W, H, eps2d, near_plane,
-                                       far_plane, radius_clip);
+  const ProjResult r =
+      project_forward(p, Sigma, cam, W, H, eps2d, near_plane, far_plane, radius_clip);
   float4* out = splats + (uint64_t)e * 3;
   if (r.radius <= 0) {
     out[0] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -299,9 +290,7 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
     return;
   }
   float col[3];
-  sh_eval3(sh_degree, p[0] - s_cam.campos[c][0], p[1] - s_cam.campos[c][1],
-           p[2] - s_cam.campos[c][2], row + 11, col);
-  const float opac = sigmoidf_(row[10]);
+  sh_eval3(sh_degree, p[0] - campos[0], p[1] - campos[1], p[2] - campos[2], sh, col);
   out[0] = make_float4(r.mean2d[0], r.mean2d[1], opac, r.depth);
   out[1] = make_float4(r.conic[0], r.conic[1], r.conic[2], (float)r.radius);
   out[2] = make_float4(fmaxf(col[0] + 0.5f, 0.f), fmaxf(col[1] + 0.5f, 0.f),
@@ -321,6 +310,42 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
   depth_keys[e] = __float_as_uint(r.depth);
   entry_rects[e] = ((uint64_t)pack_rect(x0, x1, y0, y1) << 32) | e;
 }
+
+// One thread per touched row: the row (59 floats) is read once and projected
+// into every camera it is visible in (its visits, in camera order, are the
+// set bits of its visibility mask); SH coefficients stay in registers.
+__global__ void __launch_bounds__(256) tide_project_fwd_kernel(
+    uint32_t n_touched, const int32_t* __restrict__ touched,
+    const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
+    const uint32_t* __restrict__ masks, TideCams tc, const float* __restrict__ params, int W,
+    int H, float eps2d, float near_plane, float far_plane, float radius_clip, int sh_degree,
+    uint32_t tile_size, uint32_t tw, uint32_t th, float4* __restrict__ splats,
+    uint32_t* __restrict__ depth_keys, uint64_t* __restrict__ entry_rects) {
+  __shared__ CamLDS s_cam;
+  load_cams_lds(tc, s_cam);
+  __syncthreads();
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_touched) return;
+  const uint32_t n = (uint32_t)touched[t];
+  const float* row = params + (uint64_t)n * TIDE_ROW;
+  const float p[3] = {row[0], row[1], row[2]};
+  const m3 Sigma = row_covariance(row);
+  const float opac = sigmoidf_(row[10]);
+  float sh[48];
+#pragma unroll
+  for (int k = 0; k < 48; ++k) sh[k] = row[11 + k];
+  uint32_t mask = masks[n];
+  const int32_t* vis = visits + visit_base[t];
+  for (int j = 0; mask != 0u; ++j) {
+    const uint32_t c = (uint32_t)__builtin_ctz(mask);
+    mask &= mask - 1u;
+    const uint32_t e = (uint32_t)vis[j];
+    project_entry(p, Sigma, opac, sh, s_cam.cam[c], s_cam.campos[c], W, H, eps2d, near_plane,
+                  far_plane, radius_clip, sh_degree, tile_size, tw, th, e, splats, depth_keys,
+                  entry_rects);
+  }
+}
+
 
 // ---------------------------------------------------------------------------
 // Intersections in the reference's order (isect_tiles.cu:73-98,189-227).
@@ -541,8 +566,9 @@ extern "C" int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* mas
   TGS_RETURN_LAUNCH("tgs_tide_compact");
 }
 
-extern "C" int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries,
-                                    const int32_t* cam_offsets, uint32_t C, const float* params,
+extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched,
+                                    const int32_t* visit_base, const int32_t* visits,
+                                    const uint32_t* masks, uint32_t C, const float* params,
                                     const float* viewmats, const float* Ks, const float* campos,
                                     int32_t W, int32_t H, float eps2d, float near_plane,
                                     float far_plane, float radius_clip, int32_t sh_degree,
@@ -551,9 +577,9 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries,
                                     hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;
-  if (n_entries == 0) return TGS_OK;
-  TGS_CHECK_ARG(entries && cam_offsets && params && viewmats && Ks && campos && splats &&
-                    depth_keys && entry_rects,
+  if (n_touched == 0) return TGS_OK;
+  TGS_CHECK_ARG(touched && visit_base && visits && masks && params && viewmats && Ks && campos &&
+                    splats && depth_keys && entry_rects,
                 "tide_project_fwd: null");
   TGS_CHECK_ARG(tile_width >= 1 && tile_width <= 255 && tile_height >= 1 && tile_height <= 255,
                 "tide step: tile grid must be at most 255 x 255 tiles (got %u x %u)", tile_width,
@@ -561,10 +587,10 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_entries, const int32_t* entries,
   TGS_CHECK_ARG(sh_degree >= 0 && sh_degree <= 3, "tide step: sh_degree must be in [0,3]");
   TGS_CHECK_ARG(((uintptr_t)splats & 15) == 0, "tide_project_fwd: splats must be 16-byte aligned");
   TideCams tc{viewmats, Ks, campos, C};
-  hipLaunchKernelGGL(tide_project_fwd_kernel, dim3(tgs_blocks(n_entries, 256)), dim3(256), 0,
-                     stream, n_entries, entries, cam_offsets, tc, params, W, H, eps2d, near_plane,
-                     far_plane, radius_clip, sh_degree, tile_size, tile_width, tile_height,
-                     (float4*)splats, depth_keys, entry_rects);
+  hipLaunchKernelGGL(tide_project_fwd_kernel, dim3(tgs_blocks(n_touched, 256)), dim3(256), 0,
+                     stream, n_touched, touched, visit_base, visits, masks, tc, params, W, H,
+                     eps2d, near_plane, far_plane, radius_clip, sh_degree, tile_size, tile_width,
+                     tile_height, (float4*)splats, depth_keys, entry_rects);
   TGS_RETURN_LAUNCH("tgs_tide_project_fwd");
 }
 

@@ -218,17 +218,17 @@ class TideStep:
         V = tot[C + 1]
         T = tot[C]
 
-        # 2. projection + SH colours for every (camera, visible row); depth keys
-        #    and tile rectangles for the intersection sort
+        # 2. projection + SH colours for every (camera, visible row), one pass over
+        #    the touched rows; depth keys and tile rectangles for the sort
         n_buckets = C * th * tw
         splats = self._buf("splats", max(V, 1) * 12, torch.float32)
         dkeys = self._buf("depth_keys", max(V, 1), torch.int32)
         rects = self._buf("entry_rects", max(V, 1), torch.int64)
         self._begin("project_fwd")
-        N.call("tgs_tide_project_fwd", V, N.ptr(entries), N.ptr(cam_offsets), C, N.ptr(P),
-               N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H, self.eps2d, self.near, self.far,
-               0.0, self.sh_degree, self.TILE, tw, th, N.ptr(splats), N.ptr(dkeys), N.ptr(rects),
-               s)
+        N.call("tgs_tide_project_fwd", T, N.ptr(touched), N.ptr(visit_base), N.ptr(visits),
+               N.ptr(masks), C, N.ptr(P), N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H,
+               self.eps2d, self.near, self.far, 0.0, self.sh_degree, self.TILE, tw, th,
+               N.ptr(splats), N.ptr(dkeys), N.ptr(rects), s)
         self._end()
 
         # 3. intersections in the reference's (camera, tile, depth, entry) order:
