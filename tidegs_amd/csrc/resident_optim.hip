@@ -13,9 +13,10 @@
 //
 // The reference issues one Triton launch per component (6 per step) plus host
 // searchsorted/index_select.  Here a single launch covers all 59 columns: one
-// wavefront owns one touched row at a time, lane l handles column l (59 of 64
-// lanes busy), and the row -> (slot, state row) lookup is a wave-uniform binary
-// search that runs on the scalar unit.  The column -> (component tensor,
+// wavefront walks a contiguous range of touched rows, four rows in flight,
+// lane l handles column l (59 of 64 lanes busy), and the row -> (slot, state
+// row) lookup is a wave-uniform binary search on the scalar unit that runs
+// only when the (sorted) rows cross into another resident block.  The column -> (component tensor,
 // column) map is fixed per lane, so the same kernel serves six split component
 // tensors or one unified [N,59] table.
 //
@@ -81,6 +82,32 @@ __device__ __forceinline__ int64_t layout_search(const OptimLayout& L, int64_t r
   return lo;
 }
 
+// The resident block holding the current rows: [start, end) -> slot.  Touched
+// rows arrive sorted, so a wavefront walking a contiguous range of them
+// searches the layout only when it crosses into another block.
+struct BlockCache {
+  int64_t start = 0, end = 0, slot = 0;  // empty until the first lookup
+  bool ok = false;
+  __device__ __forceinline__ bool lookup(const OptimLayout& L, int64_t row) {
+    if (row >= start && row < end) return true;
+    const int64_t pos = layout_search(L, row);
+    ok = false;
+    start = end = 0;
+    if (pos < L.n) {
+      const int64_t s = L.starts[pos], e = L.ends[pos];
+      if (row >= s && row < e && row - s < L.block_size) {
+        start = s;
+        end = e;
+        slot = L.slots[pos];
+        ok = true;
+      }
+    }
+    return ok;
+  }
+};
+
+#define OPT_UNROLL 4
+
 template <typename IdxT, bool SOPHIA>
 __global__ void __launch_bounds__(256) resident_optim_kernel(
     int64_t n_rows, const IdxT* __restrict__ local_rows, OptimLayout L,
@@ -113,44 +140,68 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
   const float one_m_b1 = 1.0f - beta1;
   const float one_m_b2 = 1.0f - beta2;
 
-  for (int64_t t = wave; t < n_rows; t += n_waves) {
-    const int64_t row = (int64_t)local_rows[t];
-    const int64_t pos = layout_search(L, row);
-    bool ok = pos < L.n;
-    int64_t in_block = 0, slot = 0;
-    if (ok) {
-      in_block = row - L.starts[pos];
-      slot = L.slots[pos];
-      ok = in_block >= 0 && in_block < L.block_size && row < L.ends[pos];
+  // a contiguous range of touched rows per wavefront, OPT_UNROLL rows in flight
+  const int64_t per = (n_rows + n_waves - 1) / n_waves;
+  const int64_t t0 = wave * per;
+  const int64_t t1 = t0 + per < n_rows ? t0 + per : n_rows;
+  BlockCache bc;
+  for (int64_t t = t0; t < t1; t += OPT_UNROLL) {
+    int64_t poff[OPT_UNROLL], soff[OPT_UNROLL];
+    float scale[OPT_UNROLL], dscale[OPT_UNROLL];
+    bool live[OPT_UNROLL];
+#pragma unroll
+    for (int u = 0; u < OPT_UNROLL; ++u) {
+      live[u] = false;
+      poff[u] = soff[u] = 0;
+      scale[u] = dscale[u] = 1.f;
+      if (t + u < t1) {
+        const int64_t row = (int64_t)local_rows[t + u];
+        if (bc.lookup(L, row)) {
+          live[u] = active;
+          poff[u] = row * pstride + col;
+          soff[u] = (bc.slot * L.block_size + (row - bc.start)) * sstride + col;
+          if (!SOPHIA) {
+            scale[u] = lr / bias1[bc.slot];  // same rounding as (lr / bias1) * m
+            dscale[u] = denom_scale[bc.slot];
+          }
+        } else if (lane == 0) {
+          // A touched row outside every resident block: the host checks this
+          // flag and raises (the reference raises on a missing slot, :275-279).
+          atomicOr(error_flag, 1);
+        }
+      }
     }
-    if (!ok) {
-      // A touched row outside every resident block: the host checks this flag
-      // and raises (the reference raises on a missing slot, :275-279).
-      if (lane == 0) atomicOr(error_flag, 1);
-      continue;
+    float g[OPT_UNROLL], mm[OPT_UNROLL], vv[OPT_UNROLL], p[OPT_UNROLL];
+#pragma unroll
+    for (int u = 0; u < OPT_UNROLL; ++u) {
+      if (live[u]) {
+        g[u] = grad[(t + u) * gstride + col];
+        mm[u] = m[soff[u]];
+        vv[u] = v[soff[u]];
+        p[u] = param[poff[u]];
+      }
     }
-    if (!active) continue;
-    const int64_t state_row = slot * L.block_size + in_block;
-    const int64_t poff = row * pstride + col;
-    const int64_t soff = state_row * sstride + col;
-    float g = grad[t * gstride + col] / batch_size;
-    float mm = m[soff];
-    float vv = v[soff];
-    float p = param[poff];
-    mm = beta1 * mm + one_m_b1 * g;
-    if (SOPHIA) {
-      if (update_h) vv = beta2 * vv + one_m_b2 * g * g;
-      float r = mm / fmaxf(vv, eps);
-      r = fminf(fmaxf(r, -rho), rho);
-      p -= lr * r;
-    } else {
-      vv = beta2 * vv + one_m_b2 * g * g;
-      const float denom = sqrtf(vv) / denom_scale[slot] + eps;
-      p -= (lr / bias1[slot]) * mm / denom;
+#pragma unroll
+    for (int u = 0; u < OPT_UNROLL; ++u) {
+      if (!live[u]) continue;
+      const float gg = g[u] / batch_size;
+      float m1 = beta1 * mm[u] + one_m_b1 * gg;
+      float v1 = vv[u];
+      float p1 = p[u];
+      if (SOPHIA) {
+        if (update_h) v1 = beta2 * v1 + one_m_b2 * gg * gg;
+        float r = m1 / fmaxf(v1, eps);
+        r = fminf(fmaxf(r, -rho), rho);
+        p1 -= lr * r;
+      } else {
+        v1 = beta2 * v1 + one_m_b2 * gg * gg;
+        const float denom = sqrtf(v1) / dscale[u] + eps;
+        p1 -= scale[u] * m1 / denom;
+      }
+      m[soff[u]] = m1;
+      v[soff[u]] = v1;
+      param[poff[u]] = p1;
     }
-    m[soff] = mm;
-    v[soff] = vv;
-    param[poff] = p;
   }
 }
 
@@ -233,10 +284,12 @@ static int launch_optim(int64_t n_rows, const void* local_rows, int index_is_i64
   if (rc) return rc;
   OptimLayout L{starts, ends, slots, n_layout, block_size};
   const int threads = 256;
-  // ~8 resident waves per SIMD over 256 CUs; rows are strided over waves.
-  int64_t waves_needed = n_rows;
+  // each wavefront takes a contiguous range of >= 16 rows; at most ~8 waves
+  // per SIMD over 256 CUs
+  int64_t waves_needed = (n_rows + 15) / 16;
   int64_t blocks = (waves_needed + 3) / 4;
   if (blocks > 256 * 32) blocks = 256 * 32;
+  if (blocks < 1) blocks = 1;
   if (index_is_i64)
     hipLaunchKernelGGL((resident_optim_kernel<int64_t, SOPHIA>), dim3((unsigned)blocks),
                        dim3(threads), 0, stream, n_rows, (const int64_t*)local_rows, L, bias1,
