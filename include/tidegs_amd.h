@@ -165,17 +165,14 @@ int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, float C1, fl
                        const float* dm_dmu1, const float* dm_dsigma1_sq, const float* dm_dsigma12,
                        float* dL_dimg1, tgs_stream_t stream);
 /* Fused L1 + SSIM training loss of strategies/base_engine.py:464-488 for B
- * rendered images [B,H,W,3] (HWC) against gt [B,3,H,W]:
- * sums[2b] += sum|I_b - gt'_b|, sums[2b+1] += sum SSIM (double[2B],
- * caller-zeroed), gt' = clamp(gt / gt_div, 0, 1); partial maps [B,3,H,W]. */
-int tgs_tide_loss_fwd(int32_t B, int32_t H, int32_t W, const float* images_hwc,
-                      const float* gt_chw, float gt_div, float* dm_dmu1, float* dm_dsigma1_sq,
-                      float* dm_dsigma12, double* sums, tgs_stream_t stream);
-/* dL_b/dI_b (HWC) of L_b = (1-lambda) mean|I_b-gt'_b| + lambda (1 - mean SSIM_b). */
-int tgs_tide_loss_bwd(int32_t B, int32_t H, int32_t W, const float* images_hwc,
-                      const float* gt_chw, float gt_div, float lambda_dssim,
-                      const float* dm_dmu1, const float* dm_dsigma1_sq,
-                      const float* dm_dsigma12, float* v_images_hwc, tgs_stream_t stream);
+ * rendered images [B,H,W,3] (HWC) against gt [B,3,H,W]: forward and
+ * backward in one pass.  sums[2b] += sum|I_b - gt'_b|, sums[2b+1] += sum SSIM
+ * (double[2B], caller-zeroed), gt' = clamp(gt / gt_div, 0, 1);
+ * v_images = dL_b/dI_b (HWC) of
+ * L_b = (1-lambda) mean|I_b-gt'_b| + lambda (1 - mean SSIM_b). */
+int tgs_tide_loss(int32_t B, int32_t H, int32_t W, const float* images_hwc, const float* gt_chw,
+                  float gt_div, float lambda_dssim, double* sums, float* v_images_hwc,
+                  tgs_stream_t stream);
 
 /* ---- resident optimizer ------------------------------------------------ */
 /* Replaces the six _fused_resident_adam_kernel launches of GPUResidentAdam.step

@@ -307,26 +307,25 @@ def test_fused_ssim(gpu):
     assert abs(float(val) - float(rm[:, :, 5:-5, 5:-5].mean())) < 1e-5
 
 
-def test_tide_loss_kernels(gpu):
-    announce("tide loss (L1 + SSIM)")
+@pytest.mark.parametrize("B,H,W", [(1, 70, 130), (2, 37, 21)])
+def test_tide_loss_kernel(gpu, B, H, W):
+    """One-pass L1 + SSIM loss and gradient (tgs_tide_loss) against the oracle
+    restatement of base_engine.py:464-488, per image of the batch."""
+    announce(f"tide loss (L1 + SSIM) B={B} {H}x{W}")
     from tidegs_amd import _native as N
 
-    g = torch.Generator().manual_seed(3)
-    H, W = 70, 130
-    img = torch.rand((H, W, 3), generator=g)
-    gt = torch.rand((3, H, W), generator=g) * 300 - 20
-    d_img, d_gt = img.to(gpu), gt.to(gpu)
-    parts = [torch.empty((3, H, W), device=gpu) for _ in range(3)]
-    sums = torch.zeros(2, dtype=torch.float64, device=gpu)
-    s = N.stream_handle()
-    N.call("tgs_tide_loss_fwd", 1, H, W, N.ptr(d_img), N.ptr(d_gt), 255.0, *[N.ptr(p) for p in parts],
-           N.ptr(sums), s)
-    v = torch.empty((H, W, 3), device=gpu)
-    N.call("tgs_tide_loss_bwd", 1, H, W, N.ptr(d_img), N.ptr(d_gt), 255.0, 0.2,
-           *[N.ptr(p) for p in parts], N.ptr(v), s)
-    loss_ref, grad_ref = S.tide_loss(img.permute(2, 0, 1).numpy(), gt.numpy())
-    n = 3 * H * W
+    g = torch.Generator().manual_seed(3 + B)
+    img = torch.rand((B, H, W, 3), generator=g)
+    gt = torch.rand((B, 3, H, W), generator=g) * 300 - 20
+    d_img, d_gt = img.to(gpu), gt.to(gpu)  # keep the device copies alive
+    sums = torch.zeros(2 * B, dtype=torch.float64, device=gpu)
+    v = torch.empty((B, H, W, 3), device=gpu)
+    N.call("tgs_tide_loss", B, H, W, N.ptr(d_img), N.ptr(d_gt), 255.0, 0.2, N.ptr(sums), N.ptr(v),
+           N.stream_handle())
     sums = to_np(sums)
-    loss = 0.8 * sums[0] / n + 0.2 * (1 - sums[1] / n)
-    assert abs(loss - loss_ref) < 1e-6
-    assert rel_l2(to_np(v).transpose(2, 0, 1), grad_ref) < 1e-5
+    n = 3 * H * W
+    for bi in range(B):
+        loss_ref, grad_ref = S.tide_loss(img[bi].permute(2, 0, 1).numpy(), gt[bi].numpy())
+        loss = 0.8 * sums[2 * bi] / n + 0.2 * (1 - sums[2 * bi + 1] / n)
+        assert abs(loss - loss_ref) < 1e-6
+        assert rel_l2(to_np(v[bi]).transpose(2, 0, 1), grad_ref) < 1e-5

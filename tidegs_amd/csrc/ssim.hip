@@ -245,45 +245,230 @@ extern "C" int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, f
 // Fused-step loss of strategies/base_engine.py:464-488 for a batch of B
 // rendered images: per image b, L_b = (1-lambda) mean|I_b - gt'_b| +
 // lambda (1 - mean SSIM(I_b, gt'_b)), gt' = clamp(gt / gt_div, 0, 1), with
-// I [B,H,W,3] (HWC, as rendered) and gt [B,3,H,W] (CHW).  Forward adds
-// sum|I-gt'| and sum SSIM of image b into sums[2b], sums[2b+1] (double,
-// caller-zeroed) and stores the three partial maps ([B,3,H,W] each).
-extern "C" int tgs_tide_loss_fwd(int32_t B, int32_t H, int32_t W, const float* images_hwc,
-                                 const float* gt_chw, float gt_div, float* dm_dmu1,
-                                 float* dm_dsigma1_sq, float* dm_dsigma12, double* sums,
-                                 hipStream_t stream) {
-  if ((int64_t)B * H * W == 0) return TGS_OK;
-  TGS_CHECK_ARG(images_hwc && gt_chw && dm_dmu1 && dm_dsigma1_sq && dm_dsigma12 && sums,
-                "tide_loss_fwd: null pointer");
-  const int CH = 3;
-  Img a{images_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH, 1.f, 0};
-  Img b{gt_chw, (int64_t)CH * H * W, (int64_t)H * W, W, 1, gt_div, 1};
-  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, B);
-  hipLaunchKernelGGL(ssim_fwd_kernel, grid, dim3(256), 0, stream, B, CH, H, W, 1e-4f, 9e-4f, a, b,
-                     OutImg{nullptr, 0, 0, 0, 0}, nchw_out(dm_dmu1, CH, H, W),
-                     nchw_out(dm_dsigma1_sq, CH, H, W), nchw_out(dm_dsigma12, CH, H, W), sums);
-  TGS_RETURN_LAUNCH("tgs_tide_loss_fwd");
+// I [B,H,W,3] (HWC, as rendered) and gt [B,3,H,W] (CHW).  The loss is fixed,
+// so dL/dSSIM-map is the constant -lambda/N and the whole forward + backward
+// runs in one pass per 16x16 output tile and channel, keeping every
+// intermediate in LDS:
+//   inputs   x, y on the 36x36 region (tile + 2 x 5 halo each side);
+//   stats    mu, sigma over the 26x26 region (separable 11-tap window),
+//            giving SSIM (summed over the tile's own pixels) and
+//            g dm/dmu1, g dm/dsigma1^2, g dm/dsigma12 (zero off the image);
+//   gradient G * (g dm) on the tile: f0 + 2 x f1 + y f2, plus the L1 term.
+// sums[2b] += sum|I-gt'|, sums[2b+1] += sum SSIM (double, caller-zeroed).
+#define TL_D1 (SS_T + 2 * SS_R)  // 26: dm region
+#define TL_D2 (SS_T + 4 * SS_R)  // 36: input region
+
+__global__ void __launch_bounds__(256) tide_loss_kernel(int H, int W,
+                                                        const float* __restrict__ images_hwc,
+                                                        const float* __restrict__ gt_chw,
+                                                        float gt_div, float C1, float C2,
+                                                        float g_ssim, float g_l1,
+                                                        float* __restrict__ v_images_hwc,
+                                                        double* __restrict__ sums) {
+  // phase-aliased LDS: inputs -> dm maps, horizontal sums -> backward sums
+  __shared__ union {
+    struct {
+      float sx[TL_D2][TL_D2 + 1];
+      float sy[TL_D2][TL_D2 + 1];
+    } in;
+    float sdm[3][TL_D1][TL_D1];
+  } su;
+  __shared__ union {
+    float hq[5][TL_D2][TL_D1];
+    float h2[3][TL_D1][SS_T];
+  } sv;
+  __shared__ float red[2][4];
+  auto& sx = su.in.sx;
+  auto& sy = su.in.sy;
+  auto& sdm = su.sdm;
+  auto& hq = sv.hq;
+  auto& h2 = sv.h2;
+  const int bidx = blockIdx.z;
+  const int x0 = blockIdx.x * SS_T, y0 = blockIdx.y * SS_T;
+  const int tid = threadIdx.x;
+  const int ty = tid / SS_T, tx = tid % SS_T;
+  const int px = x0 + tx, py = y0 + ty;
+  const bool inside = px < W && py < H;
+  const int HW = H * W;
+  const float* img = images_hwc + (int64_t)bidx * HW * 3;
+  const float* gtb = gt_chw + (int64_t)bidx * HW * 3;
+  float* vimg = v_images_hwc + (int64_t)bidx * HW * 3;
+  const float rdiv = 1.f / gt_div;
+  float l1_acc = 0.f, m_acc = 0.f;
+
+  for (int c = 0; c < 3; ++c) {
+    const float* gtc = gtb + c * HW;
+    __syncthreads();
+    // inputs on the 36x36 region: thread (ty, tx) fills rows ty+16i, columns tx+16j
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int r = ty + 16 * i;
+      if (r < TL_D2) {
+        const int yy = y0 + r - 2 * SS_R;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const int col = tx + 16 * j;
+          if (col < TL_D2) {
+            const int xx = x0 + col - 2 * SS_R;
+            float u = 0.f, w = 0.f;
+            if (xx >= 0 && yy >= 0 && xx < W && yy < H) {
+              const int pix = yy * W + xx;
+              u = img[pix * 3 + c];
+              // gt / gt_div, rounded like the division: product plus one
+              // residual correction
+              const float g = gtc[pix];
+              float q = g * rdiv;
+              q = fmaf(fmaf(-q, gt_div, g), rdiv, q);
+              w = fminf(fmaxf(q, 0.f), 1.f);
+            }
+            sx[r][col] = u;
+            sy[r][col] = w;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const float x_own = sx[ty + 2 * SS_R][tx + 2 * SS_R];
+    const float y_own = sy[ty + 2 * SS_R][tx + 2 * SS_R];
+    if (inside) l1_acc += fabsf(x_own - y_own);
+    // horizontal pass of x, y, x^2, y^2, xy: 36 rows x 26 columns, each
+    // thread one row segment of 4 outputs from 14 inputs held in registers
+    if (tid < TL_D2 * 7) {
+      const int r = tid / 7, c0 = (tid % 7) * 4;  // segments 0..6 cover 28 >= 26 columns
+      float u[14], w[14];
+#pragma unroll
+      for (int k = 0; k < 14; ++k) {
+        const int cc = min(c0 + k, TL_D2 - 1);
+        u[k] = sx[r][cc];
+        w[k] = sy[r][cc];
+      }
+#pragma unroll
+      for (int o = 0; o < 4; ++o) {
+        float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f, q4 = 0.f;
+#pragma unroll
+        for (int t = 0; t < 11; ++t) {
+          const float uu = u[o + t], ww = w[o + t], k = c_gauss[t];
+          q0 += k * uu;
+          q1 += k * ww;
+          q2 += k * (uu * uu);
+          q3 += k * (ww * ww);
+          q4 += k * (uu * ww);
+        }
+        if (c0 + o < TL_D1) {
+          hq[0][r][c0 + o] = q0;
+          hq[1][r][c0 + o] = q1;
+          hq[2][r][c0 + o] = q2;
+          hq[3][r][c0 + o] = q3;
+          hq[4][r][c0 + o] = q4;
+        }
+      }
+    }
+    __syncthreads();
+    // vertical pass on the 26x26 region: SSIM and the scaled partial maps;
+    // thread (ty, tx) takes rows ty+16i, columns tx+16j (the inputs are dead:
+    // the dm maps take their place)
+#pragma unroll 1
+    for (int i = 0; i < 2; ++i) {
+      const int r = ty + 16 * i;
+#pragma unroll 1
+      for (int j = 0; j < 2; ++j) {
+        const int col = tx + 16 * j;
+        if (r < TL_D1 && col < TL_D1) {
+          float f[5];
+#pragma unroll
+          for (int k = 0; k < 5; ++k) {
+            float acc = 0.f;
+#pragma unroll
+            for (int t = 0; t < 11; ++t) acc += c_gauss[t] * hq[k][r + t][col];
+            f[k] = acc;
+          }
+          const float mu1 = f[0], mu2 = f[1];
+          const float sigma1_sq = f[2] - mu1 * mu1;
+          const float sigma2_sq = f[3] - mu2 * mu2;
+          const float sigma12 = f[4] - mu1 * mu2;
+          const float Cc = 2.f * mu1 * mu2 + C1;
+          const float D = 2.f * sigma12 + C2;
+          const float A = mu1 * mu1 + mu2 * mu2 + C1;
+          const float Bb = sigma1_sq + sigma2_sq + C2;
+          const int yy = y0 + r - SS_R, xx = x0 + col - SS_R;
+          const bool in_img = xx >= 0 && yy >= 0 && xx < W && yy < H;
+          float d0 = 0.f, d1 = 0.f, d2 = 0.f;
+          if (in_img) {
+            // the partial maps of clm_kernels/ssim.cu:240-262 from two reciprocals
+            const float rA = 1.f / A, rB = 1.f / Bb;
+            const float rAB = rA * rB;
+            const float CD = Cc * D;
+            d0 = 2.f * rAB * (mu2 * D - mu2 * Cc + mu1 * CD * (rB - rA));
+            d1 = -CD * rAB * rB;
+            d2 = 2.f * Cc * rAB;
+            if (r >= SS_R && r < SS_R + SS_T && col >= SS_R && col < SS_R + SS_T)
+              m_acc += CD * rAB;
+          }
+          sdm[0][r][col] = g_ssim * d0;
+          sdm[1][r][col] = g_ssim * d1;
+          sdm[2][r][col] = g_ssim * d2;
+        }
+      }
+    }
+    __syncthreads();
+    // backward: horizontal pass (26 rows x 16 columns) ...
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = ty + 16 * i;
+      if (r < TL_D1) {
+        float q0 = 0.f, q1 = 0.f, q2 = 0.f;
+#pragma unroll
+        for (int t = 0; t < 11; ++t) {
+          const float k = c_gauss[t];
+          q0 += k * sdm[0][r][tx + t];
+          q1 += k * sdm[1][r][tx + t];
+          q2 += k * sdm[2][r][tx + t];
+        }
+        h2[0][r][tx] = q0;
+        h2[1][r][tx] = q1;
+        h2[2][r][tx] = q2;
+      }
+    }
+    __syncthreads();
+    // ... then vertical, and the gradient of this pixel
+    if (inside) {
+      float f0 = 0.f, f1 = 0.f, f2 = 0.f;
+#pragma unroll
+      for (int t = 0; t < 11; ++t) {
+        const float k = c_gauss[t];
+        f0 += k * h2[0][ty + t][tx];
+        f1 += k * h2[1][ty + t][tx];
+        f2 += k * h2[2][ty + t][tx];
+      }
+      const float d = x_own - y_own;
+      vimg[(py * W + px) * 3 + c] =
+          f0 + 2.f * x_own * f1 + y_own * f2 + (d > 0.f ? g_l1 : (d < 0.f ? -g_l1 : 0.f));
+    }
+  }
+  const float l1 = tgs_wave_sum(l1_acc);
+  const float ms = tgs_wave_sum(m_acc);
+  const int lane = tid & 63, wave = tid >> 6;
+  if (lane == 0) {
+    red[0][wave] = l1;
+    red[1][wave] = ms;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    atomicAdd(&sums[2 * bidx + 0], (double)(red[0][0] + red[0][1] + red[0][2] + red[0][3]));
+    atomicAdd(&sums[2 * bidx + 1], (double)(red[1][0] + red[1][1] + red[1][2] + red[1][3]));
+  }
 }
 
-// dL_b/dI_b (HWC) for the loss above, for every image of the batch.
-extern "C" int tgs_tide_loss_bwd(int32_t B, int32_t H, int32_t W, const float* images_hwc,
-                                 const float* gt_chw, float gt_div, float lambda_dssim,
-                                 const float* dm_dmu1, const float* dm_dsigma1_sq,
-                                 const float* dm_dsigma12, float* v_images_hwc,
-                                 hipStream_t stream) {
+extern "C" int tgs_tide_loss(int32_t B, int32_t H, int32_t W, const float* images_hwc,
+                             const float* gt_chw, float gt_div, float lambda_dssim, double* sums,
+                             float* v_images_hwc, hipStream_t stream) {
   if ((int64_t)B * H * W == 0) return TGS_OK;
-  TGS_CHECK_ARG(images_hwc && gt_chw && dm_dmu1 && dm_dsigma1_sq && dm_dsigma12 && v_images_hwc,
-                "tide_loss_bwd: null pointer");
-  const int CH = 3;
-  const float inv_n = 1.f / (float)((int64_t)CH * H * W);
-  Img a{images_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH, 1.f, 0};
-  Img b{gt_chw, (int64_t)CH * H * W, (int64_t)H * W, W, 1, gt_div, 1};
-  Img none{nullptr, 0, 0, 0, 0, 1.f, 0};
-  OutImg out{v_images_hwc, (int64_t)H * W * CH, 1, (int64_t)W * CH, CH};
+  TGS_CHECK_ARG(images_hwc && gt_chw && sums && v_images_hwc, "tide_loss: null pointer");
+  TGS_CHECK_ARG((int64_t)H * W * 3 < (1ll << 31), "tide_loss: image too large");
+  const float inv_n = 1.f / (float)((int64_t)3 * H * W);
   dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, B);
-  hipLaunchKernelGGL(ssim_bwd_kernel, grid, dim3(256), 0, stream, B, CH, H, W, a, b, none,
-                     -lambda_dssim * inv_n, nchw(dm_dmu1, CH, H, W),
-                     nchw(dm_dsigma1_sq, CH, H, W), nchw(dm_dsigma12, CH, H, W),
-                     (1.f - lambda_dssim) * inv_n, out);
-  TGS_RETURN_LAUNCH("tgs_tide_loss_bwd");
+  hipLaunchKernelGGL(tide_loss_kernel, grid, dim3(256), 0, stream, H, W, images_hwc, gt_chw, gt_div,
+                     1e-4f, 9e-4f, -lambda_dssim * inv_n, (1.f - lambda_dssim) * inv_n,
+                     v_images_hwc, sums);
+  TGS_RETURN_LAUNCH("tgs_tide_loss");
 }

@@ -297,17 +297,12 @@ class TideStep:
                N.ptr(offsets), N.ptr(fids), n_isects, N.ptr(images), N.ptr(alphas),
                N.ptr(last_ids), s)
         self._end()
-        parts = self._buf("loss_parts", 3 * C * 3 * H * W, torch.float32)
-        plane = C * 3 * H * W
         sums = self._buf("loss_sums", 2 * C, torch.float64)
+        v_images = self._buf("v_images", C * H * W * 3, torch.float32)
         self._begin("loss")
         N.call("tgs_fill_u32", N.ptr(sums), 4 * C, 0, s)
-        N.call("tgs_tide_loss_fwd", C, H, W, N.ptr(images), N.ptr(gt), self.gt_div,
-               N.ptr(parts), N.ptr(parts[plane:]), N.ptr(parts[2 * plane:]), N.ptr(sums), s)
-        v_images = self._buf("v_images", C * H * W * 3, torch.float32)
-        N.call("tgs_tide_loss_bwd", C, H, W, N.ptr(images), N.ptr(gt), self.gt_div,
-               self.lambda_dssim, N.ptr(parts), N.ptr(parts[plane:]), N.ptr(parts[2 * plane:]),
-               N.ptr(v_images), s)
+        N.call("tgs_tide_loss", C, H, W, N.ptr(images), N.ptr(gt), self.gt_div,
+               self.lambda_dssim, N.ptr(sums), N.ptr(v_images), s)
         self._end()
         sgrads = self._buf("splat_grads", max(V, 1) * 9, torch.float32)
         N.call("tgs_fill_u32", N.ptr(sgrads), max(V, 1) * 9, 0, s)
