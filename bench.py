@@ -37,6 +37,19 @@ BYTES = {
 }
 
 
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` at cfg3 from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (profiles/*_traffic.md), or None."""
+    import re
+
+    for f in sorted((ROOT / "profiles").glob("*_traffic.md")):
+        m = re.search(rf"^traffic_bytes_per_launch {re.escape(kernel)}: (\d+)", f.read_text(),
+                      re.M)
+        if m:
+            return int(m.group(1))
+    return None
+
+
 def cpu_baseline(width, height, frac_a=1 / 16, frac_b=1 / 8, seed=0):
     """Time the CPU oracle on one camera of the same workload with a random
     subset of the Gaussians at two subset sizes, fit t = t_pix + f * t_gauss,
@@ -86,6 +99,9 @@ def main():
     ap.add_argument("--height", type=int, default=1080)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-timing", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run 3 plain device copies of MIB MiB (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the TideGS step is single-GPU; "
@@ -111,6 +127,14 @@ def main():
         stats = ts.step(sc.viewmats, sc.Ks, sc.gt)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+
+    if args.copy_calibration:
+        src = torch.ones(args.copy_calibration * (1 << 20) // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # Per-stage kernel times from HIP events on the launch stream (separate
     # pass so the timed loop above carries no event overhead).
@@ -138,8 +162,10 @@ def main():
     roofline = None
     if dominant:
         d = kernels[dominant]
+        default_cfg = (args.n, args.cams, args.width, args.height) == (4_000_000, 16, 1920, 1080)
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": None}
+                    "unit": "GB/s", "frac": round(d["GBs"] / HBM_PEAK_GBS, 4),
+                    "traffic": profiled_traffic(dominant) if default_cfg else None}
     bwd_names = ("raster_bwd", "project_bwd")
     bwd_ms = sum(kernels[k]["ms"] for k in bwd_names if k in kernels)
     bwd_bytes = sum(kernels[k]["bytes"] for k in bwd_names if k in kernels)
