@@ -21,10 +21,10 @@
 // Every wavefront then compacts the batch to the Gaussians whose box meets its
 // own 16x4 pixel strip; each lane marks which of those reach its pixel and
 // walks only its own marks (lane-compacted iteration, below).
-// In the backward each lane leaves its per-(Gaussian, pixel) terms in LDS and
-// owner lanes sum them per Gaussian as moments (sum v_sigma dx, dx^2, ...),
-// turned into mean2d / conic / opacity gradients once per Gaussian and
-// wavefront.
+// In the backward each lane leaves its per-(Gaussian, pixel) terms in a
+// compact LDS pair buffer and owner lanes sum them per Gaussian as moments
+// (sum v_sigma dx, dx^2, ...), turned into mean2d / conic / opacity gradients
+// once per Gaussian and wavefront.
 //
 // The splat source/gradient sink are policies so the same kernels serve
 // gsplat's SoA tensors (drop-in op) and the packed 48-byte splat records of the
@@ -337,24 +337,27 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Backward.  Per batch and wavefront the list is processed in chunks of CH
-// entries, all within the wavefront (no block barriers):
-//   1. test     lane bit e = list entry e reaches my pixel; the wavefront's
-//               ballot of it is the entry's pixel mask (LDS);
-//   2. pixels   each lane walks its own entries back to front (T, colour
-//               buffer) and leaves (alpha T, v_sigma) for (entry, pixel) in a
-//               per-wavefront LDS pair buffer;
-//   3. owners   lanes 4e..4e+3 own entry e, each summing the moments
-//               (v_sigma dx, dy, dx^2, dx dy, dy^2, v_sigma, colour terms,
-//               |v_mean2d|) over the pixels of its 16-lane quarter from the
-//               pair buffer; a quad DPP sum gives the entry's totals, turned
-//               into mean2d / conic / opacity gradients with its constants;
+// Backward.  Per batch and wavefront:
+//   1. test     as in the forward: each lane's bitmask over the list (alpha
+//               test and last-contributor bound); the wavefront's ballot of
+//               each entry is that Gaussian's pixel mask, and a running sum of
+//               their popcounts gives each entry's slot range in a compact
+//               (Gaussian, pixel) pair buffer;
+//   2. walk     each lane walks its own entries back to front (T, colour
+//               buffer) and leaves (alpha T, v_sigma) in the entry's slot
+//               range at its rank among the entry's pixels;
+//   3. owners   lanes 4e..4e+3 own entry e of a group of 16, each summing the
+//               moments (v_sigma dx, dy, dx^2, dx dy, dy^2, v_sigma, colour
+//               terms, |v_mean2d|) over the pairs of its 16 pixel lanes; a quad
+//               DPP sum gives the entry's totals, turned into mean2d / conic /
+//               opacity gradients with its constants;
 //   4. flush    (entry, value) pairs in value-fastest order, so each atomic
 //               instruction covers a few Gaussians' contiguous records.
-// Every pixel-side term is one product per (entry, pixel), so no lane ever
-// adds to a shared location: no LDS atomics and no per-entry wave reduction.
+// No lane ever adds to a shared location: no LDS atomics and no per-entry
+// wave reduction.  When a batch has more pairs than the buffer holds, the list
+// is processed in consecutive segments (each Gaussian's pairs fit: <= 64).
 // ---------------------------------------------------------------------------
-#define RB_CH 8  // list entries per chunk (8 owner lanes each)
+#define RB_PAIRS 384  // pair-buffer slots per wavefront
 
 template <int CDIM, int TILE, class Src, class Sink>
 __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
@@ -365,6 +368,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   constexpr int BLOCK = TILE * TILE;
   constexpr int WAVES = BLOCK / 64;
   constexpr int ROWS = 64 / TILE;
+  constexpr int WORDS = BLOCK / 32;
   // value slots: 0,1 mean2d; 2..4 conic; 5.. color; 5+CDIM opacity; then |mean2d|
   constexpr int NV = 6 + CDIM;
   constexpr int NA = NV + 2;
@@ -373,15 +377,16 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   __shared__ float s_col[BLOCK][CDIM];
   __shared__ float s_vrc[BLOCK][CDIM];  // dL/dcolor of each pixel
   __shared__ int32_t s_id[BLOCK];
-  __shared__ __align__(16) uint8_t s_list[WAVES][BLOCK];
+  __shared__ uint8_t s_list[WAVES][BLOCK];
   // boxes are dead once the lists are built (barrier), then the pair buffer
-  // (alpha T, v_sigma) per (entry, lane) takes their place
+  // (alpha T, v_sigma) takes their place
   __shared__ union {
     float4 box[BLOCK];
-    float2 pair[WAVES][RB_CH][64];
+    float2 pair[WAVES][RB_PAIRS];
   } s_u;
-  __shared__ uint64_t s_emask[WAVES][RB_CH];
-  __shared__ float s_stage[WAVES][RB_CH * NA];
+  __shared__ uint64_t s_em[WAVES][BLOCK];         // pixel mask of each list entry
+  __shared__ uint16_t s_po[WAVES][BLOCK + 1];     // first pair slot of each list entry
+  __shared__ float s_stage[WAVES][16 * NA];
 
   const uint32_t cam = blockIdx.x;
   const uint32_t ty = blockIdx.y, tx = blockIdx.z;
@@ -389,6 +394,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   const uint32_t tr = threadIdx.x;
   const int lane = tr & 63;
   const int wave = tr >> 6;
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
   const uint32_t i = ty * TILE + tr / TILE;
   const uint32_t j = tx * TILE + tr % TILE;
   const bool inside = i < G.H && j < G.W;
@@ -427,9 +433,8 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   const int32_t wave_bin_final = tgs_wave_max_i32(bin_final);
   const bool absg = sink.absgrad();
   const int nval = absg ? NA : NV;
-
-  // owner role: entry oe of a chunk, pixel lanes [8 oq, 8 oq + 8) of the wave
-  const int oe = lane >> 3, oq = lane & 7;
+  // owner role within a group of 16 entries: entry oe, pixel lanes [16 oq, 16 oq + 16)
+  const int oe = lane >> 2, oq = lane & 3;
 
   for (int32_t b = 0; b < n_batches; ++b) {
     __syncthreads();
@@ -453,127 +458,163 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
     const int j_lo = max(0, batch_end - wave_bin_final);
     const int n_list =
         build_wave_list<BLOCK>(s_u.box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1);
-    __syncthreads();
-    // batch entry t is global index batch_end - t: at or before bin_final
+    // 1. test; batch entry t is global index batch_end - t: at or before bin_final
     const int t_min = batch_end - bin_final;
-    for (int c0 = 0; c0 < n_list; c0 += RB_CH) {
-      const int cn = min(RB_CH, n_list - c0);
-      // the chunk's batch indices, eight bytes of the (8-byte aligned) list
-      const uint64_t l8 = *reinterpret_cast<const uint64_t*>(s_list[wave] + c0);
-      auto entry = [&](int e) { return (int)((l8 >> (8 * e)) & (uint64_t)(BLOCK - 1)); };
-      // 1. test
-      uint32_t m = 0;
+    uint32_t m[WORDS];
+    uint32_t n_pairs = 0;  // wave-uniform
 #pragma unroll
-      for (int e = 0; e < RB_CH; ++e) {
-        const int t = entry(e);
+    for (int W = 0; W < WORDS; ++W) {
+      uint32_t mw = 0;
+      for (int bb = 0; bb < 32 && W * 32 + bb < n_list; ++bb) {
+        const int li = W * 32 + bb;
+        const int t = s_list[wave][li];
         const float4 g0 = s_g0[t];
         const float2 g1 = s_g1[t];
         const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
-        const bool ok = e < cn && inside && t >= t_min &&
-                        !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
-        m |= (ok ? 1u : 0u) << e;
+        const bool ok =
+            inside && t >= t_min && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
+        mw |= (ok ? 1u : 0u) << bb;
         const uint64_t em = tgs_ballot(ok);
-        if (lane == 0) s_emask[wave][e] = em;
+        if (lane == 0) {
+          s_em[wave][li] = em;
+          s_po[wave][li] = (uint16_t)n_pairs;
+        }
+        n_pairs += (uint32_t)__popcll(em);
       }
-      // 2. per-pixel walk, back to front
-      while (tgs_ballot(m != 0u)) {
-        if (m != 0u) {
-          const int e = __builtin_ctz(m);
-          m &= m - 1u;
-          const int t = entry(e);
+      m[W] = mw;
+    }
+    if (lane == 0) s_po[wave][n_list] = (uint16_t)n_pairs;
+    __syncthreads();  // every wavefront is past its list build: boxes are dead
+    int a = 0;        // first list entry of the current segment
+    while (a < n_list) {
+      const uint32_t base = s_po[wave][a];
+      // largest end with at most RB_PAIRS pairs (an entry has <= 64)
+      int e_end = n_list;
+      if (n_pairs - base > RB_PAIRS) {
+        int lo = a + 1, hi = n_list;  // s_po[lo] - base <= RB_PAIRS < s_po[hi] - base
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if ((uint32_t)s_po[wave][mid] - base <= RB_PAIRS) lo = mid;
+          else hi = mid;
+        }
+        e_end = lo;
+      }
+      // 2. per-pixel walk over entries [a, e_end), back to front
+#pragma unroll
+      for (int W = 0; W < WORDS; ++W) {
+        if (W * 32 >= e_end || W * 32 + 32 <= a) continue;
+        const int lo_b = max(a - W * 32, 0), hi_b = min(e_end - W * 32, 32);
+        const uint32_t range = (hi_b >= 32 ? 0xffffffffu : ((1u << hi_b) - 1u)) &
+                               ~((1u << lo_b) - 1u);
+        uint32_t mw = m[W] & range;
+        while (tgs_ballot(mw != 0u)) {
+          if (mw != 0u) {
+            const int li = W * 32 + __builtin_ctz(mw);
+            mw &= mw - 1u;
+            const int t = s_list[wave][li];
+            const float4 g0 = s_g0[t];
+            const float2 g1 = s_g1[t];
+            const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
+            const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
+            const float alpha = fminf(0.999f, raw);
+            const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
+            T *= ra;
+            const float fac = alpha * T;
+            float v_alpha = ra * tf_term;
+#pragma unroll
+            for (int k = 0; k < CDIM; ++k) {
+              const float ck = s_col[t][k];
+              v_alpha += (ck * T - buffer[k] * ra) * v_rc[k];
+              buffer[k] += ck * fac;
+            }
+            // reference: the sigma terms only where alpha was not clamped
+            const float v_sigma = raw <= 0.999f ? -raw * v_alpha : 0.f;
+            const uint32_t slot = (uint32_t)s_po[wave][li] - base +
+                                  (uint32_t)__popcll(s_em[wave][li] & lt_mask);
+            s_u.pair[wave][slot] = make_float2(fac, v_sigma);
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // 3. owners, groups of 16 entries
+      for (int e0 = a; e0 < e_end; e0 += 16) {
+        const int gn = min(16, e_end - e0);
+        float acc[NA];
+#pragma unroll
+        for (int k = 0; k < NA; ++k) acc[k] = 0.f;
+        float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (oe < gn) {
+          const int li = e0 + oe;
+          const int t = s_list[wave][li];
           const float4 g0 = s_g0[t];
-          const float2 g1 = s_g1[t];
-          const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
-          const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
-          const float alpha = fminf(0.999f, raw);
-          const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
-          T *= ra;
-          const float fac = alpha * T;
-          float v_alpha = ra * tf_term;
+          q = staged_conic_rop(g0, s_g1[t]);
+          const uint64_t em = s_em[wave][li];
+          const uint64_t below = oq == 0 ? 0ull : (em & (~0ull >> (64 - 16 * oq)));
+          uint32_t slot = (uint32_t)s_po[wave][li] - base + (uint32_t)__popcll(below);
+          uint32_t rb = (uint32_t)(em >> (16 * oq)) & 0xffffu;
+          while (rb != 0u) {
+            const int pl = 16 * oq + __builtin_ctz(rb);
+            rb &= rb - 1u;
+            const float2 pr = s_u.pair[wave][slot++];
+            const int pix = wave * 64 + pl;
+            const float dx = g0.x - ((float)(tx * TILE + pix % TILE) + 0.5f);
+            const float dy = g0.y - ((float)(ty * TILE + pix / TILE) + 0.5f);
+            const float vs = pr.y;
+            const float mx = vs * dx, my = vs * dy;
+            acc[0] += mx;
+            acc[1] += my;
+            acc[2] += mx * dx;
+            acc[3] += mx * dy;
+            acc[4] += my * dy;
 #pragma unroll
-          for (int k = 0; k < CDIM; ++k) {
-            const float ck = s_col[t][k];
-            v_alpha += (ck * T - buffer[k] * ra) * v_rc[k];
-            buffer[k] += ck * fac;
+            for (int k = 0; k < CDIM; ++k) acc[5 + k] += pr.x * s_vrc[pix][k];
+            acc[5 + CDIM] += vs;
+            if (absg) {
+              acc[NV] += fabsf(q.x * mx + q.y * my);
+              acc[NV + 1] += fabsf(q.y * mx + q.z * my);
+            }
           }
-          // reference: the sigma terms only where alpha was not clamped
-          const float v_sigma = raw <= 0.999f ? -raw * v_alpha : 0.f;
-          s_u.pair[wave][e][lane] = make_float2(fac, v_sigma);
         }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // 3. owners
-      float acc[NA];
 #pragma unroll
-      for (int k = 0; k < NA; ++k) acc[k] = 0.f;
-      float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (oe < cn) {
-        const int t = entry(oe);
-        const float4 g0 = s_g0[t];
-        q = staged_conic_rop(g0, s_g1[t]);
-        uint32_t pm = (uint32_t)(s_emask[wave][oe] >> (8 * oq)) & 0xffu;
-        while (pm != 0u) {
-          const int pl = 8 * oq + __builtin_ctz(pm);
-          pm &= pm - 1u;
-          const float2 pr = s_u.pair[wave][oe][pl];
-          const int pix = wave * 64 + pl;
-          const float dx = g0.x - ((float)(tx * TILE + pix % TILE) + 0.5f);
-          const float dy = g0.y - ((float)(ty * TILE + pix / TILE) + 0.5f);
-          const float vs = pr.y;
-          const float mx = vs * dx, my = vs * dy;
-          acc[0] += mx;
-          acc[1] += my;
-          acc[2] += mx * dx;
-          acc[3] += mx * dy;
-          acc[4] += my * dy;
+        for (int k = 0; k < NA; ++k) {
+          if (k < NV || absg) {
+            acc[k] += tgs_dpp<0xB1>(acc[k]);  // quad_perm [1,0,3,2]
+            acc[k] += tgs_dpp<0x4E>(acc[k]);  // quad_perm [2,3,0,1]
+          }
+        }
+        if (oq == 0 && oe < gn) {
+          float* st = s_stage[wave] + oe * nval;
+          st[0] = q.x * acc[0] + q.y * acc[1];
+          st[1] = q.y * acc[0] + q.z * acc[1];
+          st[2] = 0.5f * acc[2];
+          st[3] = acc[3];
+          st[4] = 0.5f * acc[4];
 #pragma unroll
-          for (int k = 0; k < CDIM; ++k) acc[5 + k] += pr.x * s_vrc[pix][k];
-          acc[5 + CDIM] += vs;
+          for (int k = 0; k < CDIM; ++k) st[5 + k] = acc[5 + k];
+          st[5 + CDIM] = -acc[5 + CDIM] * q.w;
           if (absg) {
-            acc[NV] += fabsf(q.x * mx + q.y * my);
-            acc[NV + 1] += fabsf(q.y * mx + q.z * my);
+            st[NV] = acc[NV];
+            st[NV + 1] = acc[NV + 1];
           }
         }
-      }
-#pragma unroll
-      for (int k = 0; k < NA; ++k) {
-        if (k < NV || absg) {
-          acc[k] += tgs_dpp<0xB1>(acc[k]);   // quad_perm [1,0,3,2]
-          acc[k] += tgs_dpp<0x4E>(acc[k]);   // quad_perm [2,3,0,1]
-          acc[k] += tgs_dpp<0x141>(acc[k]);  // row_half_mirror: 8-lane sum
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // 4. flush
+        const int total = gn * nval;
+        for (int L = lane; L < total; L += 64) {
+          const int e = absg ? L / NA : L / NV;
+          const int k = L - e * nval;
+          const float v = s_stage[wave][L];
+          if (v != 0.f) tgs_atomic_add(sink.ptr(s_id[s_list[wave][e0 + e]], k), v);
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
-      if (oq == 0 && oe < cn) {
-        float* st = s_stage[wave] + oe * nval;
-        st[0] = q.x * acc[0] + q.y * acc[1];
-        st[1] = q.y * acc[0] + q.z * acc[1];
-        st[2] = 0.5f * acc[2];
-        st[3] = acc[3];
-        st[4] = 0.5f * acc[4];
-#pragma unroll
-        for (int k = 0; k < CDIM; ++k) st[5 + k] = acc[5 + k];
-        st[5 + CDIM] = -acc[5 + CDIM] * q.w;
-        if (absg) {
-          st[NV] = acc[NV];
-          st[NV + 1] = acc[NV + 1];
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // 4. flush
-      const int total = cn * nval;
-      for (int L = lane; L < total; L += 64) {
-        const int e = absg ? L / NA : L / NV;
-        const int k = L - e * nval;
-        const float v = s_stage[wave][L];
-        if (v != 0.f) tgs_atomic_add(sink.ptr(s_id[entry(e)], k), v);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      a = e_end;
     }
   }
 }

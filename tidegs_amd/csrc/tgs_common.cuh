@@ -116,6 +116,11 @@ __device__ __forceinline__ float tgs_dpp(float v) {
                                                     BANK_MASK, BOUND_CTRL));
 }
 
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf, bool BOUND_CTRL = false>
+__device__ __forceinline__ uint32_t tgs_dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, BOUND_CTRL);
+}
+
 __device__ __forceinline__ float tgs_wave_sum(float v) {
   v += tgs_dpp<0xB1>(v);           // quad_perm [1,0,3,2]
   v += tgs_dpp<0x4E>(v);           // quad_perm [2,3,0,1]
