@@ -358,6 +358,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
 // is processed in consecutive segments (each Gaussian's pairs fit: <= 64).
 // ---------------------------------------------------------------------------
 #define RB_PAIRS 384  // pair-buffer slots per wavefront
+#define RB_BATCH 128  // Gaussians staged per batch
 
 template <int CDIM, int TILE, class Src, class Sink>
 __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
@@ -368,24 +369,25 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   constexpr int BLOCK = TILE * TILE;
   constexpr int WAVES = BLOCK / 64;
   constexpr int ROWS = 64 / TILE;
-  constexpr int WORDS = BLOCK / 32;
+  constexpr int BATCH = RB_BATCH < BLOCK ? RB_BATCH : BLOCK;
+  constexpr int WORDS = BATCH / 32;
   // value slots: 0,1 mean2d; 2..4 conic; 5.. color; 5+CDIM opacity; then |mean2d|
   constexpr int NV = 6 + CDIM;
   constexpr int NA = NV + 2;
-  __shared__ float4 s_g0[BLOCK];
-  __shared__ float2 s_g1[BLOCK];
-  __shared__ float s_col[BLOCK][CDIM];
+  __shared__ float4 s_g0[BATCH];
+  __shared__ float2 s_g1[BATCH];
+  __shared__ float s_col[BATCH][CDIM];
   __shared__ float s_vrc[BLOCK][CDIM];  // dL/dcolor of each pixel
-  __shared__ int32_t s_id[BLOCK];
-  __shared__ uint8_t s_list[WAVES][BLOCK];
+  __shared__ int32_t s_id[BATCH];
+  __shared__ uint8_t s_list[WAVES][BATCH];
   // boxes are dead once the lists are built (barrier), then the pair buffer
   // (alpha T, v_sigma) takes their place
   __shared__ union {
-    float4 box[BLOCK];
+    float4 box[BATCH];
     float2 pair[WAVES][RB_PAIRS];
   } s_u;
-  __shared__ uint64_t s_em[WAVES][BLOCK];         // pixel mask of each list entry
-  __shared__ uint16_t s_po[WAVES][BLOCK + 1];     // first pair slot of each list entry
+  __shared__ uint64_t s_em[WAVES][BATCH];         // pixel mask of each list entry
+  __shared__ uint16_t s_po[WAVES][BATCH + 1];     // first pair slot of each list entry
   __shared__ float s_stage[WAVES][16 * NA];
 
   const uint32_t cam = blockIdx.x;
@@ -409,7 +411,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   const int32_t range_end = (cam == G.C - 1 && tile_id == G.tile_w * G.tile_h - 1)
                                 ? (int32_t)G.n_isects
                                 : offs[tile_id + 1];
-  const int32_t n_batches = (range_end - range_start + BLOCK - 1) / BLOCK;
+  const int32_t n_batches = (range_end - range_start + BATCH - 1) / BATCH;
 
   const float T_final = 1.f - render_alphas[pid];
   float T = T_final;
@@ -438,10 +440,10 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
 
   for (int32_t b = 0; b < n_batches; ++b) {
     __syncthreads();
-    const int32_t batch_end = range_end - 1 - BLOCK * b;
-    const int32_t batch_size = min(BLOCK, batch_end + 1 - range_start);
+    const int32_t batch_end = range_end - 1 - BATCH * b;
+    const int32_t batch_size = min(BATCH, batch_end + 1 - range_start);
     const int32_t idx = batch_end - (int32_t)tr;
-    if (idx >= range_start) {
+    if ((int)tr < BATCH && idx >= range_start) {
       const int32_t g = flatten_ids[idx];
       SplatData<CDIM> s;
       src.load(g, s);
@@ -457,7 +459,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
     // entries with global index > wave_bin_final contribute to no pixel of this wave
     const int j_lo = max(0, batch_end - wave_bin_final);
     const int n_list =
-        build_wave_list<BLOCK>(s_u.box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1);
+        build_wave_list<BATCH>(s_u.box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1);
     // 1. test; batch entry t is global index batch_end - t: at or before bin_final
     const int t_min = batch_end - bin_final;
     uint32_t m[WORDS];
