@@ -358,7 +358,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
 // is processed in consecutive segments (each Gaussian's pairs fit: <= 64).
 // ---------------------------------------------------------------------------
 #define RB_PAIRS 384  // pair-buffer slots per wavefront
-#define RB_BATCH 128  // Gaussians staged per batch
+#define RB_BATCH 64  // Gaussians staged per batch
 
 template <int CDIM, int TILE, class Src, class Sink>
 __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
