@@ -232,6 +232,8 @@ __device__ __forceinline__ void lane_masks(LaneMask<BLOCK>& m, const uint8_t* li
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
+#define RF_BATCH 128  // Gaussians staged per batch
+
 template <int CDIM, int TILE, class Src>
 __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
     RasterGeom G, Src src, const float* __restrict__ backgrounds,
@@ -241,11 +243,12 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
   constexpr int BLOCK = TILE * TILE;
   constexpr int WAVES = BLOCK / 64;
   constexpr int ROWS = 64 / TILE;  // pixel rows per wavefront
-  __shared__ float4 s_g0[BLOCK];
-  __shared__ float2 s_g1[BLOCK];
-  __shared__ float4 s_box[BLOCK];
-  __shared__ float s_col[BLOCK][CDIM];
-  __shared__ uint8_t s_list[WAVES][BLOCK];
+  constexpr int BATCH = RF_BATCH < BLOCK ? RF_BATCH : BLOCK;
+  __shared__ float4 s_g0[BATCH];
+  __shared__ float2 s_g1[BATCH];
+  __shared__ float4 s_box[BATCH];
+  __shared__ float s_col[BATCH][CDIM];
+  __shared__ uint8_t s_list[WAVES][BATCH];
 
   const uint32_t cam = blockIdx.x;
   const uint32_t ty = blockIdx.y, tx = blockIdx.z;
@@ -266,7 +269,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
   const int32_t range_end = (cam == G.C - 1 && tile_id == G.tile_w * G.tile_h - 1)
                                 ? (int32_t)G.n_isects
                                 : offs[tile_id + 1];
-  const int32_t n_batches = (range_end - range_start + BLOCK - 1) / BLOCK;
+  const int32_t n_batches = (range_end - range_start + BATCH - 1) / BATCH;
 
   float T = 1.f;
   uint32_t cur_idx = 0;
@@ -277,9 +280,9 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
 
   for (int32_t b = 0; b < n_batches; ++b) {
     if (__syncthreads_count(done) >= BLOCK) break;
-    const int32_t batch_start = range_start + BLOCK * b;
+    const int32_t batch_start = range_start + BATCH * b;
     const int32_t idx = batch_start + (int32_t)tr;
-    if (idx < range_end) {
+    if ((int)tr < BATCH && idx < range_end) {
       SplatData<CDIM> s;
       src.load(flatten_ids[idx], s);
       const StagedGeo sg = stage_geo<CDIM>(s);
@@ -290,14 +293,14 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
       for (int k = 0; k < CDIM; ++k) s_col[tr][k] = s.col[k];
     }
     __syncthreads();
-    const int32_t batch_size = min(BLOCK, range_end - batch_start);
+    const int32_t batch_size = min(BATCH, range_end - batch_start);
     int n_list = 0;
     if (tgs_ballot(!done))
-      n_list = build_wave_list<BLOCK>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1);
-    LaneMask<BLOCK> m;
-    lane_masks<BLOCK>(m, s_list[wave], n_list, s_g0, s_g1, px, py, !done, 0);
+      n_list = build_wave_list<BATCH>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1);
+    LaneMask<BATCH> m;
+    lane_masks<BATCH>(m, s_list[wave], n_list, s_g0, s_g1, px, py, !done, 0);
 #pragma unroll
-    for (int W = 0; W < LaneMask<BLOCK>::WORDS; ++W) {
+    for (int W = 0; W < LaneMask<BATCH>::WORDS; ++W) {
       if (W * 32 >= n_list) break;
       uint32_t mw = m.w[W];
       while (true) {
