@@ -247,46 +247,48 @@ extern "C" int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, f
 // lambda (1 - mean SSIM(I_b, gt'_b)), gt' = clamp(gt / gt_div, 0, 1), with
 // I [B,H,W,3] (HWC, as rendered) and gt [B,3,H,W] (CHW).  The loss is fixed,
 // so dL/dSSIM-map is the constant -lambda/N and the whole forward + backward
-// runs in one pass per 16x16 output tile and channel, keeping every
+// runs in one pass per 32x32 output tile and channel, keeping every
 // intermediate in LDS:
-//   inputs   x, y on the 36x36 region (tile + 2 x 5 halo each side);
-//   stats    mu, sigma over the 26x26 region (separable 11-tap window),
+//   inputs   x, y on the 52x52 region (tile + 2 x 5 halo each side);
+//   stats    mu, sigma over the 42x42 region (separable 11-tap window),
 //            giving SSIM (summed over the tile's own pixels) and
 //            g dm/dmu1, g dm/dsigma1^2, g dm/dsigma12 (zero off the image);
 //   gradient G * (g dm) on the tile: f0 + 2 x f1 + y f2, plus the L1 term.
 // sums[2b] += sum|I-gt'|, sums[2b+1] += sum SSIM (double, caller-zeroed).
-#define TL_D1 (SS_T + 2 * SS_R)  // 26: dm region
-#define TL_D2 (SS_T + 4 * SS_R)  // 36: input region
+#define TL_T 32                   // output tile edge
+#define TL_D1 (TL_T + 2 * SS_R)   // 42: dm region
+#define TL_D2 (TL_T + 4 * SS_R)   // 52: input region
+#define TL_THREADS (TL_T * TL_T)  // 1024
 
-__global__ void __launch_bounds__(256) tide_loss_kernel(int H, int W,
-                                                        const float* __restrict__ images_hwc,
-                                                        const float* __restrict__ gt_chw,
-                                                        float gt_div, float C1, float C2,
-                                                        float g_ssim, float g_l1,
-                                                        float* __restrict__ v_images_hwc,
-                                                        double* __restrict__ sums) {
+__global__ void __launch_bounds__(TL_THREADS) tide_loss_kernel(int H, int W,
+                                                               const float* __restrict__ images_hwc,
+                                                               const float* __restrict__ gt_chw,
+                                                               float gt_div, float C1, float C2,
+                                                               float g_ssim, float g_l1,
+                                                               float* __restrict__ v_images_hwc,
+                                                               double* __restrict__ sums) {
   // phase-aliased LDS: inputs -> dm maps, horizontal sums -> backward sums
   __shared__ union {
     struct {
-      float sx[TL_D2][TL_D2 + 1];
-      float sy[TL_D2][TL_D2 + 1];
+      float sx[TL_D2][TL_D2];
+      float sy[TL_D2][TL_D2];
     } in;
     float sdm[3][TL_D1][TL_D1];
   } su;
   __shared__ union {
     float hq[5][TL_D2][TL_D1];
-    float h2[3][TL_D1][SS_T];
+    float h2[3][TL_D1][TL_T];
   } sv;
-  __shared__ float red[2][4];
+  __shared__ float red[2][TL_THREADS / 64];
   auto& sx = su.in.sx;
   auto& sy = su.in.sy;
   auto& sdm = su.sdm;
   auto& hq = sv.hq;
   auto& h2 = sv.h2;
   const int bidx = blockIdx.z;
-  const int x0 = blockIdx.x * SS_T, y0 = blockIdx.y * SS_T;
+  const int x0 = blockIdx.x * TL_T, y0 = blockIdx.y * TL_T;
   const int tid = threadIdx.x;
-  const int ty = tid / SS_T, tx = tid % SS_T;
+  const int ty = tid / TL_T, tx = tid % TL_T;
   const int px = x0 + tx, py = y0 + ty;
   const bool inside = px < W && py < H;
   const int HW = H * W;
@@ -299,31 +301,29 @@ __global__ void __launch_bounds__(256) tide_loss_kernel(int H, int W,
   for (int c = 0; c < 3; ++c) {
     const float* gtc = gtb + c * HW;
     __syncthreads();
-    // inputs on the 36x36 region: thread (ty, tx) fills rows ty+16i, columns tx+16j
+    // inputs on the 52x52 region: thread (ty, tx) fills rows ty+32i, columns tx+32j
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const int r = ty + 16 * i;
-      if (r < TL_D2) {
-        const int yy = y0 + r - 2 * SS_R;
+    for (int i = 0; i < 2; ++i) {
+      const int r = ty + TL_T * i;
+      const int yy = y0 + r - 2 * SS_R;
 #pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          const int col = tx + 16 * j;
-          if (col < TL_D2) {
-            const int xx = x0 + col - 2 * SS_R;
-            float u = 0.f, w = 0.f;
-            if (xx >= 0 && yy >= 0 && xx < W && yy < H) {
-              const int pix = yy * W + xx;
-              u = img[pix * 3 + c];
-              // gt / gt_div, rounded like the division: product plus one
-              // residual correction
-              const float g = gtc[pix];
-              float q = g * rdiv;
-              q = fmaf(fmaf(-q, gt_div, g), rdiv, q);
-              w = fminf(fmaxf(q, 0.f), 1.f);
-            }
-            sx[r][col] = u;
-            sy[r][col] = w;
+      for (int jj = 0; jj < 2; ++jj) {
+        const int col = tx + TL_T * jj;
+        if (r < TL_D2 && col < TL_D2) {
+          const int xx = x0 + col - 2 * SS_R;
+          float u = 0.f, w = 0.f;
+          if (xx >= 0 && yy >= 0 && xx < W && yy < H) {
+            const int pix = yy * W + xx;
+            u = img[pix * 3 + c];
+            // gt / gt_div, rounded like the division: product plus one
+            // residual correction
+            const float g = gtc[pix];
+            float q = g * rdiv;
+            q = fmaf(fmaf(-q, gt_div, g), rdiv, q);
+            w = fminf(fmaxf(q, 0.f), 1.f);
           }
+          sx[r][col] = u;
+          sy[r][col] = w;
         }
       }
     }
@@ -331,48 +331,41 @@ __global__ void __launch_bounds__(256) tide_loss_kernel(int H, int W,
     const float x_own = sx[ty + 2 * SS_R][tx + 2 * SS_R];
     const float y_own = sy[ty + 2 * SS_R][tx + 2 * SS_R];
     if (inside) l1_acc += fabsf(x_own - y_own);
-    // horizontal pass of x, y, x^2, y^2, xy: 36 rows x 26 columns, each
-    // thread one row segment of 4 outputs from 14 inputs held in registers
-    if (tid < TL_D2 * 7) {
-      const int r = tid / 7, c0 = (tid % 7) * 4;  // segments 0..6 cover 28 >= 26 columns
-      float u[14], w[14];
+    // horizontal pass of x, y, x^2, y^2, xy: 52 rows x 42 columns
 #pragma unroll
-      for (int k = 0; k < 14; ++k) {
-        const int cc = min(c0 + k, TL_D2 - 1);
-        u[k] = sx[r][cc];
-        w[k] = sy[r][cc];
-      }
+    for (int i = 0; i < 2; ++i) {
+      const int r = ty + TL_T * i;
 #pragma unroll
-      for (int o = 0; o < 4; ++o) {
-        float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f, q4 = 0.f;
+      for (int jj = 0; jj < 2; ++jj) {
+        const int col = tx + TL_T * jj;
+        if (r < TL_D2 && col < TL_D1) {
+          float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f, q4 = 0.f;
 #pragma unroll
-        for (int t = 0; t < 11; ++t) {
-          const float uu = u[o + t], ww = w[o + t], k = c_gauss[t];
-          q0 += k * uu;
-          q1 += k * ww;
-          q2 += k * (uu * uu);
-          q3 += k * (ww * ww);
-          q4 += k * (uu * ww);
-        }
-        if (c0 + o < TL_D1) {
-          hq[0][r][c0 + o] = q0;
-          hq[1][r][c0 + o] = q1;
-          hq[2][r][c0 + o] = q2;
-          hq[3][r][c0 + o] = q3;
-          hq[4][r][c0 + o] = q4;
+          for (int t = 0; t < 11; ++t) {
+            const float uu = sx[r][col + t], ww = sy[r][col + t], k = c_gauss[t];
+            q0 += k * uu;
+            q1 += k * ww;
+            q2 += k * (uu * uu);
+            q3 += k * (ww * ww);
+            q4 += k * (uu * ww);
+          }
+          hq[0][r][col] = q0;
+          hq[1][r][col] = q1;
+          hq[2][r][col] = q2;
+          hq[3][r][col] = q3;
+          hq[4][r][col] = q4;
         }
       }
     }
     __syncthreads();
-    // vertical pass on the 26x26 region: SSIM and the scaled partial maps;
-    // thread (ty, tx) takes rows ty+16i, columns tx+16j (the inputs are dead:
-    // the dm maps take their place)
+    // vertical pass on the 42x42 region: SSIM and the scaled partial maps (the
+    // inputs are dead: the dm maps take their place)
 #pragma unroll 1
     for (int i = 0; i < 2; ++i) {
-      const int r = ty + 16 * i;
+      const int r = ty + TL_T * i;
 #pragma unroll 1
-      for (int j = 0; j < 2; ++j) {
-        const int col = tx + 16 * j;
+      for (int jj = 0; jj < 2; ++jj) {
+        const int col = tx + TL_T * jj;
         if (r < TL_D1 && col < TL_D1) {
           float f[5];
 #pragma unroll
@@ -401,7 +394,7 @@ __global__ void __launch_bounds__(256) tide_loss_kernel(int H, int W,
             d0 = 2.f * rAB * (mu2 * D - mu2 * Cc + mu1 * CD * (rB - rA));
             d1 = -CD * rAB * rB;
             d2 = 2.f * Cc * rAB;
-            if (r >= SS_R && r < SS_R + SS_T && col >= SS_R && col < SS_R + SS_T)
+            if (r >= SS_R && r < SS_R + TL_T && col >= SS_R && col < SS_R + TL_T)
               m_acc += CD * rAB;
           }
           sdm[0][r][col] = g_ssim * d0;
@@ -411,10 +404,10 @@ __global__ void __launch_bounds__(256) tide_loss_kernel(int H, int W,
       }
     }
     __syncthreads();
-    // backward: horizontal pass (26 rows x 16 columns) ...
+    // backward: horizontal pass (42 rows x 32 columns) ...
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int r = ty + 16 * i;
+      const int r = ty + TL_T * i;
       if (r < TL_D1) {
         float q0 = 0.f, q1 = 0.f, q2 = 0.f;
 #pragma unroll
@@ -454,8 +447,13 @@ __global__ void __launch_bounds__(256) tide_loss_kernel(int H, int W,
   }
   __syncthreads();
   if (tid == 0) {
-    atomicAdd(&sums[2 * bidx + 0], (double)(red[0][0] + red[0][1] + red[0][2] + red[0][3]));
-    atomicAdd(&sums[2 * bidx + 1], (double)(red[1][0] + red[1][1] + red[1][2] + red[1][3]));
+    float a0 = 0.f, a1 = 0.f;
+    for (int w = 0; w < TL_THREADS / 64; ++w) {
+      a0 += red[0][w];
+      a1 += red[1][w];
+    }
+    atomicAdd(&sums[2 * bidx + 0], (double)a0);
+    atomicAdd(&sums[2 * bidx + 1], (double)a1);
   }
 }
 
@@ -466,8 +464,9 @@ extern "C" int tgs_tide_loss(int32_t B, int32_t H, int32_t W, const float* image
   TGS_CHECK_ARG(images_hwc && gt_chw && sums && v_images_hwc, "tide_loss: null pointer");
   TGS_CHECK_ARG((int64_t)H * W * 3 < (1ll << 31), "tide_loss: image too large");
   const float inv_n = 1.f / (float)((int64_t)3 * H * W);
-  dim3 grid((W + SS_T - 1) / SS_T, (H + SS_T - 1) / SS_T, B);
-  hipLaunchKernelGGL(tide_loss_kernel, grid, dim3(256), 0, stream, H, W, images_hwc, gt_chw, gt_div,
+  dim3 grid((W + TL_T - 1) / TL_T, (H + TL_T - 1) / TL_T, B);
+  hipLaunchKernelGGL(tide_loss_kernel, grid, dim3(TL_THREADS), 0, stream, H, W, images_hwc, gt_chw,
+                     gt_div,
                      1e-4f, 9e-4f, -lambda_dssim * inv_n, (1.f - lambda_dssim) * inv_n,
                      v_images_hwc, sums);
   TGS_RETURN_LAUNCH("tgs_tide_loss");
