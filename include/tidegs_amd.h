@@ -218,6 +218,9 @@ int tgs_block_touch_counts(int64_t n_rows, const void* rows, int index_is_i64,
  * 1435-1827 filters + touched rows, 1874-2695 per-camera render/backward,
  * 2434-2469 scatter_add) over a resident [N,59] fp32 table in CACHE column
  * order (storage/block_reader.py:35-44).  Cameras per batch: 1..32. */
+/* Camera centres campos [C,3] = translation of inverse(viewmats[c]) for affine
+ * world->camera matrices (the SH view directions of engine.py:458-512). */
+int tgs_tide_camera_centers(uint32_t C, const float* viewmats, float* campos, tgs_stream_t stream);
 /* Row blocks of the visibility/compaction passes for n_rows rows. */
 uint32_t tgs_tide_row_blocks(uint64_t n_rows);
 /* Packed-projection visibility (gsplat fully_fused_projection_packed_fwd.cu:

@@ -76,6 +76,7 @@ SIGNATURES = {
         ctypes.c_int, [I32, I32, I32, I32, F32, F32, P, P, P, P, P, P, P, P]
     ),
     "tgs_tide_loss": (ctypes.c_int, [I32, I32, I32, P, P, F32, F32, P, P, P]),
+    "tgs_tide_camera_centers": (ctypes.c_int, [U32, P, P, P]),
     "tgs_tide_row_blocks": (U32, [U64]),
     "tgs_tide_visibility": (
         ctypes.c_int, [U64, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, P, P, P]),

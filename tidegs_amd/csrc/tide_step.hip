@@ -517,6 +517,37 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
   for (int k = 0; k < 48; ++k) out[11 + k] = v_sh[k];
 }
 
+// Camera centres: the translation of inverse(viewmat) for an affine world->camera
+// matrix [A | t; 0 0 0 1], i.e. -A^{-1} t (engine.py:459 via the SH
+// directions), evaluated in double from the adjugate.
+__global__ void tide_camera_centers_kernel(uint32_t C, const float* __restrict__ viewmats,
+                                           float* __restrict__ campos) {
+  const uint32_t c = threadIdx.x;
+  if (c >= C) return;
+  const float* M = viewmats + (uint64_t)c * 16;
+  double a[3][3], t[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) a[i][j] = M[i * 4 + j];
+    t[i] = M[i * 4 + 3];
+  }
+  double adj[3][3];
+  adj[0][0] = a[1][1] * a[2][2] - a[1][2] * a[2][1];
+  adj[0][1] = a[0][2] * a[2][1] - a[0][1] * a[2][2];
+  adj[0][2] = a[0][1] * a[1][2] - a[0][2] * a[1][1];
+  adj[1][0] = a[1][2] * a[2][0] - a[1][0] * a[2][2];
+  adj[1][1] = a[0][0] * a[2][2] - a[0][2] * a[2][0];
+  adj[1][2] = a[0][2] * a[1][0] - a[0][0] * a[1][2];
+  adj[2][0] = a[1][0] * a[2][1] - a[1][1] * a[2][0];
+  adj[2][1] = a[0][1] * a[2][0] - a[0][0] * a[2][1];
+  adj[2][2] = a[0][0] * a[1][1] - a[0][1] * a[1][0];
+  const double det = a[0][0] * adj[0][0] + a[0][1] * adj[1][0] + a[0][2] * adj[2][0];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    campos[c * 3 + i] = (float)(-(adj[i][0] * t[0] + adj[i][1] * t[1] + adj[i][2] * t[2]) / det);
+}
+
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
@@ -524,6 +555,15 @@ static int check_cams(uint32_t C) {
   TGS_CHECK_ARG(C >= 1 && C <= TIDE_MAX_CAMS, "tide step: 1..%d cameras per batch (got %u)",
                 TIDE_MAX_CAMS, C);
   return TGS_OK;
+}
+
+extern "C" int tgs_tide_camera_centers(uint32_t C, const float* viewmats, float* campos,
+                                       hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  TGS_CHECK_ARG(viewmats && campos, "tide_camera_centers: null");
+  hipLaunchKernelGGL(tide_camera_centers_kernel, dim3(1), dim3(64), 0, stream, C, viewmats, campos);
+  TGS_RETURN_LAUNCH("tgs_tide_camera_centers");
 }
 
 extern "C" uint32_t tgs_tide_row_blocks(uint64_t n_rows) {

@@ -21,6 +21,7 @@ import ctypes
 import math
 from typing import Any, Dict, List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from . import _native as N
@@ -63,9 +64,13 @@ class GPUResidentAdam:
         self._block_to_slot: Dict[int, int] = {}
         self._slot_to_block: List[Optional[int]] = []
         self._free_slots: List[int] = []
-        self._slot_steps: List[int] = []
-        self._slot_initialized: List[bool] = []
-        self._slot_row_counts: List[int] = []
+        # per state slot (numpy, so that a step updates all touched slots at once)
+        self._slot_steps = np.zeros(0, dtype=np.int64)
+        self._slot_initialized = np.zeros(0, dtype=bool)
+        self._slot_row_counts = np.zeros(0, dtype=np.int64)
+        self._layout_key = None   # cached block layout (see _layout_tables)
+        self._layout_cached = None
+        self._resident_epoch = 0
         self._exp_avg: Optional[torch.Tensor] = None     # [slots*block, 59]
         self._exp_avg_sq: Optional[torch.Tensor] = None  # [slots*block, 59]
         self._bias_correction1: Optional[torch.Tensor] = None
@@ -139,9 +144,20 @@ class GPUResidentAdam:
         self._exp_avg, self._exp_avg_sq = avg, avg_sq
         self._bias_correction1, self._denom_scale = bias, denom
         self._slot_to_block.extend([None] * (target - old_slots))
-        self._slot_steps.extend([0] * (target - old_slots))
-        self._slot_initialized.extend([False] * (target - old_slots))
-        self._slot_row_counts.extend([0] * (target - old_slots))
+        grow = target - old_slots
+        self._slot_steps = np.concatenate([self._slot_steps, np.zeros(grow, dtype=np.int64)])
+        self._slot_initialized = np.concatenate([self._slot_initialized, np.zeros(grow, dtype=bool)])
+        self._slot_row_counts = np.concatenate([self._slot_row_counts,
+                                                np.zeros(grow, dtype=np.int64)])
+        # host mirrors of the bias tables (the source of truth, uploaded whole
+        # after each step's update), pinned for asynchronous copies
+        pin = self.device.type == "cuda"
+        bias_host = torch.zeros(target, dtype=torch.float32, pin_memory=pin)
+        denom_host = torch.zeros(target, dtype=torch.float32, pin_memory=pin)
+        if old_slots:
+            bias_host[:old_slots].copy_(self._bias_host[:old_slots])
+            denom_host[:old_slots].copy_(self._denom_host[:old_slots])
+        self._bias_host, self._denom_host = bias_host, denom_host
         self._free_slots.extend(range(target - 1, old_slots - 1, -1))
         self._allocated_slots = target
 
@@ -168,7 +184,7 @@ class GPUResidentAdam:
             if self._slot_initialized[slot]:
                 self._stats["state_evictions"] += 1
                 self._logical_state_blocks -= 1
-                self._logical_state_bytes -= self._slot_row_counts[slot] * self.TOTAL_WIDTH * 2 * 4
+                self._logical_state_bytes -= int(self._slot_row_counts[slot]) * self.TOTAL_WIDTH * 2 * 4
             self._slot_to_block[slot] = None
             self._slot_steps[slot] = 0
             self._slot_initialized[slot] = False
@@ -194,6 +210,7 @@ class GPUResidentAdam:
             incoming_slots.append(slot)
         self._clear_slots(incoming_slots)
         self._resident_blocks = next_resident
+        self._resident_epoch += 1
         self._update_state_stats()
 
     def _layout(self, manager) -> List[Tuple[int, int, int, int]]:
@@ -213,40 +230,57 @@ class GPUResidentAdam:
             raise RuntimeError("[GPUResidentAdam] working set contains no resident blocks")
         return layout
 
-    def _touched_blocks(self, layout, starts, ends, local_rows, index_is_i64):
-        counts = torch.empty(len(layout), dtype=torch.int64, device=self.device)
-        N.call("tgs_block_touch_counts", local_rows.numel(), N.ptr(local_rows), index_is_i64,
-               N.ptr(starts), N.ptr(ends), len(layout), N.ptr(counts), N.stream_handle(self.device))
-        counts_cpu = counts.cpu().tolist()
-        touched = [(layout[i][2], layout[i][3], int(c)) for i, c in enumerate(counts_cpu) if c > 0]
-        return touched
+    def _layout_tables(self, manager):
+        """The sorted block layout (the reference's per-step searchsorted table,
+        gpu_resident_optimizer.py:266-300) with its device copies.  Rebuilt when
+        the resident set changes (set_resident_blocks) or the working-set
+        manager, its block count or its ``layout_version`` (if it has one) does."""
+        key = (self._resident_epoch, id(manager), id(manager.block_to_gpu_slice),
+               len(manager.block_to_gpu_slice), len(manager.loaded_blocks),
+               getattr(manager, "layout_version", None))
+        if key != self._layout_key:
+            layout = self._layout(manager)
+            arr = np.array(layout, dtype=np.int64).reshape(-1, 4)
+            table = torch.from_numpy(np.ascontiguousarray(arr[:, [0, 1, 3]].T)).to(self.device)
+            self._layout_cached = (layout, arr, table[0], table[1], table[2])
+            self._layout_key = key
+        return self._layout_cached
 
-    def _update_touched_slot_metadata(self, manager, touched, beta1: float, beta2: float) -> int:
-        cold_rows = 0
-        slots, bias_values, denom_values = [], [], []
-        for block_id, slot, count in touched:
-            if not self._slot_initialized[slot]:
-                self._slot_initialized[slot] = True
-                block_slice = manager.block_to_gpu_slice[block_id]
-                row_count = int(block_slice.stop - block_slice.start)
-                self._slot_row_counts[slot] = row_count
-                self._logical_state_blocks += 1
-                self._logical_state_bytes += row_count * self.TOTAL_WIDTH * 2 * 4
-                self._stats["cold_restarts"] += 1
-                self._stats["cold_restarted_rows_touched_total"] += int(count)
-                cold_rows += int(count)
-            self._slot_steps[slot] += 1
-            step = self._slot_steps[slot]
-            slots.append(slot)
-            bias_values.append(1.0 - beta1 ** step)
-            denom_values.append(math.sqrt(1.0 - beta2 ** step))
-        if slots:
-            idx = torch.tensor(slots, dtype=torch.long, device=self.device)
-            self._bias_correction1.index_copy_(
-                0, idx, torch.tensor(bias_values, dtype=torch.float32, device=self.device))
-            self._denom_scale.index_copy_(
-                0, idx, torch.tensor(denom_values, dtype=torch.float32, device=self.device))
-        return cold_rows
+    def _touched_counts(self, n_layout, starts, ends, local_rows, index_is_i64) -> np.ndarray:
+        counts = torch.empty(n_layout, dtype=torch.int64, device=self.device)
+        N.call("tgs_block_touch_counts", local_rows.numel(), N.ptr(local_rows), index_is_i64,
+               N.ptr(starts), N.ptr(ends), n_layout, N.ptr(counts), N.stream_handle(self.device))
+        return counts.cpu().numpy()
+
+    def _update_touched_slot_metadata(self, arr: np.ndarray, counts: np.ndarray, beta1: float,
+                                      beta2: float):
+        """Advance the step of every slot with touched rows and refresh its bias
+        terms (gpu_resident_optimizer.py:302-337); returns (touched layout rows,
+        cold rows)."""
+        hit = np.nonzero(counts > 0)[0]
+        slots = arr[hit, 3]
+        cold = ~self._slot_initialized[slots]
+        cold_slots = slots[cold]
+        cold_rows = int(counts[hit][cold].sum())
+        if cold_slots.size:
+            row_counts = arr[hit, 1][cold] - arr[hit, 0][cold]
+            self._slot_initialized[cold_slots] = True
+            self._slot_row_counts[cold_slots] = row_counts
+            self._logical_state_blocks += int(cold_slots.size)
+            self._logical_state_bytes += int(row_counts.sum()) * self.TOTAL_WIDTH * 2 * 4
+            self._stats["cold_restarts"] += int(cold_slots.size)
+            self._stats["cold_restarted_rows_touched_total"] += cold_rows
+        if slots.size:
+            self._slot_steps[slots] += 1
+            steps = self._slot_steps[slots].astype(np.float64)
+            bias = self._bias_host.numpy()
+            denom = self._denom_host.numpy()
+            bias[slots] = 1.0 - beta1 ** steps
+            denom[slots] = np.sqrt(1.0 - beta2 ** steps)
+            n = self._allocated_slots
+            self._bias_correction1.copy_(self._bias_host[:n], non_blocking=True)
+            self._denom_scale.copy_(self._denom_host[:n], non_blocking=True)
+        return hit, cold_rows
 
     # ---- fused update --------------------------------------------------------
     @staticmethod
@@ -282,7 +316,6 @@ class GPUResidentAdam:
             widths[k] = width
             strides[3 * k + 0], strides[3 * k + 1], strides[3 * k + 2] = ps, gs, self.TOTAL_WIDTH
             lrs[k] = component_lrs[name]
-        self._error_flag.zero_()
         hooks = getattr(self, "kernel_hooks", None)
         if hooks:
             hooks[0]()
@@ -309,17 +342,26 @@ class GPUResidentAdam:
             local_rows = local_rows.to(torch.int64)
         local_rows = local_rows.contiguous()
         index_is_i64 = 1 if local_rows.dtype == torch.int64 else 0
-        layout = self._layout(manager)
-        table = torch.tensor([[s, e, sl] for s, e, _, sl in layout], dtype=torch.int64)
-        table = table.t().contiguous().to(self.device)
-        starts, ends, slots = table[0], table[1], table[2]
+        layout, arr, starts, ends, slots = self._layout_tables(manager)
         for name, _, _, _ in self.COMPONENT_SPECS:
             if name not in sparse_grad_components:
                 raise KeyError(
                     f"[GPUResidentAdam] Missing sparse_grad_components[{name!r}] at iter={iteration}")
-        return manager, local_rows, index_is_i64, layout, starts, ends, slots
+        return manager, local_rows, index_is_i64, layout, arr, starts, ends, slots
+
+    def _touched(self, arr, starts, ends, local_rows, idx64):
+        """Per-block touched counts; rows outside every resident block raise here,
+        before any update, as the reference's slot lookup does (:275-279).  The
+        rows must be sorted (TideGS passes unique ids)."""
+        counts = self._touched_counts(len(arr), starts, ends, local_rows, idx64)
+        if int(counts.sum()) != local_rows.numel():
+            raise RuntimeError(
+                "[GPUResidentAdam] a touched row lies outside every resident block of the layout")
+        return counts
 
     def _check_error(self):
+        """Device-side guard of the update kernel (a row that misses every block);
+        read lazily, since the host check in _touched already covers sorted rows."""
         if int(self._error_flag.item()) != 0:
             raise RuntimeError(
                 "[GPUResidentAdam] a touched row lies outside every resident block of the layout")
@@ -331,30 +373,30 @@ class GPUResidentAdam:
             return empty
         if sparse_grad_local_ids.numel() == 0:
             return empty
-        manager, local_rows, idx64, layout, starts, ends, slots = self._prepare(
+        manager, local_rows, idx64, layout, arr, starts, ends, slots = self._prepare(
             iteration, gaussians, sparse_grad_local_ids, sparse_grad_components)
-        touched = self._touched_blocks(layout, starts, ends, local_rows, idx64)
+        counts = self._touched(arr, starts, ends, local_rows, idx64)
         component_lrs = self._normalize_columns_lr(getattr(gaussians.optimizer, "columns_lr", None))
         beta1, beta2 = gaussians.optimizer.param_groups[0]["betas"]
         beta1, beta2 = float(beta1), float(beta2)
         eps = float(gaussians.optimizer.param_groups[0]["eps"])
-        cold_rows = self._update_touched_slot_metadata(manager, touched, beta1, beta2)
+        hit, cold_rows = self._update_touched_slot_metadata(arr, counts, beta1, beta2)
         param_views = {name: getattr(gaussians, attr).data for name, attr, _, _ in self.COMPONENT_SPECS}
         self._launch("tgs_resident_adam_step", local_rows.numel(), local_rows, idx64, starts, ends,
                      slots, len(layout), param_views, sparse_grad_components, component_lrs,
                      (beta1, beta2, eps, float(self.batch_size)))
-        self._check_error()
         touched_rows = int(local_rows.numel())
         self._stats["optimizer_rows_touched_total"] += touched_rows
         self._update_state_stats()
         return {
-            "updated_blocks": len(touched),
-            "updated_block_ids": [b for b, _, _ in touched],
+            "updated_blocks": int(hit.size),
+            "updated_block_ids": arr[hit, 2].tolist(),
             "touched_rows": touched_rows,
             "cold_rows": int(cold_rows),
         }
 
     def get_stats(self) -> Dict[str, Any]:
+        self._check_error()
         self._update_state_stats()
         return dict(self._stats)
 
@@ -380,25 +422,24 @@ class GPUResidentSophia(GPUResidentAdam):
             return empty
         if sparse_grad_local_ids.numel() == 0:
             return empty
-        manager, local_rows, idx64, layout, starts, ends, slots = self._prepare(
+        manager, local_rows, idx64, layout, arr, starts, ends, slots = self._prepare(
             iteration, gaussians, sparse_grad_local_ids, sparse_grad_components)
-        touched = self._touched_blocks(layout, starts, ends, local_rows, idx64)
+        counts = self._touched(arr, starts, ends, local_rows, idx64)
         component_lrs = self._normalize_columns_lr(getattr(gaussians.optimizer, "columns_lr", None))
         beta1, beta2 = gaussians.optimizer.param_groups[0]["betas"]
         eps = float(gaussians.optimizer.param_groups[0]["eps"])
-        cold_rows = self._update_touched_slot_metadata(manager, touched, float(beta1), float(beta2))
+        hit, cold_rows = self._update_touched_slot_metadata(arr, counts, float(beta1), float(beta2))
         update_h = 1 if (int(iteration) % self.hessian_interval) == 0 else 0
         param_views = {name: getattr(gaussians, attr).data for name, attr, _, _ in self.COMPONENT_SPECS}
         self._launch("tgs_resident_sophia_step", local_rows.numel(), local_rows, idx64, starts, ends,
                      slots, len(layout), param_views, sparse_grad_components, component_lrs,
                      (float(beta1), float(beta2), eps, self.rho, float(self.batch_size), update_h))
-        self._check_error()
         touched_rows = int(local_rows.numel())
         self._stats["optimizer_rows_touched_total"] += touched_rows
         self._update_state_stats()
         return {
-            "updated_blocks": len(touched),
-            "updated_block_ids": [b for b, _, _ in touched],
+            "updated_blocks": int(hit.size),
+            "updated_block_ids": arr[hit, 2].tolist(),
             "touched_rows": touched_rows,
             "cold_rows": int(cold_rows),
         }

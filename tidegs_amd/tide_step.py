@@ -188,7 +188,8 @@ class TideStep:
         W, H, tw, th = self.W, self.H, self.tw, self.th
         viewmats = viewmats.to(self.device, torch.float32).contiguous()
         Ks = Ks.to(self.device, torch.float32).contiguous()
-        campos = torch.linalg.inv(viewmats)[:, :3, 3].contiguous()
+        campos = self._buf("campos", 3 * C, torch.float32).view(C, 3)
+        N.call("tgs_tide_camera_centers", C, N.ptr(viewmats), N.ptr(campos), s)
         gt = gt.to(self.device, torch.float32).contiguous()
         lib = N.load()
 
