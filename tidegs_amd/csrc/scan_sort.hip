@@ -18,7 +18,7 @@
 #include "tgs_common.cuh"
 
 #define SCAN_THREADS 256
-#define SCAN_ITEMS 8
+#define SCAN_ITEMS 16
 #define SCAN_CHUNK (SCAN_THREADS * SCAN_ITEMS)
 
 #define SORT_THREADS 256
@@ -72,46 +72,71 @@ __global__ void __launch_bounds__(SCAN_THREADS) scan_reduce_kernel(const InT* __
   if (threadIdx.x == 0) sums[blockIdx.x] = total;
 }
 
-// In-place exclusive scan of `n` block sums by one block.
+// In-place exclusive scan of `n` block sums by one block: each thread scans a
+// contiguous run of the sums, one block-wide scan joins the runs.
 template <typename OutT>
 __global__ void __launch_bounds__(SCAN_THREADS) scan_sums_kernel(OutT* __restrict__ sums,
                                                                  uint64_t n) {
   __shared__ OutT s_wave[SCAN_THREADS / 64];
-  OutT carry = 0;
-  for (uint64_t base = 0; base < n; base += SCAN_THREADS) {
-    const uint64_t i = base + threadIdx.x;
-    const OutT v = i < n ? sums[i] : (OutT)0;
-    OutT total;
-    const OutT ex = block_exclusive_scan<OutT>(v, s_wave, total);
-    if (i < n) sums[i] = carry + ex;
-    carry += total;
+  const uint64_t per = (n + SCAN_THREADS - 1) / SCAN_THREADS;
+  const uint64_t b0 = (uint64_t)threadIdx.x * per;
+  const uint64_t b1 = b0 + per < n ? b0 + per : n;
+  OutT run = 0;
+  for (uint64_t i = b0; i < b1; ++i) run += sums[i];
+  OutT total;
+  OutT carry = block_exclusive_scan<OutT>(run, s_wave, total);
+  for (uint64_t i = b0; i < b1; ++i) {
+    const OutT v = sums[i];
+    sums[i] = carry;
+    carry += v;
   }
 }
 
+// Wave-level inclusive scan (wave64, shuffles).
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_scan(T v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const T o = __shfl_up(v, off, 64);
+    if (lane >= off) v += o;
+  }
+  return v;
+}
+
+// Striped arrangement: wave w of the block owns items [w*64*ITEMS, (w+1)*64*ITEMS)
+// of the chunk in rounds of 64 consecutive items, so every load and store of
+// a round is one contiguous span.
 template <typename InT, typename OutT, bool INCLUSIVE>
 __global__ void __launch_bounds__(SCAN_THREADS) scan_apply_kernel(const InT* __restrict__ in,
                                                                   uint64_t n,
                                                                   const OutT* __restrict__ sums,
                                                                   OutT* __restrict__ out) {
-  __shared__ OutT s_wave[SCAN_THREADS / 64];
-  // Blocked arrangement: thread t owns items [t*ITEMS, (t+1)*ITEMS).
-  const uint64_t base = (uint64_t)blockIdx.x * SCAN_CHUNK + (uint64_t)threadIdx.x * SCAN_ITEMS;
+  __shared__ OutT s_wtot[SCAN_THREADS / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t wbase = (uint64_t)blockIdx.x * SCAN_CHUNK + (uint64_t)wave * 64 * SCAN_ITEMS;
   OutT vals[SCAN_ITEMS];
   OutT acc = 0;
 #pragma unroll
   for (int k = 0; k < SCAN_ITEMS; ++k) {
-    const uint64_t i = base + k;
+    const uint64_t i = wbase + (uint64_t)k * 64 + lane;
     vals[k] = i < n ? (OutT)in[i] : (OutT)0;
     acc += vals[k];
   }
-  OutT total;
-  OutT run = block_exclusive_scan<OutT>(acc, s_wave, total) + sums[blockIdx.x];
+  // wave total -> exclusive prefix of the waves before this one
+  OutT wt = acc;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) wt += __shfl_xor(wt, off, 64);
+  if (lane == 0) s_wtot[wave] = wt;
+  __syncthreads();
+  OutT carry = sums[blockIdx.x];
+  for (int w = 0; w < wave; ++w) carry += s_wtot[w];
 #pragma unroll
   for (int k = 0; k < SCAN_ITEMS; ++k) {
-    const uint64_t i = base + k;
-    if (INCLUSIVE) run += vals[k];
-    if (i < n) out[i] = run;
-    if (!INCLUSIVE) run += vals[k];
+    const OutT inc = wave_inclusive_scan<OutT>(vals[k]);
+    const uint64_t i = wbase + (uint64_t)k * 64 + lane;
+    if (i < n) out[i] = carry + (INCLUSIVE ? inc : inc - vals[k]);
+    carry += __shfl(inc, 63, 64);
   }
 }
 
