@@ -41,6 +41,9 @@ struct OptimComponents {
   int64_t sstride[TGS_MAX_COMP];
   float lr[TGS_MAX_COMP];
   int n;
+  int total;    // sum of widths
+  int unified;  // components are adjacent columns of one table for param,
+                // grad and both states, every row stride == total
 };
 
 struct OptimLayout {
@@ -107,6 +110,7 @@ struct BlockCache {
 };
 
 #define OPT_UNROLL 4
+#define OPT_RUN 64  // rows per flat-path run
 
 template <typename IdxT, bool SOPHIA>
 __global__ void __launch_bounds__(256) resident_optim_kernel(
@@ -140,12 +144,94 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
   const float one_m_b1 = 1.0f - beta1;
   const float one_m_b2 = 1.0f - beta2;
 
-  // a contiguous range of touched rows per wavefront, OPT_UNROLL rows in flight
+  // per-column learning rate (for the flat path: column -> lr)
+  __shared__ float s_lr[64];
+  __shared__ float s_scale[4][64];  // per wavefront: step size per column of the current run
+  if (threadIdx.x < 64) s_lr[threadIdx.x] = active ? lr : 0.f;
+  __syncthreads();
+
+  // a contiguous range of touched rows per wavefront
   const int64_t per = (n_rows + n_waves - 1) / n_waves;
   const int64_t t0 = wave * per;
   const int64_t t1 = t0 + per < n_rows ? t0 + per : n_rows;
   BlockCache bc;
-  for (int64_t t = t0; t < t1; t += OPT_UNROLL) {
+  int64_t t = t0;
+  while (t < t1) {
+    // Flat path: when the next rows are consecutive and inside one resident
+    // block, param, grad and state rows of the run are each one contiguous span
+    // (unified table), streamed 64 floats per instruction across row bounds.
+    if (C.unified) {
+      const int64_t te = t + OPT_RUN < t1 ? t + OPT_RUN : t1;
+      const int64_t r0 = (int64_t)local_rows[t], rl = (int64_t)local_rows[te - 1];
+      if (rl - r0 == te - 1 - t && bc.lookup(L, r0) && rl < bc.end &&
+          rl - bc.start < L.block_size) {
+        const int W = C.total;
+        const int64_t F = (te - t) * W;
+        const float* __restrict__ g = C.grad[0] + t * W;
+        float* __restrict__ p = C.param[0] + r0 * W;
+        const int64_t srow = bc.slot * L.block_size + (r0 - bc.start);
+        float* __restrict__ mp = C.m[0] + srow * W;
+        float* __restrict__ vp = C.v[0] + srow * W;
+        float dsc = 1.f;
+        // per-column step size lr (Adam: lr / bias1 of this slot, the
+        // reference's rounding of (lr / bias1) * m)
+        float* s_sc = s_scale[threadIdx.x >> 6];
+        if (lane < W) s_sc[lane] = SOPHIA ? s_lr[lane] : s_lr[lane] / bias1[bc.slot];
+        if (!SOPHIA) dsc = denom_scale[bc.slot];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int step = 64 % W;
+        int c = lane % W;  // column of element lane + 64 k
+        for (int64_t i0 = lane; i0 < F; i0 += 64 * OPT_UNROLL) {
+          float gv[OPT_UNROLL], mv[OPT_UNROLL], vv[OPT_UNROLL], pv[OPT_UNROLL];
+#pragma unroll
+          for (int u = 0; u < OPT_UNROLL; ++u) {
+            const int64_t i = i0 + 64 * u;
+            if (i < F) {
+              gv[u] = g[i];
+              mv[u] = mp[i];
+              vv[u] = vp[i];
+              pv[u] = p[i];
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < OPT_UNROLL; ++u) {
+            const int64_t i = i0 + 64 * u;
+            if (i < F) {
+              const float gg = gv[u] / batch_size;
+              const float m1 = beta1 * mv[u] + one_m_b1 * gg;
+              float v1 = vv[u];
+              float p1 = pv[u];
+              const float sc = s_sc[c];
+              if (SOPHIA) {
+                if (update_h) v1 = beta2 * v1 + one_m_b2 * gg * gg;
+                float r = m1 / fmaxf(v1, eps);
+                r = fminf(fmaxf(r, -rho), rho);
+                p1 -= sc * r;
+              } else {
+                v1 = beta2 * v1 + one_m_b2 * gg * gg;
+                const float denom = sqrtf(v1) / dsc + eps;
+                p1 -= sc * m1 / denom;
+              }
+              mp[i] = m1;
+              vp[i] = v1;
+              p[i] = p1;
+            }
+            c += step;
+            if (c >= W) c -= W;
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        t = te;
+        continue;
+      }
+    }
+    // Per-row path: OPT_UNROLL rows in flight, lane = column.
+    const int64_t tb = t;
+    const int64_t te = tb + OPT_UNROLL < t1 ? tb + OPT_UNROLL : t1;
     int64_t poff[OPT_UNROLL], soff[OPT_UNROLL];
     float scale[OPT_UNROLL], dscale[OPT_UNROLL];
     bool live[OPT_UNROLL];
@@ -154,8 +240,8 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
       live[u] = false;
       poff[u] = soff[u] = 0;
       scale[u] = dscale[u] = 1.f;
-      if (t + u < t1) {
-        const int64_t row = (int64_t)local_rows[t + u];
+      if (tb + u < te) {
+        const int64_t row = (int64_t)local_rows[tb + u];
         if (bc.lookup(L, row)) {
           live[u] = active;
           poff[u] = row * pstride + col;
@@ -175,7 +261,7 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
 #pragma unroll
     for (int u = 0; u < OPT_UNROLL; ++u) {
       if (live[u]) {
-        g[u] = grad[(t + u) * gstride + col];
+        g[u] = grad[(tb + u) * gstride + col];
         mm[u] = m[soff[u]];
         vv[u] = v[soff[u]];
         p[u] = param[poff[u]];
@@ -202,6 +288,7 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
       v[soff[u]] = v1;
       param[poff[u]] = p1;
     }
+    t = te;
   }
 }
 
@@ -262,6 +349,15 @@ static int fill_components(OptimComponents& C, int n_comp, float* const* params,
     }
   }
   TGS_CHECK_ARG(total <= 64, "total row width %d exceeds one wavefront (64)", total);
+  C.total = total;
+  int unified = 1, col = 0;
+  for (int k = 0; k < n_comp; ++k) {
+    unified &= C.pstride[k] == total && C.gstride[k] == total && C.sstride[k] == total;
+    unified &= C.param[k] == C.param[0] + col && C.grad[k] == C.grad[0] + col &&
+               C.m[k] == C.m[0] + col && C.v[k] == C.v[0] + col;
+    col += widths[k];
+  }
+  C.unified = unified;
   return TGS_OK;
 }
 

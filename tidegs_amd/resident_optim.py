@@ -39,13 +39,20 @@ class GPUResidentAdam:
         ("features_rest", "_features_rest", 45, 5),
     )
     TOTAL_WIDTH = sum(spec[2] for spec in COMPONENT_SPECS)
-    # Column offsets of each component inside the unified state rows.
-    _STATE_COLS = {}
-    _c = 0
-    for _name, _, _w, _ in COMPONENT_SPECS:
-        _STATE_COLS[_name] = _c
-        _c += _w
-    del _c, _name, _w
+    # Column offsets of each component inside the unified state rows: the
+    # resident table's CACHE column order (storage/block_reader.py:35-44), so
+    # that a [N,59] parameter table, its [T,59] gradient rows and the state rows
+    # share one column layout (the kernel then streams runs of rows as flat
+    # spans).  The state layout is internal to this class.
+    _STATE_COLS = {"xyz": 0, "scaling": 3, "rotation": 6, "opacity": 10, "features_dc": 11,
+                   "features_rest": 14}
+    # components in state-column order (the kernel's component order)
+    _order = []
+    for _spec in COMPONENT_SPECS:
+        _order.append((_STATE_COLS[_spec[0]], _spec))
+    _order.sort()
+    _LAUNCH_ORDER = tuple(_item[1] for _item in _order)
+    del _order, _spec
 
     def __init__(self, batch_size: int = 1, block_size: int = 4096, capacity_blocks: int = 0,
                  device: str = "cuda"):
@@ -298,7 +305,7 @@ class GPUResidentAdam:
 
     def _launch(self, kernel: str, n_rows, local_rows, index_is_i64, starts, ends, slots,
                 n_layout, param_views, grads, component_lrs, extra_args):
-        n = len(self.COMPONENT_SPECS)
+        n = len(self._LAUNCH_ORDER)
         params_p = (ctypes.c_void_p * n)()
         grads_p = (ctypes.c_void_p * n)()
         m_p = (ctypes.c_void_p * n)()
@@ -306,7 +313,7 @@ class GPUResidentAdam:
         widths = (ctypes.c_int32 * n)()
         strides = (ctypes.c_int64 * (3 * n))()
         lrs = (ctypes.c_float * n)()
-        for k, (name, _, width, _) in enumerate(self.COMPONENT_SPECS):
+        for k, (name, _, width, _) in enumerate(self._LAUNCH_ORDER):
             pp, ps = self._row_view(param_views[name], width, name)
             gp, gs = self._row_view(grads[name], width, name)
             col = self._STATE_COLS[name]
