@@ -32,7 +32,7 @@ BYTES = {
     "project_fwd": lambda s: s["T"] * (4 + 4 + 4 + 236) + s["V"] * (4 + 48 + 4 + 8),
     "raster_fwd": lambda s: s["C"] * s["P"] * 20 + s["I"] * 52,
     "raster_bwd": lambda s: s["C"] * s["P"] * 20 + s["I"] * 52 + s["V"] * 36,
-    "project_bwd": lambda s: s["T"] * (4 + 4 + 236 + 236) + s["V"] * (4 + 16 + 36),
+    "project_bwd": lambda s: s["T"] * (4 + 4 + 4 + 236 + 236) + s["V"] * (4 + 36),
     "adam": lambda s: s["T"] * 1656,
 }
 

@@ -293,13 +293,15 @@ int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const float* backgro
                            uint32_t n_isects, const float* alphas, const int32_t* last_ids,
                            const float* v_images, float* splat_grads, tgs_stream_t stream);
 /* Per touched row: projection + SH + activation backward over its visits in
- * camera order; writes the compact gradient row grads[t, 0:59] once. */
+ * camera order (the set bits of masks[row]); the render projection (near, far,
+ * radius_clip as in tgs_tide_project_fwd) is recomputed per visit.  Writes the
+ * compact gradient row grads[t, 0:59] once. */
 int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched, const int32_t* visit_base,
-                         const int32_t* visits, const int32_t* cam_offsets, uint32_t C,
+                         const int32_t* visits, const uint32_t* masks, uint32_t C,
                          const float* params, const float* viewmats, const float* Ks,
-                         const float* campos, int32_t W, int32_t H, float eps2d,
-                         int32_t sh_degree, const float* splats, const float* splat_grads,
-                         float* grads, tgs_stream_t stream);
+                         const float* campos, int32_t W, int32_t H, float eps2d, float near_plane,
+                         float far_plane, float radius_clip, int32_t sh_degree,
+                         const float* splat_grads, float* grads, tgs_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -434,13 +434,11 @@ __global__ void __launch_bounds__(256) tide_isect_ids_kernel(
 __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
     uint32_t n_touched, const int32_t* __restrict__ touched,
     const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
-    const int32_t* __restrict__ cam_offsets, TideCams tc, const float* __restrict__ params,
-    int W, int H, float eps2d, int sh_degree, const float4* __restrict__ splats,
+    const uint32_t* __restrict__ masks, TideCams tc, const float* __restrict__ params, int W,
+    int H, float eps2d, float near_plane, float far_plane, float radius_clip, int sh_degree,
     const float* __restrict__ splat_grads, float* __restrict__ grads) {
   __shared__ CamLDS s_cam;
-  __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
   load_cams_lds(tc, s_cam);
-  if (threadIdx.x <= tc.C) s_off[threadIdx.x] = cam_offsets[threadIdx.x];
   __syncthreads();
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_touched) return;
@@ -466,12 +464,18 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
     for (int j = 0; j < 3; ++j) v_S.m[i][j] = 0.f;
   float v_op = 0.f;
 
-  const int32_t v0 = visit_base[t], v1 = visit_base[t + 1];
-  for (int32_t v = v0; v < v1; ++v) {
-    const uint32_t e = (uint32_t)visits[v];
-    const float4 r1 = splats[(uint64_t)e * 3 + 1];
-    if (r1.w <= 0.f) continue;  // culled by the render projection: zero gradient
-    const uint32_t c = entry_camera(s_off, tc.C, e);
+  // visits in camera order = the set bits of the row's visibility mask; the
+  // render projection is recomputed (bit-identical to the forward's) instead
+  // of reading the conic and radius back from the splat records
+  uint32_t mask = masks[touched[t]];
+  const int32_t* vis = visits + visit_base[t];
+  for (int j = 0; mask != 0u; ++j) {
+    const uint32_t c = (uint32_t)__builtin_ctz(mask);
+    mask &= mask - 1u;
+    const uint32_t e = (uint32_t)vis[j];
+    const ProjResult pr =
+        project_forward(p, Sigma, s_cam.cam[c], W, H, eps2d, near_plane, far_plane, radius_clip);
+    if (pr.radius <= 0) continue;  // culled by the render projection: zero gradient
     const float* g = splat_grads + (uint64_t)e * 9;
     const float vm[2] = {g[0], g[1]};
     const float vc[3] = {g[2], g[3], g[4]};
@@ -486,7 +490,7 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
     for (int k = 0; k < 3; ++k) vcol[k] = (col[k] + 0.5f >= 0.f) ? vcol[k] : 0.f;
     float vdir[3];
     sh_vjp3<true>(sh_degree, dx, dy, dz, sh, vcol, v_sh, true, vdir);
-    const float conic[3] = {r1.x, r1.y, r1.z};
+    const float conic[3] = {pr.conic[0], pr.conic[1], pr.conic[2]};
     ProjGrad pg;
     project_backward(p, Sigma, s_cam.cam[c], W, H, eps2d, conic, 0.f, vm, 0.f, vc, false, 0.f,
                      false, pg);
@@ -734,21 +738,21 @@ extern "C" int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const flo
 
 extern "C" int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched,
                                     const int32_t* visit_base, const int32_t* visits,
-                                    const int32_t* cam_offsets, uint32_t C, const float* params,
+                                    const uint32_t* masks, uint32_t C, const float* params,
                                     const float* viewmats, const float* Ks, const float* campos,
-                                    int32_t W, int32_t H, float eps2d, int32_t sh_degree,
-                                    const float* splats, const float* splat_grads, float* grads,
-                                    hipStream_t stream) {
+                                    int32_t W, int32_t H, float eps2d, float near_plane,
+                                    float far_plane, float radius_clip, int32_t sh_degree,
+                                    const float* splat_grads, float* grads, hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;
   if (n_touched == 0) return TGS_OK;
-  TGS_CHECK_ARG(touched && visit_base && visits && cam_offsets && params && viewmats && Ks &&
-                    campos && splats && splat_grads && grads,
+  TGS_CHECK_ARG(touched && visit_base && visits && masks && params && viewmats && Ks && campos &&
+                    splat_grads && grads,
                 "tide_project_bwd: null");
   TGS_CHECK_ARG(sh_degree >= 0 && sh_degree <= 3, "tide step: sh_degree must be in [0,3]");
   TideCams tc{viewmats, Ks, campos, C};
   hipLaunchKernelGGL(tide_project_bwd_kernel, dim3(tgs_blocks(n_touched, 256)), dim3(256), 0,
-                     stream, n_touched, touched, visit_base, visits, cam_offsets, tc, params, W,
-                     H, eps2d, sh_degree, (const float4*)splats, splat_grads, grads);
+                     stream, n_touched, touched, visit_base, visits, masks, tc, params, W, H,
+                     eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads, grads);
   TGS_RETURN_LAUNCH("tgs_tide_project_bwd");
 }

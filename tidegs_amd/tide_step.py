@@ -317,8 +317,9 @@ class TideStep:
         grads = self._buf("grads", max(T, 1) * ROW, torch.float32).view(-1, ROW)[:T]
         self._begin("project_bwd")
         N.call("tgs_tide_project_bwd", T, N.ptr(touched), N.ptr(visit_base), N.ptr(visits),
-               N.ptr(cam_offsets), C, N.ptr(P), N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H,
-               self.eps2d, self.sh_degree, N.ptr(splats), N.ptr(sgrads), N.ptr(grads), s)
+               N.ptr(masks), C, N.ptr(P), N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H,
+               self.eps2d, self.near, self.far, 0.0, self.sh_degree, N.ptr(sgrads),
+               N.ptr(grads), s)
         self._end()
         if self._timing:
             self.last_visible_entries = int((splats[: V * 12].view(-1, 12)[:, 7] > 0).sum())
