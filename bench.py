@@ -88,36 +88,43 @@ def cpu_baseline(width, height, frac_a=1 / 16, frac_b=1 / 8, seed=0):
     }
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--n", type=int, default=4_000_000)
-    ap.add_argument("--cams", type=int, default=16)
-    ap.add_argument("--width", type=int, default=1920)
-    ap.add_argument("--height", type=int, default=1080)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-stage-timing", action="store_true")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="also run 3 plain device copies of MIB MiB (the reference kernel for "
-                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the TideGS step is single-GPU; "
-              "see DESIGN.md for how it would shard by camera). Run with --gpus 1.",
-              file=sys.stderr)
-        sys.exit(2)
+WORKLOADS = {
+    "cfg3": "cfg3: 4M Gaussians, 16 cams x 1920x1080, L1+SSIM, fwd+bwd+Adam",
+    "cfg2": "cfg2: 1M Gaussians, 1 cam 1920x1080, rasterizer fwd+bwd",
+    "cfg4": "cfg4: 16M-Gaussian aerial city, 4 oblique cams x 1920x1080, fwd+bwd+Adam",
+    "cfg5": "cfg5: resident [32M,59] optimizer step, 30% rows visible",
+}
 
+
+def _stage_kernels(ts, stats, args, stage_ms, C, P):
+    Vvis = int(ts.last_visible_entries)
+    shape = {"N": ts.params.shape[0], "C": C, "P": P, "V": stats.entries, "Vvis": Vvis,
+             "I": stats.n_isects, "T": stats.touched_rows}
+    kernels = {}
+    for name, f in BYTES.items():
+        if name in stage_ms and stage_ms[name] > 0:
+            b = f(shape)
+            kernels[name] = {"ms": stage_ms[name], "bytes": b,
+                             "GBs": round(b / (stage_ms[name] * 1e-3) / 1e9, 1)}
+    return kernels
+
+
+def bench_step(args, dev):
+    """Full TideGS step (cfg3, cfg4) or the rasterizer pair alone (cfg2)."""
     import torch
 
     from tidegs_amd import scenes
     from tidegs_amd.tide_step import TideStep
 
-    dev = torch.device("cuda:0")
-    sc = scenes.cfg3(seed=0, n=args.n, n_cams=args.cams, width=args.width, height=args.height,
-                     with_gt=True).to(dev)
-    ts = TideStep(sc.params.contiguous(), sc.width, sc.height, batch_size=args.cams)
+    if args.workload == "cfg3":
+        sc = scenes.cfg3(seed=0, n=args.n, n_cams=args.cams, width=args.width,
+                         height=args.height, with_gt=True).to(dev)
+    elif args.workload == "cfg4":
+        sc = scenes.cfg4(seed=0, device=dev)
+    else:
+        sc = scenes.cfg2(seed=0).to(dev)
+    C = sc.n_cams
+    ts = TideStep(sc.params.contiguous(), sc.width, sc.height, batch_size=C)
 
     for _ in range(args.warmup):
         ts.step(sc.viewmats, sc.Ks, sc.gt)
@@ -139,7 +146,7 @@ def main():
     # Per-stage kernel times from HIP events on the launch stream (separate
     # pass so the timed loop above carries no event overhead).
     stage_ms = {}
-    if not args.no_stage_timing:
+    if not args.no_stage_timing or args.workload == "cfg2":
         reps = 3
         acc = {}
         for _ in range(reps):
@@ -148,29 +155,28 @@ def main():
                 acc[k] = acc.get(k, 0.0) + v
         stage_ms = {k: round(v / reps, 4) for k, v in acc.items()}
         stats = st
-    C, P = args.cams, args.width * args.height
-    Vvis = int(ts.last_visible_entries)
-    shape = {"N": args.n, "C": C, "P": P, "V": stats.entries, "Vvis": Vvis, "I": stats.n_isects,
-             "T": stats.touched_rows}
-    kernels = {}
-    for name, f in BYTES.items():
-        if name in stage_ms and stage_ms[name] > 0:
-            b = f(shape)
-            kernels[name] = {"ms": stage_ms[name], "bytes": b,
-                             "GBs": round(b / (stage_ms[name] * 1e-3) / 1e9, 1)}
+    P = sc.width * sc.height
+    kernels = _stage_kernels(ts, stats, args, stage_ms, C, P)
+    default_cfg = (args.workload == "cfg3" and
+                   (args.n, args.cams, args.width, args.height) == (4_000_000, 16, 1920, 1080))
+    if args.workload == "cfg2":
+        kernels = {k: v for k, v in kernels.items() if k in ("raster_fwd", "raster_bwd")}
+        ms = sum(v["ms"] for v in kernels.values())
     dominant = max(kernels, key=lambda k: kernels[k]["ms"]) if kernels else None
     roofline = None
     if dominant:
         d = kernels[dominant]
-        default_cfg = (args.n, args.cams, args.width, args.height) == (4_000_000, 16, 1920, 1080)
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(d["GBs"] / HBM_PEAK_GBS, 4),
                     "traffic": profiled_traffic(dominant) if default_cfg else None}
     bwd_names = ("raster_bwd", "project_bwd")
     bwd_ms = sum(kernels[k]["ms"] for k in bwd_names if k in kernels)
     bwd_bytes = sum(kernels[k]["bytes"] for k in bwd_names if k in kernels)
+    metric = {"cfg3": METRIC,
+              "cfg4": "ms/train-step (fwd+bwd+Adam) at 16M Gaussians (aerial city), 4×1080p",
+              "cfg2": "ms/rasterizer fwd+bwd at 1M Gaussians, 1×1080p"}[args.workload]
     line = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(ms, 3),
         "unit": "ms",
         "n_gpus": 1,
@@ -181,10 +187,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded cfg3 scene, random-init Gaussians, random targets)",
-        "config": {"workload": "cfg3: 4M Gaussians, 16 cams x 1920x1080, L1+SSIM, fwd+bwd+Adam",
-                   "gaussians": args.n, "cameras": C, "width": args.width,
-                   "height": args.height, "visible_entries": stats.entries,
+        "data": f"synthetic (seeded {args.workload} scene, random-init Gaussians, random targets)",
+        "config": {"workload": WORKLOADS[args.workload],
+                   "gaussians": ts.params.shape[0], "cameras": C, "width": sc.width,
+                   "height": sc.height, "visible_entries": stats.entries,
                    "touched_rows": stats.touched_rows, "isects": stats.n_isects,
                    "isects_per_tile": round(stats.n_isects / (C * ts.tw * ts.th), 1)},
         "bwd_hbm_GBs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1) if bwd_ms else None,
@@ -193,8 +199,116 @@ def main():
         "kernels": kernels,
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline:
+    if args.workload == "cfg3" and not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.width, args.height)
+    return line
+
+
+def bench_optimizer(args, dev):
+    """cfg5: fused resident Adam and Sophia over a [32M, 59] CACHE-order table
+    with 30% of the rows visible (sorted int32 ids).  The timed step is the
+    whole GPUResidentAdam.step (host bookkeeping + one kernel); the kernel
+    alone is timed with HIP events on its stream."""
+    import torch
+
+    from tidegs_amd import scenes
+    from tidegs_amd.resident_optim import GPUResidentAdam, GPUResidentSophia
+    from tidegs_amd.tide_step import _CACHE_COLS, _Manager, _TableGaussians
+
+    n = 32_000_000 if args.n == 4_000_000 else args.n
+    case = scenes.cfg5(seed=0, n=n, device=dev)
+    T = case.rows.numel()
+    mgr = _Manager(n, 4096, dev)
+    lrs = torch.tensor([1.6e-4, 0.05, 5e-3, 1e-3, 2.5e-3, 1.25e-4])
+    comps = {name: case.grads[:, a:b] for name, (a, b) in _CACHE_COLS.items()}
+    out = {}
+    for kind, cls, kw, betas in (("adam", GPUResidentAdam, {}, (0.9, 0.999)),
+                                 ("sophia", GPUResidentSophia, {"rho": 0.04}, (0.9, 0.99))):
+        gs = _TableGaussians(case.table, mgr, lrs, betas, 1e-15)
+        opt = cls(batch_size=1, block_size=4096, capacity_blocks=len(mgr.loaded_blocks),
+                  device=str(dev), **kw)
+        opt.set_resident_blocks(mgr.loaded_blocks)
+        it = 0
+        for _ in range(args.warmup):
+            it += 1
+            opt.step(it, gs, case.rows, comps)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            it += 1
+            opt.step(it, gs, case.rows, comps)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+        evs = []
+        opt.kernel_hooks = (lambda: evs.append([torch.cuda.Event(enable_timing=True)]) or
+                            evs[-1][0].record(),
+                            lambda: evs[-1].append(torch.cuda.Event(enable_timing=True)) or
+                            evs[-1][1].record())
+        for _ in range(3):
+            it += 1
+            opt.step(it, gs, case.rows, comps)
+        opt.kernel_hooks = None
+        torch.cuda.synchronize()
+        k_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        b = T * 1656
+        out[kind] = {"ms_per_step": round(ms, 4), "kernel_ms": round(k_ms, 4), "bytes": b,
+                     "GBs": round(b / (k_ms * 1e-3) / 1e9, 1)}
+        del opt
+        torch.cuda.empty_cache()
+    a = out["adam"]
+    return {
+        "metric": "ms/optimizer-step (fused resident Adam) at [32M,59], 30% rows visible",
+        "value": a["ms_per_step"],
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": a["ms_per_step"],
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) table, N(0,1e-3) gradients, sorted int32 rows)",
+        "config": {"workload": WORKLOADS["cfg5"], "rows": n, "touched_rows": T},
+        "roofline": {"kernel": "resident_optim (adam)", "bound": "hbm", "achieved": a["GBs"],
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(a["GBs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "optimizers": out,
+        "cpu_baseline": None,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="cfg3",
+                    help="cfg3 (default) is the headline step; the others are the "
+                         "remaining BASELINE configurations")
+    ap.add_argument("--n", type=int, default=4_000_000)
+    ap.add_argument("--cams", type=int, default=16)
+    ap.add_argument("--width", type=int, default=1920)
+    ap.add_argument("--height", type=int, default=1080)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-stage-timing", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run 3 plain device copies of MIB MiB (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the TideGS step is single-GPU; "
+              "see DESIGN.md for how it would shard by camera). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    if args.workload == "cfg5":
+        line = bench_optimizer(args, dev)
+    else:
+        line = bench_step(args, dev)
     print(json.dumps(line), flush=True)
 
 

@@ -112,7 +112,7 @@ def camera_step(params, rows, viewmat, K, gt, W, H, sh_degree=3, background=None
 
 
 def batch_grads(params, viewmats, Ks, gts, W, H, sh_degree=3, backgrounds=None,
-                proj_dtype=torch.float64, raster_dtype=np.float32):
+                proj_dtype=torch.float64, raster_dtype=np.float32, lambda_dssim=0.2):
     """touched rows [T], compact grads [T,59], per-camera losses and images."""
     filters = packed_filters(params, viewmats, Ks, W, H)
     touched = torch.unique(torch.cat(filters)) if filters else torch.empty(0, dtype=torch.long)
@@ -125,8 +125,8 @@ def batch_grads(params, viewmats, Ks, gts, W, H, sh_degree=3, backgrounds=None,
             continue
         bg = None if backgrounds is None else backgrounds[c]
         loss, img, g = camera_step(params, rows, viewmats[c], Ks[c], gts[c], W, H, sh_degree,
-                                   background=bg, proj_dtype=proj_dtype,
-                                   raster_dtype=raster_dtype)
+                                   background=bg, lambda_dssim=lambda_dssim,
+                                   proj_dtype=proj_dtype, raster_dtype=raster_dtype)
         idx = torch.searchsorted(touched, rows)
         grads.index_add_(0, idx, g)
         losses.append(loss)
