@@ -217,7 +217,9 @@ int tgs_block_touch_counts(int64_t n_rows, const void* rows, int index_is_i64,
 /* These replace TideGS's per-camera loop (strategies/tide_engine/engine.py:
  * 1435-1827 filters + touched rows, 1874-2695 per-camera render/backward,
  * 2434-2469 scatter_add) over a resident [N,59] fp32 table in CACHE column
- * order (storage/block_reader.py:35-44).  Cameras per batch: 1..32. */
+ * order (storage/block_reader.py:35-44).  Cameras per batch: 1..32.
+ * row_stride (>= 59 floats) is the table's row pitch: 59 for a dense table,
+ * 64 for the padded layout whose rows are whole 256-byte lines. */
 /* Camera centres campos [C,3] = translation of inverse(viewmats[c]) for affine
  * world->camera matrices (the SH view directions of engine.py:458-512). */
 int tgs_tide_camera_centers(uint32_t C, const float* viewmats, float* campos, tgs_stream_t stream);
@@ -226,8 +228,9 @@ uint32_t tgs_tide_row_blocks(uint64_t n_rows);
 /* Packed-projection visibility (gsplat fully_fused_projection_packed_fwd.cu:
  * 50-131) of every row in every camera: masks [N] (bit c = camera c), and
  * per-block counts [(C+2)*nb] (per camera, touched rows, visits). */
-int tgs_tide_visibility(uint64_t n_rows, const float* params, uint32_t C, const float* viewmats,
-                        const float* Ks, const float* campos, int32_t W, int32_t H, float eps2d,
+int tgs_tide_visibility(uint64_t n_rows, const float* params, uint32_t row_stride, uint32_t C,
+                        const float* viewmats, const float* Ks, const float* campos, int32_t W,
+                        int32_t H, float eps2d,
                         float near_plane, float far_plane, float radius_clip, uint32_t* masks,
                         uint32_t* counts, tgs_stream_t stream);
 /* Compaction from offs = exclusive scan of counts: entries (concatenated
@@ -248,7 +251,8 @@ int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* masks, const u
  * 255 x 255. */
 int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched, const int32_t* visit_base,
                          const int32_t* visits, const uint32_t* masks, uint32_t C,
-                         const float* params, const float* viewmats, const float* Ks,
+                         const float* params, uint32_t row_stride, const float* viewmats,
+                         const float* Ks,
                          const float* campos, int32_t W, int32_t H, float eps2d, float near_plane,
                          float far_plane, float radius_clip, int32_t sh_degree,
                          uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
@@ -295,13 +299,15 @@ int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const float* backgro
 /* Per touched row: projection + SH + activation backward over its visits in
  * camera order (the set bits of masks[row]); the render projection (near, far,
  * radius_clip as in tgs_tide_project_fwd) is recomputed per visit.  Writes the
- * compact gradient row grads[t, 0:59] once. */
+ * compact gradient row grads[t * grad_stride + 0..58] once, and zeros in the
+ * padding columns 59..grad_stride-1. */
 int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched, const int32_t* visit_base,
                          const int32_t* visits, const uint32_t* masks, uint32_t C,
-                         const float* params, const float* viewmats, const float* Ks,
-                         const float* campos, int32_t W, int32_t H, float eps2d, float near_plane,
-                         float far_plane, float radius_clip, int32_t sh_degree,
-                         const float* splat_grads, float* grads, tgs_stream_t stream);
+                         const float* params, uint32_t row_stride, const float* viewmats,
+                         const float* Ks, const float* campos, int32_t W, int32_t H, float eps2d,
+                         float near_plane, float far_plane, float radius_clip, int32_t sh_degree,
+                         const float* splat_grads, float* grads, uint32_t grad_stride,
+                         tgs_stream_t stream);
 
 #ifdef __cplusplus
 }

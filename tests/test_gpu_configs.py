@@ -296,15 +296,21 @@ def _lr_cols(lrs, order):
     return lr
 
 
-@pytest.mark.parametrize("kind,order", [("adam", "cache"), ("adam", "unified"),
-                                        ("sophia", "cache")])
-def test_cfg5_optimizer_32m_rows(gpu, kind, order):
-    announce(f"cfg5: resident [32M,59] {kind} ({order} column order), 30% visible, two steps")
+@pytest.mark.parametrize("kind,order,pitch", [("adam", "cache", 64), ("adam", "cache", 59),
+                                              ("adam", "unified", 59), ("sophia", "cache", 64)])
+def test_cfg5_optimizer_32m_rows(gpu, kind, order, pitch):
+    announce(f"cfg5: resident [32M,59] {kind} ({order} column order, row pitch {pitch}), "
+             f"30% visible, two steps")
     n, block = 32_000_000, 4096
     case1 = scenes.cfg5(seed=0, n=n, device=gpu)
     case2 = scenes.cfg5(seed=1, n=n, device=gpu)
+    if pitch == 64:
+        case1.table = scenes.padded_table(case1.table)
+        case1.grads = scenes.padded_table(case1.grads)
+        case2.grads = scenes.padded_table(case2.grads)
     table = case1.table
     del case2.table
+    torch.cuda.empty_cache()
     before = table.clone()
     lrs = [1e-3, 0.05, 5e-3, 1e-3, 2.5e-3, 1.25e-4]
     b1, b2 = (0.9, 0.999) if kind == "adam" else (0.9, 0.99)
@@ -332,6 +338,9 @@ def test_cfg5_optimizer_32m_rows(gpu, kind, order):
     assert not bool((changed & ~vis2).any()), "a row outside the visible set changed"
     untouched = ~(vis1 | vis2)
     assert bool(((table == before).all(dim=1) | ~untouched).all())
+    if pitch == 64:  # the padding columns keep their bits (zeros)
+        full = table.as_strided((n, 64), (64, 1))
+        assert not bool(full[:, 59:].any())
     # every block is touched by both steps, so the slot step count is 2 for all
     # visible rows of step 2; check a random sample of rows against the closed form
     rng = np.random.default_rng(7)

@@ -24,12 +24,14 @@ def _scene(seed=0, n=3000, C=3, W=96, H=64):
     return scenes.small(seed=seed, n=n, n_cams=C, W=W, H=H, log_scale_mu=-2.3)
 
 
-@pytest.mark.parametrize("with_bg", [False, True])
-def test_tide_step_grads_match_oracle(gpu, with_bg):
-    announce(f"tide step grads bg={with_bg}")
+@pytest.mark.parametrize("with_bg,pitch", [(False, 59), (True, 59), (False, 64)])
+def test_tide_step_grads_match_oracle(gpu, with_bg, pitch):
+    announce(f"tide step grads bg={with_bg} row pitch={pitch}")
     sc = _scene(seed=1 if with_bg else 0)
     bgs = torch.tensor([[0.1, 0.5, 0.9], [1.0, 1.0, 1.0], [0.0, 0.2, 0.3]]) if with_bg else None
     params = sc.params.to(gpu).contiguous()
+    if pitch == 64:
+        params = scenes.padded_table(params)
     ts = TideStep(params, sc.width, sc.height, batch_size=sc.n_cams,
                   backgrounds=bgs.to(gpu) if with_bg else None)
     touched, grads, stats = ts.forward_backward(sc.viewmats, sc.Ks, sc.gt)
@@ -76,10 +78,13 @@ def test_tide_step_isect_bit_exact(gpu):
     np.testing.assert_array_equal(to_np(ts.last["offsets"]), R.isect_offset_encode(o_ids, C, tw, th))
 
 
-def test_tide_step_optimizer_untouched_rows_bitwise(gpu):
-    announce("tide step optimizer")
+@pytest.mark.parametrize("pitch", [59, 64])
+def test_tide_step_optimizer_untouched_rows_bitwise(gpu, pitch):
+    announce(f"tide step optimizer row pitch={pitch}")
     sc = _scene(seed=3, n=20000, C=2)
     params = sc.params.to(gpu).contiguous()
+    if pitch == 64:
+        params = scenes.padded_table(params)
     before = params.clone()
     ts = TideStep(params, sc.width, sc.height, batch_size=2, block_size=4096)
     touched, grads, stats = ts.forward_backward(sc.viewmats, sc.Ks, sc.gt)
@@ -90,6 +95,8 @@ def test_tide_step_optimizer_untouched_rows_bitwise(gpu):
     mask = torch.ones(params.shape[0], dtype=torch.bool, device=gpu)
     mask[t] = False
     assert torch.equal(params[mask], before[mask])
+    if pitch == 64:  # the padding columns keep their bits (zeros)
+        assert not bool(params.as_strided((params.shape[0], 64), (64, 1))[:, 59:].any())
     # touched rows follow the closed-form first Adam step with TideGS's sqrt-mode
     # scaling (gaussian_model.py:855-888): lr*sqrt(bsz), betas^bsz, eps/sqrt(bsz)
     lr_groups = np.array([1.6e-4, 0.05, 5e-3, 1e-3, 2.5e-3, 2.5e-3 / 20.0]) * np.sqrt(2)

@@ -79,12 +79,12 @@ SIGNATURES = {
     "tgs_tide_camera_centers": (ctypes.c_int, [U32, P, P, P]),
     "tgs_tide_row_blocks": (U32, [U64]),
     "tgs_tide_visibility": (
-        ctypes.c_int, [U64, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, P, P, P]),
+        ctypes.c_int, [U64, P, U32, U32, P, P, P, I32, I32, F32, F32, F32, F32, P, P, P]),
     "tgs_tide_compact": (ctypes.c_int, [U64, U32, P, P, P, P, P, P, P, P, P, P]),
     "tgs_tide_project_fwd": (
         ctypes.c_int,
-        [U32, P, P, P, P, U32, P, P, P, P, I32, I32, F32, F32, F32, F32, I32, U32, U32, U32, P,
-         P, P, P]),
+        [U32, P, P, P, P, U32, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, I32, U32, U32, U32,
+         P, P, P, P]),
     "tgs_tide_isect_count": (ctypes.c_int, [U32, P, P, P]),
     "tgs_tide_isect_segments": (ctypes.c_int, [U32, P, P, P, P]),
     "tgs_tide_isect_emit": (ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P]),
@@ -95,7 +95,7 @@ SIGNATURES = {
         ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, P]),
     "tgs_tide_project_bwd": (
         ctypes.c_int,
-        [U32, P, P, P, P, U32, P, P, P, P, I32, I32, F32, F32, F32, F32, I32, P, P, P]),
+        [U32, P, P, P, P, U32, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, I32, P, P, U32, P]),
     "tgs_resident_adam_step": (
         ctypes.c_int,
         [I64, P, ctypes.c_int, P, P, P, I64, I64, P, P, ctypes.c_int, P, P, P, P, P, P, P,

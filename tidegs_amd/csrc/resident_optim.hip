@@ -30,6 +30,16 @@
 
 #define TGS_MAX_COMP 8
 
+__device__ __forceinline__ int64_t tgs_readlane_i64(int64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ float tgs_readlane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 struct OptimComponents {
   float* param[TGS_MAX_COMP];
   const float* grad[TGS_MAX_COMP];
@@ -43,7 +53,8 @@ struct OptimComponents {
   int n;
   int total;    // sum of widths
   int unified;  // components are adjacent columns of one table for param,
-                // grad and both states, every row stride == total
+                // grad and both states, each table with one row stride <= 64
+  int pw, gw, sw;  // unified: the param, grad and state row strides
 };
 
 struct OptimLayout {
@@ -52,6 +63,7 @@ struct OptimLayout {
   const int64_t* slots;   // [L]
   int64_t n;              // L
   int64_t block_size;
+  int block_shift;        // log2(block_size) when it is a power of two, else -1
 };
 
 // Resolve lane -> (component, column); lanes beyond the total width get comp=-1.
@@ -72,12 +84,19 @@ __device__ __forceinline__ void lane_column(const OptimComponents& c, int lane, 
   }
 }
 
+// A wave-uniform 64-bit value loaded from memory, moved to scalar registers
+// (the compiler cannot prove the layout tables read-only, so the loads are
+// vector loads; the readfirstlane keeps everything derived from them scalar).
+__device__ __forceinline__ int64_t tgs_uniform_i64(int64_t v) {
+  return tgs_readlane_i64(v, 0);
+}
+
 // Number of ends <= row (searchsorted right=True), wave-uniform.
 __device__ __forceinline__ int64_t layout_search(const OptimLayout& L, int64_t row) {
   int64_t lo = 0, hi = L.n;
   while (lo < hi) {
     int64_t mid = (lo + hi) >> 1;
-    if (L.ends[mid] <= row)
+    if (tgs_uniform_i64(L.ends[mid]) <= row)
       lo = mid + 1;
     else
       hi = mid;
@@ -90,18 +109,31 @@ __device__ __forceinline__ int64_t layout_search(const OptimLayout& L, int64_t r
 // searches the layout only when it crosses into another block.
 struct BlockCache {
   int64_t start = 0, end = 0, slot = 0;  // empty until the first lookup
+  int64_t s0 = -1;                       // starts[0], loaded on first use
   bool ok = false;
   __device__ __forceinline__ bool lookup(const OptimLayout& L, int64_t row) {
     if (row >= start && row < end) return true;
-    const int64_t pos = layout_search(L, row);
+    // Blocks of a working set usually sit back to back from starts[0]: guess
+    // the position from the row, check it with one pair of loads, and fall
+    // back to the binary search when the guess misses.
+    int64_t pos = -1;
+    if (L.block_shift >= 0) {
+      if (s0 < 0) s0 = tgs_uniform_i64(L.starts[0]);
+      const int64_t g = row >= s0 ? (row - s0) >> L.block_shift : -1;
+      if (g >= 0 && g < L.n) {
+        const int64_t gs = tgs_uniform_i64(L.starts[g]), ge = tgs_uniform_i64(L.ends[g]);
+        if (row >= gs && row < ge) pos = g;
+      }
+    }
+    if (pos < 0) pos = layout_search(L, row);
     ok = false;
     start = end = 0;
     if (pos < L.n) {
-      const int64_t s = L.starts[pos], e = L.ends[pos];
+      const int64_t s = tgs_uniform_i64(L.starts[pos]), e = tgs_uniform_i64(L.ends[pos]);
       if (row >= s && row < e && row - s < L.block_size) {
         start = s;
         end = e;
-        slot = L.slots[pos];
+        slot = tgs_uniform_i64(L.slots[pos]);
         ok = true;
       }
     }
@@ -109,9 +141,245 @@ struct BlockCache {
   }
 };
 
+// Adam / Sophia update of one element; `sc` is lr / bias1 (Adam: the
+// reference's rounding of (lr / bias1) * m) or lr (Sophia), `dsc` the slot's
+// sqrt(1 - b2^t).
+template <bool SOPHIA>
+__device__ __forceinline__ void optim_update(float gv, float& mv, float& vv, float& pv, float sc,
+                                             float dsc, float beta1, float beta2, float one_m_b1,
+                                             float one_m_b2, float eps, float batch_size,
+                                             float rho, int update_h) {
+  const float gg = gv / batch_size;
+  mv = beta1 * mv + one_m_b1 * gg;
+  if (SOPHIA) {
+    if (update_h) vv = beta2 * vv + one_m_b2 * gg * gg;
+    float r = mv / fmaxf(vv, eps);
+    r = fminf(fmaxf(r, -rho), rho);
+    pv -= sc * r;
+  } else {
+    vv = beta2 * vv + one_m_b2 * gg * gg;
+    const float denom = sqrtf(vv) / dsc + eps;
+    pv -= sc * mv / denom;
+  }
+}
+
+#define OPT_ROWS 8  // rows in flight per wavefront (row path)
 #define OPT_UNROLL 4
 #define OPT_RUN 64  // rows per flat-path run
 
+// Raw dword buffer over [base, base + bytes): an access whose byte offset
+// (lane offset + scalar offset) falls outside the range reads 0 or is dropped
+// by the address unit.  The third-dword value
+// is the gfx9-family raw-buffer format (32-bit data, no swizzle).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tgs_rsrc(const float* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)bytes, 0x00020000);
+}
+// The b32 builtins move raw 32-bit words: reinterpret, never convert.
+__device__ __forceinline__ float tgs_bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ void tgs_bstore(float v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                           uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, soff, 0);
+}
+// A lane offset that every range check rejects (with any scalar offset below
+// 2^31 added it stays at or above 2^31, beyond every descriptor's range).
+#define TGS_OFF_NONE 0x80000000u
+
+// Unified layout: param, grad and both state tables each hold all W columns
+// of a row contiguously, at row strides PW, GW and SW (each <= 64 floats: 59
+// for dense tables, 64 for the padded layout whose rows are whole 256-byte
+// lines).  Groups of OPT_RUN sorted touched rows are dealt to the wavefronts
+// round-robin.
+//   * flat path (dense tables only): when the group's rows are consecutive and
+//     inside one resident block, every table's part is one contiguous span,
+//     streamed 64 floats per instruction across row bounds;
+//   * row path: OPT_ROWS rows at a time, lane = column.  The row ids arrive
+//     with one vector load and are read back as scalars.  For rows inside one
+//     resident block each table gets one buffer descriptor at the first row
+//     and every row is a scalar byte offset from it, so a load is (descriptor,
+//     the lane's column offset, the row's scalar offset): one data VGPR per
+//     load and 4 * OPT_ROWS loads in flight per wavefront.  Padding lanes
+//     (W <= lane < stride) write back what they read, so a padded row is
+//     stored as a whole line and its padding keeps its bits.
+template <typename IdxT, bool SOPHIA>
+__global__ void __launch_bounds__(256) resident_optim_unified_kernel(
+    int64_t n_rows, const IdxT* __restrict__ local_rows, OptimLayout L,
+    const float* __restrict__ bias1, const float* __restrict__ denom_scale, OptimComponents C,
+    float beta1, float beta2, float eps, float batch_size, float rho, int update_h,
+    int* __restrict__ error_flag) {
+  const int lane = threadIdx.x & 63;
+  // threadIdx.x >> 6 is the same in every lane of a wavefront; readfirstlane
+  // tells the compiler so, which keeps the row range and every address derived
+  // from it in scalar registers
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) +
+                       __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t n_waves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  const int W = C.total;
+  const int PW = C.pw, GW = C.gw, SW = C.sw;
+  const int64_t PB = (int64_t)PW * 4, GB = (int64_t)GW * 4, SB = (int64_t)SW * 4;  // row bytes
+  const bool act = lane < W;
+  const uint32_t voff_g = act ? (uint32_t)lane * 4u : TGS_OFF_NONE;
+  const uint32_t voff_p = lane < PW ? (uint32_t)lane * 4u : TGS_OFF_NONE;
+  const uint32_t voff_s = lane < SW ? (uint32_t)lane * 4u : TGS_OFF_NONE;
+  const bool dense = PW == W && GW == W && SW == W;
+  const float one_m_b1 = 1.0f - beta1;
+  const float one_m_b2 = 1.0f - beta2;
+  const float* P = C.param[0];
+  const float* G = C.grad[0];
+  const float* M = C.m[0];
+  const float* V = C.v[0];
+
+  // per-column learning rate
+  __shared__ float s_lr[64];
+  __shared__ float s_scale[4][64];  // per wavefront: step size per column of the current run
+  if (threadIdx.x < 64) {
+    float lr = 0.f;
+    int base = 0;
+#pragma unroll
+    for (int k = 0; k < TGS_MAX_COMP; ++k) {
+      if (k < C.n) {
+        if ((int)threadIdx.x >= base && (int)threadIdx.x < base + C.width[k]) lr = C.lr[k];
+        base += C.width[k];
+      }
+    }
+    s_lr[threadIdx.x] = lr;
+  }
+  __syncthreads();
+  const float lr_lane = s_lr[lane];
+
+  // Groups of OPT_RUN touched rows, dealt to the wavefronts round-robin: the
+  // rows in flight across the whole GPU at any moment then lie in one narrow
+  // window of each table, instead of one region per wavefront spread over
+  // the whole table.
+  BlockCache bc;
+  const int64_t n_groups = (n_rows + OPT_RUN - 1) / OPT_RUN;
+  for (int64_t grp = wave; grp < n_groups; grp += n_waves) {
+    int64_t t = grp * OPT_RUN;
+    const int64_t t1 = t + OPT_RUN < n_rows ? t + OPT_RUN : n_rows;
+    if (dense) {
+      const int64_t r0 = tgs_uniform_i64((int64_t)local_rows[t]);
+      const int64_t rl = tgs_uniform_i64((int64_t)local_rows[t1 - 1]);
+      if (t1 - t >= 16 && rl - r0 == t1 - 1 - t && bc.lookup(L, r0) && rl < bc.end &&
+          rl - bc.start < L.block_size) {
+        const int64_t F = (t1 - t) * W;  // <= OPT_RUN * 64 floats
+        const int64_t srow = bc.slot * L.block_size + (r0 - bc.start);
+        const auto rg = tgs_rsrc(G + t * W, F * 4);
+        const auto rp = tgs_rsrc(P + r0 * W, F * 4);
+        const auto rm = tgs_rsrc(M + srow * W, F * 4);
+        const auto rv = tgs_rsrc(V + srow * W, F * 4);
+        float* s_sc = s_scale[threadIdx.x >> 6];
+        s_sc[lane] = SOPHIA ? lr_lane : lr_lane / tgs_readlane_f32(bias1[bc.slot], 0);
+        const float dsc = SOPHIA ? 1.f : tgs_readlane_f32(denom_scale[bc.slot], 0);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int step = 64 % W;
+        int c = lane % W;  // column of element lane + 64 k
+        // elements past F read as 0 and their stores are dropped (range check)
+        for (uint32_t i0 = (uint32_t)lane; i0 < (uint32_t)F; i0 += 64 * OPT_UNROLL) {
+          float gv[OPT_UNROLL], mv[OPT_UNROLL], vv[OPT_UNROLL], pv[OPT_UNROLL];
+#pragma unroll
+          for (int u = 0; u < OPT_UNROLL; ++u) {
+            const uint32_t o = (i0 + 64u * u) * 4u;
+            gv[u] = tgs_bload(rg, o, 0);
+            mv[u] = tgs_bload(rm, o, 0);
+            vv[u] = tgs_bload(rv, o, 0);
+            pv[u] = tgs_bload(rp, o, 0);
+          }
+#pragma unroll
+          for (int u = 0; u < OPT_UNROLL; ++u) {
+            const uint32_t o = (i0 + 64u * u) * 4u;
+            optim_update<SOPHIA>(gv[u], mv[u], vv[u], pv[u], s_sc[c], dsc, beta1, beta2,
+                                 one_m_b1, one_m_b2, eps, batch_size, rho, update_h);
+            tgs_bstore(mv[u], rm, o, 0);
+            tgs_bstore(vv[u], rv, o, 0);
+            tgs_bstore(pv[u], rp, o, 0);
+            c += step;
+            if (c >= W) c -= W;
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        continue;
+      }
+    }
+    // row path: OPT_ROWS rows (sorted) at a time
+    for (; t < t1;) {
+      const int n = (int)(t1 - t < OPT_ROWS ? t1 - t : OPT_ROWS);
+      const int64_t my_row = lane < n ? (int64_t)local_rows[t + lane] : 0;
+      const int64_t r_first = tgs_readlane_i64(my_row, 0);
+      const int64_t r_last = tgs_readlane_i64(my_row, n - 1);
+      const int64_t rows_span = r_last - r_first + 1;
+      const auto rg = tgs_rsrc(G + t * GW, n * GB);
+      if (bc.lookup(L, r_first) && r_last < bc.end && r_last - bc.start < L.block_size &&
+          rows_span * 256 < 0x7fffffff) {
+        // every row of the group is in this block: one descriptor per table
+        const int64_t srow = bc.slot * L.block_size + (r_first - bc.start);
+        const auto rp = tgs_rsrc(P + r_first * PW, rows_span * PB);
+        const auto rm = tgs_rsrc(M + srow * SW, rows_span * SB);
+        const auto rv = tgs_rsrc(V + srow * SW, rows_span * SB);
+        const float sc = SOPHIA ? lr_lane : lr_lane / tgs_readlane_f32(bias1[bc.slot], 0);
+        const float dsc = SOPHIA ? 1.f : tgs_readlane_f32(denom_scale[bc.slot], 0);
+        float gv[OPT_ROWS], mv[OPT_ROWS], vv[OPT_ROWS], pv[OPT_ROWS];
+#pragma unroll
+        for (int u = 0; u < OPT_ROWS; ++u) {
+          if (u < n) {
+            const int64_t d = tgs_readlane_i64(my_row, u) - r_first;
+            gv[u] = tgs_bload(rg, voff_g, (uint32_t)(u * GB));
+            mv[u] = tgs_bload(rm, voff_s, (uint32_t)(d * SB));
+            vv[u] = tgs_bload(rv, voff_s, (uint32_t)(d * SB));
+            pv[u] = tgs_bload(rp, voff_p, (uint32_t)(d * PB));
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < OPT_ROWS; ++u) {
+          if (u < n) {
+            const int64_t d = tgs_readlane_i64(my_row, u) - r_first;
+            float m1 = mv[u], v1 = vv[u], p1 = pv[u];
+            optim_update<SOPHIA>(gv[u], m1, v1, p1, sc, dsc, beta1, beta2, one_m_b1, one_m_b2,
+                                 eps, batch_size, rho, update_h);
+            tgs_bstore(act ? m1 : mv[u], rm, voff_s, (uint32_t)(d * SB));
+            tgs_bstore(act ? v1 : vv[u], rv, voff_s, (uint32_t)(d * SB));
+            tgs_bstore(act ? p1 : pv[u], rp, voff_p, (uint32_t)(d * PB));
+          }
+        }
+      } else {
+        // the rows straddle resident blocks (or span 2 GB): one row at a time
+        for (int u = 0; u < n; ++u) {
+          const int64_t row = tgs_readlane_i64(my_row, u);
+          if (!bc.lookup(L, row)) {
+            // a touched row outside every resident block: the host checks this
+            // flag and raises (the reference raises on a missing slot, :275-279)
+            if (lane == 0) atomicOr(error_flag, 1);
+            continue;
+          }
+          const int64_t srow = bc.slot * L.block_size + (row - bc.start);
+          const auto rp = tgs_rsrc(P + row * PW, PB);
+          const auto rm = tgs_rsrc(M + srow * SW, SB);
+          const auto rv = tgs_rsrc(V + srow * SW, SB);
+          const float sc = SOPHIA ? lr_lane : lr_lane / tgs_readlane_f32(bias1[bc.slot], 0);
+          const float dsc = SOPHIA ? 1.f : tgs_readlane_f32(denom_scale[bc.slot], 0);
+          const float gv = tgs_bload(rg, voff_g, (uint32_t)(u * GB));
+          const float mv = tgs_bload(rm, voff_s, 0), vv = tgs_bload(rv, voff_s, 0);
+          const float pv = tgs_bload(rp, voff_p, 0);
+          float m1 = mv, v1 = vv, p1 = pv;
+          optim_update<SOPHIA>(gv, m1, v1, p1, sc, dsc, beta1, beta2, one_m_b1, one_m_b2, eps,
+                               batch_size, rho, update_h);
+          tgs_bstore(act ? m1 : mv, rm, voff_s, 0);
+          tgs_bstore(act ? v1 : vv, rv, voff_s, 0);
+          tgs_bstore(act ? p1 : pv, rp, voff_p, 0);
+        }
+      }
+      t += n;
+    }
+  }
+}
+
+// Any layout: per-component pointers and row strides, one row per step with
+// lane = column (the reference's six separate component tensors, or a table
+// whose column order differs from the state's).
 template <typename IdxT, bool SOPHIA>
 __global__ void __launch_bounds__(256) resident_optim_kernel(
     int64_t n_rows, const IdxT* __restrict__ local_rows, OptimLayout L,
@@ -119,7 +387,8 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
     float beta1, float beta2, float eps, float batch_size, float rho, int update_h,
     int* __restrict__ error_flag) {
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) +
+                       __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t n_waves = (int64_t)gridDim.x * (blockDim.x >> 6);
 
   int comp, col;
@@ -144,93 +413,11 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
   const float one_m_b1 = 1.0f - beta1;
   const float one_m_b2 = 1.0f - beta2;
 
-  // per-column learning rate (for the flat path: column -> lr)
-  __shared__ float s_lr[64];
-  __shared__ float s_scale[4][64];  // per wavefront: step size per column of the current run
-  if (threadIdx.x < 64) s_lr[threadIdx.x] = active ? lr : 0.f;
-  __syncthreads();
-
-  // a contiguous range of touched rows per wavefront
   const int64_t per = (n_rows + n_waves - 1) / n_waves;
   const int64_t t0 = wave * per;
   const int64_t t1 = t0 + per < n_rows ? t0 + per : n_rows;
   BlockCache bc;
-  int64_t t = t0;
-  while (t < t1) {
-    // Flat path: when the next rows are consecutive and inside one resident
-    // block, param, grad and state rows of the run are each one contiguous span
-    // (unified table), streamed 64 floats per instruction across row bounds.
-    if (C.unified) {
-      const int64_t te = t + OPT_RUN < t1 ? t + OPT_RUN : t1;
-      const int64_t r0 = (int64_t)local_rows[t], rl = (int64_t)local_rows[te - 1];
-      if (rl - r0 == te - 1 - t && bc.lookup(L, r0) && rl < bc.end &&
-          rl - bc.start < L.block_size) {
-        const int W = C.total;
-        const int64_t F = (te - t) * W;
-        const float* __restrict__ g = C.grad[0] + t * W;
-        float* __restrict__ p = C.param[0] + r0 * W;
-        const int64_t srow = bc.slot * L.block_size + (r0 - bc.start);
-        float* __restrict__ mp = C.m[0] + srow * W;
-        float* __restrict__ vp = C.v[0] + srow * W;
-        float dsc = 1.f;
-        // per-column step size lr (Adam: lr / bias1 of this slot, the
-        // reference's rounding of (lr / bias1) * m)
-        float* s_sc = s_scale[threadIdx.x >> 6];
-        if (lane < W) s_sc[lane] = SOPHIA ? s_lr[lane] : s_lr[lane] / bias1[bc.slot];
-        if (!SOPHIA) dsc = denom_scale[bc.slot];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int step = 64 % W;
-        int c = lane % W;  // column of element lane + 64 k
-        for (int64_t i0 = lane; i0 < F; i0 += 64 * OPT_UNROLL) {
-          float gv[OPT_UNROLL], mv[OPT_UNROLL], vv[OPT_UNROLL], pv[OPT_UNROLL];
-#pragma unroll
-          for (int u = 0; u < OPT_UNROLL; ++u) {
-            const int64_t i = i0 + 64 * u;
-            if (i < F) {
-              gv[u] = g[i];
-              mv[u] = mp[i];
-              vv[u] = vp[i];
-              pv[u] = p[i];
-            }
-          }
-#pragma unroll
-          for (int u = 0; u < OPT_UNROLL; ++u) {
-            const int64_t i = i0 + 64 * u;
-            if (i < F) {
-              const float gg = gv[u] / batch_size;
-              const float m1 = beta1 * mv[u] + one_m_b1 * gg;
-              float v1 = vv[u];
-              float p1 = pv[u];
-              const float sc = s_sc[c];
-              if (SOPHIA) {
-                if (update_h) v1 = beta2 * v1 + one_m_b2 * gg * gg;
-                float r = m1 / fmaxf(v1, eps);
-                r = fminf(fmaxf(r, -rho), rho);
-                p1 -= sc * r;
-              } else {
-                v1 = beta2 * v1 + one_m_b2 * gg * gg;
-                const float denom = sqrtf(v1) / dsc + eps;
-                p1 -= sc * m1 / denom;
-              }
-              mp[i] = m1;
-              vp[i] = v1;
-              p[i] = p1;
-            }
-            c += step;
-            if (c >= W) c -= W;
-          }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        t = te;
-        continue;
-      }
-    }
-    // Per-row path: OPT_UNROLL rows in flight, lane = column.
-    const int64_t tb = t;
+  for (int64_t tb = t0; tb < t1; tb += OPT_UNROLL) {
     const int64_t te = tb + OPT_UNROLL < t1 ? tb + OPT_UNROLL : t1;
     int64_t poff[OPT_UNROLL], soff[OPT_UNROLL];
     float scale[OPT_UNROLL], dscale[OPT_UNROLL];
@@ -239,7 +426,8 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
     for (int u = 0; u < OPT_UNROLL; ++u) {
       live[u] = false;
       poff[u] = soff[u] = 0;
-      scale[u] = dscale[u] = 1.f;
+      scale[u] = lr;
+      dscale[u] = 1.f;
       if (tb + u < te) {
         const int64_t row = (int64_t)local_rows[tb + u];
         if (bc.lookup(L, row)) {
@@ -247,12 +435,10 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
           poff[u] = row * pstride + col;
           soff[u] = (bc.slot * L.block_size + (row - bc.start)) * sstride + col;
           if (!SOPHIA) {
-            scale[u] = lr / bias1[bc.slot];  // same rounding as (lr / bias1) * m
+            scale[u] = lr / bias1[bc.slot];
             dscale[u] = denom_scale[bc.slot];
           }
         } else if (lane == 0) {
-          // A touched row outside every resident block: the host checks this
-          // flag and raises (the reference raises on a missing slot, :275-279).
           atomicOr(error_flag, 1);
         }
       }
@@ -270,25 +456,12 @@ __global__ void __launch_bounds__(256) resident_optim_kernel(
 #pragma unroll
     for (int u = 0; u < OPT_UNROLL; ++u) {
       if (!live[u]) continue;
-      const float gg = g[u] / batch_size;
-      float m1 = beta1 * mm[u] + one_m_b1 * gg;
-      float v1 = vv[u];
-      float p1 = p[u];
-      if (SOPHIA) {
-        if (update_h) v1 = beta2 * v1 + one_m_b2 * gg * gg;
-        float r = m1 / fmaxf(v1, eps);
-        r = fminf(fmaxf(r, -rho), rho);
-        p1 -= lr * r;
-      } else {
-        v1 = beta2 * v1 + one_m_b2 * gg * gg;
-        const float denom = sqrtf(v1) / dscale[u] + eps;
-        p1 -= scale[u] * m1 / denom;
-      }
-      m[soff[u]] = m1;
-      v[soff[u]] = v1;
-      param[poff[u]] = p1;
+      optim_update<SOPHIA>(g[u], mm[u], vv[u], p[u], scale[u], dscale[u], beta1, beta2,
+                           one_m_b1, one_m_b2, eps, batch_size, rho, update_h);
+      m[soff[u]] = mm[u];
+      v[soff[u]] = vv[u];
+      param[poff[u]] = p[u];
     }
-    t = te;
   }
 }
 
@@ -352,12 +525,17 @@ static int fill_components(OptimComponents& C, int n_comp, float* const* params,
   C.total = total;
   int unified = 1, col = 0;
   for (int k = 0; k < n_comp; ++k) {
-    unified &= C.pstride[k] == total && C.gstride[k] == total && C.sstride[k] == total;
+    unified &= C.pstride[k] == C.pstride[0] && C.gstride[k] == C.gstride[0] &&
+               C.sstride[k] == C.sstride[0];
     unified &= C.param[k] == C.param[0] + col && C.grad[k] == C.grad[0] + col &&
                C.m[k] == C.m[0] + col && C.v[k] == C.v[0] + col;
     col += widths[k];
   }
+  unified &= C.pstride[0] <= 64 && C.gstride[0] <= 64 && C.sstride[0] <= 64;
   C.unified = unified;
+  C.pw = (int)C.pstride[0];
+  C.gw = (int)C.gstride[0];
+  C.sw = (int)C.sstride[0];
   return TGS_OK;
 }
 
@@ -378,22 +556,40 @@ static int launch_optim(int64_t n_rows, const void* local_rows, int index_is_i64
   OptimComponents C;
   int rc = fill_components(C, n_comp, params, grads, m, v, widths, strides, lrs);
   if (rc) return rc;
-  OptimLayout L{starts, ends, slots, n_layout, block_size};
+  int shift = -1;
+  if ((block_size & (block_size - 1)) == 0)
+    for (shift = 0; ((int64_t)1 << shift) < block_size; ++shift) {
+    }
+  OptimLayout L{starts, ends, slots, n_layout, block_size, shift};
   const int threads = 256;
-  // each wavefront takes a contiguous range of >= 16 rows; at most ~8 waves
-  // per SIMD over 256 CUs
-  int64_t waves_needed = (n_rows + 15) / 16;
-  int64_t blocks = (waves_needed + 3) / 4;
-  if (blocks > 256 * 32) blocks = 256 * 32;
+  int64_t blocks;
+  if (C.unified) {
+    // round-robin groups of OPT_RUN rows; 8 wavefronts per SIMD at most
+    blocks = ((n_rows + OPT_RUN - 1) / OPT_RUN + 3) / 4;
+    if (blocks > 256 * 8) blocks = 256 * 8;
+  } else {
+    // each wavefront takes a contiguous range of >= 16 rows
+    int64_t waves_needed = (n_rows + 15) / 16;
+    blocks = (waves_needed + 3) / 4;
+    if (blocks > 256 * 32) blocks = 256 * 32;
+  }
   if (blocks < 1) blocks = 1;
-  if (index_is_i64)
-    hipLaunchKernelGGL((resident_optim_kernel<int64_t, SOPHIA>), dim3((unsigned)blocks),
-                       dim3(threads), 0, stream, n_rows, (const int64_t*)local_rows, L, bias1,
-                       denom_scale, C, beta1, beta2, eps, batch_size, rho, update_h, error_flag);
-  else
-    hipLaunchKernelGGL((resident_optim_kernel<int32_t, SOPHIA>), dim3((unsigned)blocks),
-                       dim3(threads), 0, stream, n_rows, (const int32_t*)local_rows, L, bias1,
-                       denom_scale, C, beta1, beta2, eps, batch_size, rho, update_h, error_flag);
+#define TGS_OPTIM_LAUNCH(KERNEL, IDX)                                                     \
+  hipLaunchKernelGGL((KERNEL<IDX, SOPHIA>), dim3((unsigned)blocks), dim3(threads), 0, stream,  \
+                     n_rows, (const IDX*)local_rows, L, bias1, denom_scale, C, beta1, beta2, eps, \
+                     batch_size, rho, update_h, error_flag)
+  if (C.unified) {
+    if (index_is_i64)
+      TGS_OPTIM_LAUNCH(resident_optim_unified_kernel, int64_t);
+    else
+      TGS_OPTIM_LAUNCH(resident_optim_unified_kernel, int32_t);
+  } else {
+    if (index_is_i64)
+      TGS_OPTIM_LAUNCH(resident_optim_kernel, int64_t);
+    else
+      TGS_OPTIM_LAUNCH(resident_optim_kernel, int32_t);
+  }
+#undef TGS_OPTIM_LAUNCH
   TGS_RETURN_LAUNCH(SOPHIA ? "tgs_resident_sophia_step" : "tgs_resident_adam_step");
 }
 
@@ -429,7 +625,7 @@ extern "C" int tgs_block_touch_counts(int64_t n_rows, const void* rows, int inde
   TGS_CHECK_ARG(n_layout >= 0 && n_rows >= 0, "negative size");
   if (n_layout == 0) return TGS_OK;
   TGS_CHECK_ARG(block_starts && block_ends && counts && (rows || n_rows == 0), "null pointer");
-  OptimLayout L{block_starts, block_ends, nullptr, n_layout, 0};
+  OptimLayout L{block_starts, block_ends, nullptr, n_layout, 0, -1};
   if (index_is_i64)
     hipLaunchKernelGGL(block_touch_counts_kernel<int64_t>, dim3(tgs_blocks(n_layout, 256)),
                        dim3(256), 0, stream, n_rows, (const int64_t*)rows, L, counts);

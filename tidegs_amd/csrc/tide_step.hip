@@ -130,9 +130,9 @@ __device__ __forceinline__ m3 row_covariance(const float* __restrict__ row) {
 //   [(C+1) * nb + b]    visits (sum of popcount(mask)) in block b
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(VIS_THREADS) tide_visibility_kernel(
-    uint64_t n_rows, const float* __restrict__ params, TideCams tc, int W, int H, float eps2d,
-    float near_plane, float far_plane, float radius_clip, uint32_t* __restrict__ masks,
-    uint32_t* __restrict__ counts) {
+    uint64_t n_rows, const float* __restrict__ params, uint32_t row_stride, TideCams tc, int W,
+    int H, float eps2d, float near_plane, float far_plane, float radius_clip,
+    uint32_t* __restrict__ masks, uint32_t* __restrict__ counts) {
   __shared__ CamLDS s_cam;
   __shared__ uint32_t s_cnt[TIDE_MAX_CAMS + 2];
   load_cams_lds(tc, s_cam);
@@ -142,7 +142,7 @@ __global__ void __launch_bounds__(VIS_THREADS) tide_visibility_kernel(
   const uint32_t nb = gridDim.x;
   uint32_t mask = 0;
   if (n < n_rows) {
-    const float* row = params + n * TIDE_ROW;
+    const float* row = params + n * row_stride;
     const float p[3] = {row[0], row[1], row[2]};
     const m3 Sigma = row_covariance(row);
     for (uint32_t c = 0; c < tc.C; ++c)
@@ -317,9 +317,10 @@ __device__ __forceinline__ void project_entry(
 __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
     uint32_t n_touched, const int32_t* __restrict__ touched,
     const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
-    const uint32_t* __restrict__ masks, TideCams tc, const float* __restrict__ params, int W,
-    int H, float eps2d, float near_plane, float far_plane, float radius_clip, int sh_degree,
-    uint32_t tile_size, uint32_t tw, uint32_t th, float4* __restrict__ splats,
+    const uint32_t* __restrict__ masks, TideCams tc, const float* __restrict__ params,
+    uint32_t row_stride, int W, int H, float eps2d, float near_plane, float far_plane,
+    float radius_clip, int sh_degree, uint32_t tile_size, uint32_t tw, uint32_t th,
+    float4* __restrict__ splats,
     uint32_t* __restrict__ depth_keys, uint64_t* __restrict__ entry_rects) {
   __shared__ CamLDS s_cam;
   load_cams_lds(tc, s_cam);
@@ -327,7 +328,7 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_touched) return;
   const uint32_t n = (uint32_t)touched[t];
-  const float* row = params + (uint64_t)n * TIDE_ROW;
+  const float* row = params + (uint64_t)n * row_stride;
   const float p[3] = {row[0], row[1], row[2]};
   const m3 Sigma = row_covariance(row);
   const float opac = sigmoidf_(row[10]);
@@ -434,15 +435,16 @@ __global__ void __launch_bounds__(256) tide_isect_ids_kernel(
 __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
     uint32_t n_touched, const int32_t* __restrict__ touched,
     const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
-    const uint32_t* __restrict__ masks, TideCams tc, const float* __restrict__ params, int W,
-    int H, float eps2d, float near_plane, float far_plane, float radius_clip, int sh_degree,
-    const float* __restrict__ splat_grads, float* __restrict__ grads) {
+    const uint32_t* __restrict__ masks, TideCams tc, const float* __restrict__ params,
+    uint32_t row_stride, int W, int H, float eps2d, float near_plane, float far_plane,
+    float radius_clip, int sh_degree, const float* __restrict__ splat_grads,
+    float* __restrict__ grads, uint32_t grad_stride) {
   __shared__ CamLDS s_cam;
   load_cams_lds(tc, s_cam);
   __syncthreads();
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_touched) return;
-  const float* row = params + (uint64_t)touched[t] * TIDE_ROW;
+  const float* row = params + (uint64_t)touched[t] * row_stride;
   const float p[3] = {row[0], row[1], row[2]};
   const float s[3] = {expf(row[3]), expf(row[4]), expf(row[5])};
   float qn[4], qinv;
@@ -507,7 +509,7 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
   float vq[4], vs[3];
   covar_vjp_quat_scale(qn, s, v_S, vq, vs);
   const float dot = vq[0] * qn[0] + vq[1] * qn[1] + vq[2] * qn[2] + vq[3] * qn[3];
-  float* out = grads + (uint64_t)t * TIDE_ROW;
+  float* out = grads + (uint64_t)t * grad_stride;
   out[0] = v_p[0];
   out[1] = v_p[1];
   out[2] = v_p[2];
@@ -519,6 +521,8 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
   out[10] = v_op * (1.f - opac) * opac;
 #pragma unroll
   for (int k = 0; k < 48; ++k) out[11 + k] = v_sh[k];
+  // zero the padding of a padded row so that the whole row is written
+  for (uint32_t k = TIDE_ROW; k < grad_stride; ++k) out[k] = 0.f;
 }
 
 // Camera centres: the translation of inverse(viewmat) for an affine world->camera
@@ -574,7 +578,8 @@ extern "C" uint32_t tgs_tide_row_blocks(uint64_t n_rows) {
   return (uint32_t)((n_rows + VIS_THREADS - 1) / VIS_THREADS);
 }
 
-extern "C" int tgs_tide_visibility(uint64_t n_rows, const float* params, uint32_t C,
+extern "C" int tgs_tide_visibility(uint64_t n_rows, const float* params, uint32_t row_stride,
+                                   uint32_t C,
                                    const float* viewmats, const float* Ks, const float* campos,
                                    int32_t W, int32_t H, float eps2d, float near_plane,
                                    float far_plane, float radius_clip, uint32_t* masks,
@@ -584,9 +589,10 @@ extern "C" int tgs_tide_visibility(uint64_t n_rows, const float* params, uint32_
   if (n_rows == 0) return TGS_OK;
   TGS_CHECK_ARG(params && viewmats && Ks && campos && masks && counts, "tide_visibility: null");
   TGS_CHECK_ARG(n_rows < (1ull << 31), "tide_visibility: at most 2^31-1 rows");
+  TGS_CHECK_ARG(row_stride >= TIDE_ROW, "tide step: row_stride must be >= %d", TIDE_ROW);
   TideCams tc{viewmats, Ks, campos, C};
   hipLaunchKernelGGL(tide_visibility_kernel, dim3(tgs_tide_row_blocks(n_rows)), dim3(VIS_THREADS),
-                     0, stream, n_rows, params, tc, W, H, eps2d, near_plane, far_plane,
+                     0, stream, n_rows, params, row_stride, tc, W, H, eps2d, near_plane, far_plane,
                      radius_clip, masks, counts);
   TGS_RETURN_LAUNCH("tgs_tide_visibility");
 }
@@ -613,10 +619,11 @@ extern "C" int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* mas
 extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched,
                                     const int32_t* visit_base, const int32_t* visits,
                                     const uint32_t* masks, uint32_t C, const float* params,
-                                    const float* viewmats, const float* Ks, const float* campos,
-                                    int32_t W, int32_t H, float eps2d, float near_plane,
-                                    float far_plane, float radius_clip, int32_t sh_degree,
-                                    uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
+                                    uint32_t row_stride, const float* viewmats, const float* Ks,
+                                    const float* campos, int32_t W, int32_t H, float eps2d,
+                                    float near_plane, float far_plane, float radius_clip,
+                                    int32_t sh_degree, uint32_t tile_size, uint32_t tile_width,
+                                    uint32_t tile_height,
                                     float* splats, uint32_t* depth_keys, uint64_t* entry_rects,
                                     hipStream_t stream) {
   int rc = check_cams(C);
@@ -630,9 +637,11 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched,
                 tile_height);
   TGS_CHECK_ARG(sh_degree >= 0 && sh_degree <= 3, "tide step: sh_degree must be in [0,3]");
   TGS_CHECK_ARG(((uintptr_t)splats & 15) == 0, "tide_project_fwd: splats must be 16-byte aligned");
+  TGS_CHECK_ARG(row_stride >= TIDE_ROW, "tide step: row_stride must be >= %d", TIDE_ROW);
   TideCams tc{viewmats, Ks, campos, C};
   hipLaunchKernelGGL(tide_project_fwd_kernel, dim3(tgs_blocks(n_touched, 256)), dim3(256), 0,
-                     stream, n_touched, touched, visit_base, visits, masks, tc, params, W, H,
+                     stream, n_touched, touched, visit_base, visits, masks, tc, params, row_stride,
+                     W, H,
                      eps2d, near_plane, far_plane, radius_clip, sh_degree, tile_size, tile_width,
                      tile_height, (float4*)splats, depth_keys, entry_rects);
   TGS_RETURN_LAUNCH("tgs_tide_project_fwd");
@@ -739,10 +748,11 @@ extern "C" int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const flo
 extern "C" int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched,
                                     const int32_t* visit_base, const int32_t* visits,
                                     const uint32_t* masks, uint32_t C, const float* params,
-                                    const float* viewmats, const float* Ks, const float* campos,
-                                    int32_t W, int32_t H, float eps2d, float near_plane,
-                                    float far_plane, float radius_clip, int32_t sh_degree,
-                                    const float* splat_grads, float* grads, hipStream_t stream) {
+                                    uint32_t row_stride, const float* viewmats, const float* Ks,
+                                    const float* campos, int32_t W, int32_t H, float eps2d,
+                                    float near_plane, float far_plane, float radius_clip,
+                                    int32_t sh_degree, const float* splat_grads, float* grads,
+                                    uint32_t grad_stride, hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;
   if (n_touched == 0) return TGS_OK;
@@ -750,9 +760,12 @@ extern "C" int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched,
                     splat_grads && grads,
                 "tide_project_bwd: null");
   TGS_CHECK_ARG(sh_degree >= 0 && sh_degree <= 3, "tide step: sh_degree must be in [0,3]");
+  TGS_CHECK_ARG(row_stride >= TIDE_ROW && grad_stride >= TIDE_ROW,
+                "tide step: row_stride and grad_stride must be >= %d", TIDE_ROW);
   TideCams tc{viewmats, Ks, campos, C};
   hipLaunchKernelGGL(tide_project_bwd_kernel, dim3(tgs_blocks(n_touched, 256)), dim3(256), 0,
-                     stream, n_touched, touched, visit_base, visits, masks, tc, params, W, H,
-                     eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads, grads);
+                     stream, n_touched, touched, visit_base, visits, masks, tc, params, row_stride,
+                     W, H, eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads, grads,
+                     grad_stride);
   TGS_RETURN_LAUNCH("tgs_tide_project_bwd");
 }

@@ -9,8 +9,9 @@ that bookkeeping; the update of all 59 columns runs as ONE HIP launch
 (``tgs_resident_adam_step``) instead of six Triton launches, with the
 row -> slot mapping resolved on the GPU.
 
-Moments live in one ``[slots * block_size, 59]`` array per moment (row-contiguous),
-so a touched row's state is a single 236-byte span.
+Moments live in one ``[slots * block_size, 64]`` array per moment (59 columns
+in the resident table's CACHE order plus 5 padding columns), so a touched
+row's state is one 256-byte span of two whole cache lines.
 
 ``GPUResidentSophia`` uses the same slots with a diagonal-Hessian EMA instead of
 the second moment (Liu et al. 2023; no TideGS counterpart, see the kernel).
@@ -39,6 +40,10 @@ class GPUResidentAdam:
         ("features_rest", "_features_rest", 45, 5),
     )
     TOTAL_WIDTH = sum(spec[2] for spec in COMPONENT_SPECS)
+    # Row pitch of the moment tables: 64 floats, so that every state row is two
+    # whole 128-byte lines (a 59-float row straddles three lines, and the
+    # partial lines cost a read-modify-write on every update).
+    STATE_PITCH = 64
     # Column offsets of each component inside the unified state rows: the
     # resident table's CACHE column order (storage/block_reader.py:35-44), so
     # that a [N,59] parameter table, its [T,59] gradient rows and the state rows
@@ -78,8 +83,8 @@ class GPUResidentAdam:
         self._layout_key = None   # cached block layout (see _layout_tables)
         self._layout_cached = None
         self._resident_epoch = 0
-        self._exp_avg: Optional[torch.Tensor] = None     # [slots*block, 59]
-        self._exp_avg_sq: Optional[torch.Tensor] = None  # [slots*block, 59]
+        self._exp_avg: Optional[torch.Tensor] = None     # [slots*block, STATE_PITCH]
+        self._exp_avg_sq: Optional[torch.Tensor] = None  # [slots*block, STATE_PITCH]
         self._bias_correction1: Optional[torch.Tensor] = None
         self._denom_scale: Optional[torch.Tensor] = None
         self._error_flag = torch.zeros(1, dtype=torch.int32, device=self.device)
@@ -101,7 +106,7 @@ class GPUResidentAdam:
 
     # ---- bookkeeping (host) -------------------------------------------------
     def _physical_state_bytes(self) -> int:
-        return int(self._allocated_slots * self.block_size * self.TOTAL_WIDTH * 2 * 4)
+        return int(self._allocated_slots * self.block_size * self.STATE_PITCH * 2 * 4)
 
     def _update_state_stats(self) -> None:
         self._stats["resident_target_blocks"] = len(self._resident_blocks)
@@ -138,7 +143,7 @@ class GPUResidentAdam:
         old_slots = self._allocated_slots
         old_rows = old_slots * self.block_size
         new_rows = target * self.block_size
-        avg = torch.empty((new_rows, self.TOTAL_WIDTH), dtype=torch.float32, device=self.device)
+        avg = torch.empty((new_rows, self.STATE_PITCH), dtype=torch.float32, device=self.device)
         avg_sq = torch.empty_like(avg)
         if old_rows:
             avg[:old_rows].copy_(self._exp_avg)
@@ -169,7 +174,7 @@ class GPUResidentAdam:
         self._allocated_slots = target
 
     def _clear_slots(self, slots: List[int]) -> None:
-        row_words = self.block_size * self.TOTAL_WIDTH
+        row_words = self.block_size * self.STATE_PITCH
         s = N.stream_handle(self.device)
         for slot in slots:
             for buf in (self._exp_avg, self._exp_avg_sq):
@@ -321,7 +326,7 @@ class GPUResidentAdam:
             m_p[k] = self._exp_avg.data_ptr() + 4 * col
             v_p[k] = self._exp_avg_sq.data_ptr() + 4 * col
             widths[k] = width
-            strides[3 * k + 0], strides[3 * k + 1], strides[3 * k + 2] = ps, gs, self.TOTAL_WIDTH
+            strides[3 * k + 0], strides[3 * k + 1], strides[3 * k + 2] = ps, gs, self.STATE_PITCH
             lrs[k] = component_lrs[name]
         hooks = getattr(self, "kernel_hooks", None)
         if hooks:

@@ -90,6 +90,15 @@ def _intrinsics(f: float, W: int, H: int) -> torch.Tensor:
     return torch.tensor([[f, 0.0, W / 2.0], [0.0, f, H / 2.0], [0.0, 0.0, 1.0]])
 
 
+def padded_table(p: torch.Tensor, pitch: int = 64) -> torch.Tensor:
+    """The same [N, 59] table stored at a row pitch of ``pitch`` floats (the
+    extra columns zero): a [N, 59] view whose rows start on 256-byte
+    boundaries at pitch 64, so that a row is exactly two cache lines."""
+    out = torch.zeros((p.shape[0], pitch), dtype=p.dtype, device=p.device)
+    out[:, :ROW] = p
+    return out[:, :ROW]
+
+
 def cfg1(seed: int = 0, n: int = 10_000) -> Scene:
     """10k Gaussians, one 256x256 pinhole (fx=fy=256) at the origin looking +z."""
     g = torch.Generator().manual_seed(seed)

@@ -33,6 +33,9 @@ from . import _native as N
 from .resident_optim import GPUResidentAdam, GPUResidentSophia
 
 ROW = 59
+# Row pitch of the compact gradient rows: whole 256-byte lines (see
+# scenes.padded_table for the resident table's padded layout).
+GRAD_PITCH = 64
 # CACHE-order column slices of the optimizer components (unified names)
 _CACHE_COLS = {
     "xyz": (0, 3),
@@ -103,9 +106,11 @@ class TideStep:
                  sophia_rho: float = 0.04, gt_div: float = 255.0, keep_isect_ids: bool = False):
         if params.dim() != 2 or params.shape[1] != ROW or params.dtype != torch.float32:
             raise ValueError("params must be a float32 [N, 59] table (CACHE column order)")
-        if not params.is_cuda or not params.is_contiguous():
-            raise ValueError("params must be a contiguous GPU tensor")
+        if not params.is_cuda or params.stride(1) != 1 or not ROW <= params.stride(0) <= 64:
+            raise ValueError("params must be a GPU table with contiguous rows at a pitch of "
+                             "59..64 floats (59: dense, 64: padded to 256-byte rows)")
         self.params = params
+        self.row_stride = int(params.stride(0))
         self.device = params.device
         self.W, self.H = int(width), int(height)
         self.tw = -(-self.W // self.TILE)
@@ -198,7 +203,8 @@ class TideStep:
         masks = self._buf("masks", n, torch.int32)
         counts = self._buf("counts", (C + 2) * nb, torch.int32)
         self._begin("visibility")
-        N.call("tgs_tide_visibility", n, N.ptr(P), C, N.ptr(viewmats), N.ptr(Ks), N.ptr(campos),
+        N.call("tgs_tide_visibility", n, N.ptr(P), self.row_stride, C, N.ptr(viewmats), N.ptr(Ks),
+               N.ptr(campos),
                W, H, self.eps2d, self.near, self.far, self.radius_clip, N.ptr(masks),
                N.ptr(counts), s)
         offs = self._buf("offs", (C + 2) * nb, torch.int32)
@@ -227,7 +233,8 @@ class TideStep:
         rects = self._buf("entry_rects", max(V, 1), torch.int64)
         self._begin("project_fwd")
         N.call("tgs_tide_project_fwd", T, N.ptr(touched), N.ptr(visit_base), N.ptr(visits),
-               N.ptr(masks), C, N.ptr(P), N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H,
+               N.ptr(masks), C, N.ptr(P), self.row_stride, N.ptr(viewmats), N.ptr(Ks),
+               N.ptr(campos), W, H,
                self.eps2d, self.near, self.far, 0.0, self.sh_degree, self.TILE, tw, th,
                N.ptr(splats), N.ptr(dkeys), N.ptr(rects), s)
         self._end()
@@ -314,12 +321,13 @@ class TideStep:
         self._end()
 
         # 5. per touched row: projection + SH + activation backward
-        grads = self._buf("grads", max(T, 1) * ROW, torch.float32).view(-1, ROW)[:T]
+        grads = self._buf("grads", max(T, 1) * GRAD_PITCH, torch.float32).view(-1, GRAD_PITCH)
+        grads = grads[:T, :ROW]
         self._begin("project_bwd")
         N.call("tgs_tide_project_bwd", T, N.ptr(touched), N.ptr(visit_base), N.ptr(visits),
-               N.ptr(masks), C, N.ptr(P), N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H,
-               self.eps2d, self.near, self.far, 0.0, self.sh_degree, N.ptr(sgrads),
-               N.ptr(grads), s)
+               N.ptr(masks), C, N.ptr(P), self.row_stride, N.ptr(viewmats), N.ptr(Ks),
+               N.ptr(campos), W, H, self.eps2d, self.near, self.far, 0.0, self.sh_degree,
+               N.ptr(sgrads), N.ptr(grads), GRAD_PITCH, s)
         self._end()
         if self._timing:
             self.last_visible_entries = int((splats[: V * 12].view(-1, 12)[:, 7] > 0).sum())
