@@ -16,11 +16,17 @@
 //       power = log2(opacity) - sigma * log2(e)
 //     costs five FMAs per pixel and alpha = exp2(power) (v_exp_f32);
 //   * the bounding box of the Gaussian's alpha >= 1/255 ellipse
-//     (0.5 d^T Q d <= ln(255 opacity)), which is exact: pixels outside it
-//     are skipped by the reference too.
-// Every wavefront then compacts the batch to the Gaussians whose box meets its
-// own 16x4 pixel strip; each lane marks which of those reach its pixel and
-// walks only its own marks (lane-compacted iteration, below).
+//     (0.5 d^T Q d <= ln(255 opacity)): pixels outside it are skipped by the
+//     reference too.
+// Every wavefront compacts the batch to the Gaussians whose box meets its own
+// pixel strip, and computes for each of them, one lane per (Gaussian, pixel
+// row), the row's interval of pixels that can reach alpha >= 1/255: a
+// conservative superset of the pixels that pass the reference's test (the
+// quadratic's roots with a bound on the rounding of the per-pixel
+// evaluation).  The intervals, as a 64-bit pixel mask per Gaussian, give each
+// lane the list positions its pixel may use; the lane walks only those, and
+// the exact per-pixel test decides inside the walk (lane-compacted
+// iteration).
 // In the backward each lane leaves its per-(Gaussian, pixel) terms in a
 // compact LDS pair buffer and owner lanes sum them per Gaussian as moments
 // (sum v_sigma dx, dx^2, ...), turned into mean2d / conic / opacity gradients
@@ -30,6 +36,8 @@
 // gsplat's SoA tensors (drop-in op) and the packed 48-byte splat records of the
 // fused resident step.
 #pragma once
+
+#include <type_traits>
 
 #include "tgs_common.cuh"
 
@@ -125,7 +133,12 @@ struct StagedGeo {
   float4 g0;   // x, y, A = -0.5 log2e a, B = -log2e b
   float2 g1;   // C = -0.5 log2e c, L = log2(opacity)
   float4 box;  // x_lo, x_hi, y_lo, y_hi of the alpha >= 1/255 ellipse
+  float4 cov;  // row-coverage constants (cover_row): 2n, 1/n, k0, mode
 };
+
+#define RS_COVER_QUAD 0.f  // bounded: the row intervals come from the quadratic
+#define RS_COVER_ALL 1.f   // no bound (degenerate conic, non-finite values): every pixel
+#define RS_COVER_NONE 2.f  // never visible (opacity <= 1/255)
 
 template <int CDIM>
 __device__ __forceinline__ StagedGeo stage_geo(const SplatData<CDIM>& s) {
@@ -137,8 +150,10 @@ __device__ __forceinline__ StagedGeo stage_geo(const SplatData<CDIM>& s) {
   // extents are |dx| <= sqrt(2 t c / det), |dy| <= sqrt(2 t a / det).
   const float t = logf(255.f * s.op);
   const float det = s.a * s.c - s.b * s.b;
+  o.cov = make_float4(0.f, 0.f, 0.f, RS_COVER_ALL);
   if (!(s.op > 0.f) || t <= 0.f) {
     o.box = make_float4(INFINITY, -INFINITY, INFINITY, -INFINITY);  // never visible
+    o.cov.w = RS_COVER_NONE;
   } else if (!(det > 0.f) || !(s.a > 0.f) || !(s.c > 0.f)) {
     o.box = make_float4(-INFINITY, INFINITY, -INFINITY, INFINITY);  // no bound: never cull
   } else {
@@ -146,6 +161,18 @@ __device__ __forceinline__ StagedGeo stage_geo(const SplatData<CDIM>& s) {
     const float ex = sqrtf(2.f * tt * s.c / det) * 1.001f + 1e-3f;
     const float ey = sqrtf(2.f * tt * s.a / det) * 1.001f + 1e-3f;
     o.box = make_float4(s.x - ex, s.x + ex, s.y - ey, s.y + ey);
+    // cover_row: n = -2A > 0; delta bounds the rounding of the per-pixel
+    // evaluation (three FMAs: < 3 ulp of the largest term, itself <= M on
+    // the box) with a wide margin, 2^-17 M
+    const float A = o.g0.z, B = o.g0.w, C = o.g1.x;
+    const float M = fabsf(A) * ex * ex + fabsf(B) * ex * ey + fabsf(C) * ey * ey + fabsf(L) + 8.f;
+    const float delta = M * 0x1p-17f + 1e-6f;
+    const float n = -2.f * A;
+    if (__builtin_isfinite(o.box.x) && __builtin_isfinite(o.box.y) &&
+        __builtin_isfinite(o.box.z) && __builtin_isfinite(o.box.w) && __builtin_isfinite(L) &&
+        __builtin_isfinite(M) && n > 0.f)
+      o.cov = make_float4(2.f * n, __builtin_amdgcn_rcpf(n), (L - RS_LOG2_MIN_ALPHA) + delta,
+                          RS_COVER_QUAD);
   }
   return o;
 }
@@ -190,42 +217,96 @@ __device__ __forceinline__ int build_wave_list(const float4* s_box, uint8_t* s_l
 }
 
 // ---------------------------------------------------------------------------
-// Lane-compacted iteration.  A wavefront's list holds every Gaussian whose box
-// meets its strip, but a small Gaussian covers only a few of its 64 pixels,
-// so looping over the list with one pixel per lane leaves most lanes idle.
-// Instead every lane first records, in a bitmask over list positions, which
-// Gaussians actually reach its pixel (the cheap alpha test), and then walks
-// only its own set bits in list order: the wavefront iterates
-// max_lane(|own set|) times instead of |list| times.
+// Coverage of one pixel row by a staged Gaussian: the TILE-bit mask of pixel
+// centres px = px0 + j (j < TILE) on row py that can pass the alpha test.
+//
+// With dx = gx - px and dy = gy - py, power = A dx^2 + B dx dy + C dy^2 + L
+// (A < 0 for a bounded Gaussian).  On the row it is a quadratic in dx, and
+// power >= thr - delta holds between its roots:
+//   A dx^2 + h dx + k >= 0,  h = B dy,  k = C dy^2 + k0,  k0 = L - thr + delta,
+//   dx in [(h - sqrt(D)) / n, (h + sqrt(D)) / n],  n = -2A,  D = h^2 + 2 n k.
+// delta (stage_geo) covers the rounding of the per-pixel evaluation, and the
+// pixel interval is widened by far more than the rounding of the roots (the
+// hardware sqrt and reciprocal are within 1 ulp; the margin is 2^-10 of the
+// interval's extent plus 1e-3 px), so the mask contains every pixel whose
+// evaluated power passes.  Degenerate or non-finite Gaussians cover every
+// pixel (the exact test decides), invisible ones none.
 // ---------------------------------------------------------------------------
-template <int BLOCK>
-struct LaneMask {
-  static constexpr int WORDS = BLOCK / 32;
-  uint32_t w[WORDS];
-};
+template <int TILE>
+__device__ __forceinline__ uint32_t cover_row(const float4& g0, const float2& g1,
+                                              const float4& box, const float4& cov, float px0,
+                                              float py) {
+  constexpr uint32_t FULL = (1u << TILE) - 1u;
+  const float dy = g0.y - py;
+  const float h = g0.w * dy;
+  const float k = fmaf(g1.x * dy, dy, cov.z);
+  const float D = fmaf(h, h, cov.x * k);
+  const float half = __builtin_amdgcn_sqrtf(fmaxf(D, 0.f)) * cov.y;
+  const float cen = h * cov.y;
+  const float base = g0.x - px0;
+  const float m = 1e-3f + 0x1p-10f * (fabsf(cen) + half) + 0x1p-20f * fabsf(base);
+  // px = gx - dx  =>  j = px - px0 in [base - cen - half, base - cen + half]
+  const float lo = fmaxf(base - cen - half - m, -1.f);
+  const float hi = fminf(base - cen + half + m, (float)TILE);
+  const int jlo = max((int)ceilf(lo), 0);
+  const int jhi = min((int)floorf(hi), TILE - 1);
+  const uint32_t quad = (FULL >> (TILE - 1 - max(jhi, 0))) & (FULL << min(jlo, TILE - 1));
+  const bool in = D >= 0.f && jlo <= jhi && py >= box.z && py <= box.w;
+  return cov.w == RS_COVER_QUAD ? (in ? quad : 0u) : (cov.w == RS_COVER_ALL ? FULL : 0u);
+}
 
-// Bit li of the mask is set iff list entry li passes the pixel test of
-// rasterize_to_pixels_{fwd,bwd}.cu (sigma >= 0 and alpha >= 1/255) and, in
-// the backward, its batch index is not behind the pixel's last contributor.
-template <int BLOCK>
-__device__ __forceinline__ void lane_masks(LaneMask<BLOCK>& m, const uint8_t* list, int n_list,
-                                           const float4* s_g0, const float2* s_g1, float px,
-                                           float py, bool active, int t_min) {
-#pragma unroll
-  for (int W = 0; W < LaneMask<BLOCK>::WORDS; ++W) {
-    uint32_t mw = 0;
-    if (W * 32 < n_list) {
-      const int lim = min(32, n_list - W * 32);
-      for (int bb = 0; bb < lim; ++bb) {
-        const int t = list[W * 32 + bb];
-        const float4 g0 = s_g0[t];
-        const float2 g1 = s_g1[t];
-        const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
-        const bool ok = t >= t_min && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
-        mw |= (ok ? 1u : 0u) << bb;
-      }
+// Pixel-row masks of the first n_list entries of a wavefront's list: lane
+// (e, r) computes entry li0 + e, row r; the ROWS masks of an entry form its
+// 64-bit pixel mask (bit r * TILE + j = pixel (r, j) of the strip), which is
+// stored to s_em and also returned to lane e * ROWS.
+template <int TILE, int BATCH>
+__device__ __forceinline__ void strip_masks(const uint8_t* s_list, int n_list, const float4* s_g0,
+                                            const float2* s_g1, const float4* s_box,
+                                            const float4* s_cov, uint64_t* s_em, float px0,
+                                            float py0, uint64_t alive) {
+  using RM = typename std::conditional<TILE == 16, uint16_t, uint8_t>::type;
+  constexpr int ROWS = 64 / TILE;
+  constexpr int PER = 64 / ROWS;  // entries per pass
+  const int lane = threadIdx.x & 63;
+  const int e = lane / ROWS, r = lane % ROWS;
+  const uint32_t alive_row = (uint32_t)(alive >> (r * TILE)) & ((1u << TILE) - 1u);
+  for (int li0 = 0; li0 < n_list; li0 += PER) {
+    const int li = li0 + e;
+    if (li < n_list) {
+      const int t = s_list[li];
+      const uint32_t m =
+          cover_row<TILE>(s_g0[t], s_g1[t], s_box[t], s_cov[t], px0, py0 + (float)r);
+      reinterpret_cast<RM*>(&s_em[li])[r] = (RM)(m & alive_row);
     }
-    m.w[W] = active ? mw : 0u;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// This lane's bits of the list masks: bit li of word li / 32 is bit `lane` of
+// s_em[li], for li in [li_min, n_list).
+template <int WORDS>
+__device__ __forceinline__ void lane_bits(const uint64_t* s_em, int n_list, int li_min,
+                                          uint32_t (&mw)[WORDS]) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t* em32 = reinterpret_cast<const uint32_t*>(s_em) + (lane >> 5);
+  const int sh = lane & 31;
+#pragma unroll
+  for (int W = 0; W < WORDS; ++W) {
+    uint32_t w = 0;
+    const int lim = min(32, n_list - W * 32);
+    const uint32_t* e = em32 + 2 * W * 32;
+    int bb = 0;
+    for (; bb + 2 <= lim; bb += 2) {
+      const uint32_t d0 = e[2 * bb], d1 = e[2 * bb + 2];
+      w |= (((d0 >> sh) & 1u) | (((d1 >> sh) & 1u) << 1)) << bb;
+    }
+    if (bb < lim) w |= ((e[2 * bb] >> sh) & 1u) << bb;
+    const int lo = li_min - W * 32;  // clear positions below li_min
+    if (lo >= 32) w = 0u;
+    else if (lo > 0) w &= ~((1u << lo) - 1u);
+    mw[W] = w;
   }
 }
 
@@ -244,11 +325,14 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
   constexpr int WAVES = BLOCK / 64;
   constexpr int ROWS = 64 / TILE;  // pixel rows per wavefront
   constexpr int BATCH = RF_BATCH < BLOCK ? RF_BATCH : BLOCK;
+  constexpr int WORDS = BATCH / 32;
   __shared__ float4 s_g0[BATCH];
   __shared__ float2 s_g1[BATCH];
   __shared__ float4 s_box[BATCH];
+  __shared__ float4 s_cov[BATCH];
   __shared__ float s_col[BATCH][CDIM];
   __shared__ uint8_t s_list[WAVES][BATCH];
+  __shared__ uint64_t s_em[WAVES][BATCH];
 
   const uint32_t cam = blockIdx.x;
   const uint32_t ty = blockIdx.y, tx = blockIdx.z;
@@ -289,40 +373,46 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
       s_g0[tr] = sg.g0;
       s_g1[tr] = sg.g1;
       s_box[tr] = sg.box;
+      s_cov[tr] = sg.cov;
 #pragma unroll
       for (int k = 0; k < CDIM; ++k) s_col[tr][k] = s.col[k];
     }
     __syncthreads();
     const int32_t batch_size = min(BATCH, range_end - batch_start);
-    int n_list = 0;
-    if (tgs_ballot(!done))
-      n_list = build_wave_list<BATCH>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1);
-    LaneMask<BATCH> m;
-    lane_masks<BATCH>(m, s_list[wave], n_list, s_g0, s_g1, px, py, !done, 0);
+    const uint64_t alive = tgs_ballot(!done);
+    if (!alive) continue;
+    const int n_list =
+        build_wave_list<BATCH>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1);
+    strip_masks<TILE, BATCH>(s_list[wave], n_list, s_g0, s_g1, s_box, s_cov, s_em[wave], wx0, wy0,
+                             alive);
+    uint32_t mw[WORDS];
+    lane_bits<WORDS>(s_em[wave], n_list, 0, mw);
 #pragma unroll
-    for (int W = 0; W < LaneMask<BATCH>::WORDS; ++W) {
+    for (int W = 0; W < WORDS; ++W) {
       if (W * 32 >= n_list) break;
-      uint32_t mw = m.w[W];
+      uint32_t m = done ? 0u : mw[W];
       while (true) {
-        const bool act = mw != 0u && !done;
+        const bool act = m != 0u && !done;
         if (!tgs_ballot(act)) break;
         if (act) {
-          const int bit = __builtin_ctz(mw);
-          mw &= mw - 1u;
+          const int bit = __builtin_ctz(m);
+          m &= m - 1u;
           const int t = s_list[wave][W * 32 + bit];
           const float4 g0 = s_g0[t];
           const float2 g1 = s_g1[t];
           const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
-          const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
-          const float next_T = T * (1.f - alpha);
-          if (next_T <= 1e-4f) {
-            done = true;
-          } else {
-            const float vis = alpha * T;
+          if (!(power > g1.y || power < RS_LOG2_MIN_ALPHA)) {
+            const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
+            const float next_T = T * (1.f - alpha);
+            if (next_T <= 1e-4f) {
+              done = true;
+            } else {
+              const float vis = alpha * T;
 #pragma unroll
-            for (int k = 0; k < CDIM; ++k) pix[k] += s_col[t][k] * vis;
-            cur_idx = (uint32_t)(batch_start + t);
-            T = next_T;
+              for (int k = 0; k < CDIM; ++k) pix[k] += s_col[t][k] * vis;
+              cur_idx = (uint32_t)(batch_start + t);
+              T = next_T;
+            }
           }
         }
       }
@@ -339,16 +429,29 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
   }
 }
 
+// Inclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl_up(v, off, 64);
+    if ((int)(threadIdx.x & 63) >= off) v += o;
+  }
+  return v;
+}
+
 // ---------------------------------------------------------------------------
 // Backward.  Per batch and wavefront:
-//   1. test     as in the forward: each lane's bitmask over the list (alpha
-//               test and last-contributor bound); the wavefront's ballot of
-//               each entry is that Gaussian's pixel mask, and a running sum of
-//               their popcounts gives each entry's slot range in a compact
-//               (Gaussian, pixel) pair buffer;
-//   2. walk     each lane walks its own entries back to front (T, colour
-//               buffer) and leaves (alpha T, v_sigma) in the entry's slot
-//               range at its rank among the entry's pixels;
+//   1. masks    as in the forward: the list of entries whose box meets the
+//               strip, each entry's 64-bit pixel mask (rows' coverage, lanes
+//               that still composite part of the batch), a prefix sum of the
+//               masks' popcounts giving each entry's slot range in a
+//               (Gaussian, pixel) pair buffer, and each lane's bits over the
+//               list (positions behind its own last contributor cleared);
+//   2. walk     each lane walks its own entries back to front, applies the
+//               exact test, carries T and the colour buffer, and leaves
+//               (alpha T, v_sigma) in the entry's slot range at its rank among
+//               the entry's pixels (slots of pixels that fail the test or
+//               never composite the entry stay zero);
 //   3. owners   lanes 4e..4e+3 own entry e of a group of 16, each summing the
 //               moments (v_sigma dx, dy, dx^2, dx dy, dy^2, v_sigma, colour
 //               terms, |v_mean2d|) over the pairs of its 16 pixel lanes; a quad
@@ -383,12 +486,9 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   __shared__ float s_vrc[BLOCK][CDIM];  // dL/dcolor of each pixel
   __shared__ int32_t s_id[BATCH];
   __shared__ uint8_t s_list[WAVES][BATCH];
-  // boxes are dead once the lists are built (barrier), then the pair buffer
-  // (alpha T, v_sigma) takes their place
-  __shared__ union {
-    float4 box[BATCH];
-    float2 pair[WAVES][RB_PAIRS];
-  } s_u;
+  __shared__ float4 s_box[BATCH];
+  __shared__ float4 s_cov[BATCH];
+  __shared__ float2 s_pair[WAVES][RB_PAIRS];  // (alpha T, v_sigma)
   __shared__ uint64_t s_em[WAVES][BATCH];         // pixel mask of each list entry
   __shared__ uint16_t s_po[WAVES][BATCH + 1];     // first pair slot of each list entry
   __shared__ float s_stage[WAVES][16 * NA];
@@ -434,7 +534,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   }
   // T_final * ra * v_ra - T_final * ra * bg_dot = ra * tf_term
   const float tf_term = T_final * v_ra - T_final * bg_dot;
-  const int32_t bin_final = inside ? last_ids[pid] : 0;
+  const int32_t bin_final = inside ? last_ids[pid] : -1;
   const int32_t wave_bin_final = tgs_wave_max_i32(bin_final);
   const bool absg = sink.absgrad();
   const int nval = absg ? NA : NV;
@@ -453,43 +553,54 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
       const StagedGeo sg = stage_geo<CDIM>(s);
       s_g0[tr] = sg.g0;
       s_g1[tr] = sg.g1;
-      s_u.box[tr] = sg.box;
+      s_box[tr] = sg.box;
+      s_cov[tr] = sg.cov;
       s_id[tr] = g;
 #pragma unroll
       for (int k = 0; k < CDIM; ++k) s_col[tr][k] = s.col[k];
     }
     __syncthreads();
+    // batch entry t is global index batch_end - t; a pixel composites the
+    // entries at or before its last contributor: t >= t_min
+    const int t_min = batch_end - bin_final;
+    const uint64_t alive = tgs_ballot(inside && t_min < batch_size);
     // entries with global index > wave_bin_final contribute to no pixel of this wave
     const int j_lo = max(0, batch_end - wave_bin_final);
-    const int n_list =
-        build_wave_list<BATCH>(s_u.box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1);
-    // 1. test; batch entry t is global index batch_end - t: at or before bin_final
-    const int t_min = batch_end - bin_final;
+    int n_list = 0;
+    if (alive)
+      n_list =
+          build_wave_list<BATCH>(s_box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1);
+    // 1. pixel masks, slot ranges and this lane's bits over the list
     uint32_t m[WORDS];
-    uint32_t n_pairs = 0;  // wave-uniform
 #pragma unroll
-    for (int W = 0; W < WORDS; ++W) {
-      uint32_t mw = 0;
-      for (int bb = 0; bb < 32 && W * 32 + bb < n_list; ++bb) {
-        const int li = W * 32 + bb;
-        const int t = s_list[wave][li];
-        const float4 g0 = s_g0[t];
-        const float2 g1 = s_g1[t];
-        const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
-        const bool ok =
-            inside && t >= t_min && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
-        mw |= (ok ? 1u : 0u) << bb;
-        const uint64_t em = tgs_ballot(ok);
-        if (lane == 0) {
-          s_em[wave][li] = em;
-          s_po[wave][li] = (uint16_t)n_pairs;
+    for (int W = 0; W < WORDS; ++W) m[W] = 0u;
+    uint32_t n_pairs = 0;  // wave-uniform
+    if (n_list) {
+      strip_masks<TILE, BATCH>(s_list[wave], n_list, s_g0, s_g1, s_box, s_cov, s_em[wave], wx0, wy0,
+                               alive);
+      const uint32_t cnt = lane < n_list ? (uint32_t)__popcll(s_em[wave][lane]) : 0u;
+      const uint32_t inc = wave_incl_scan(cnt);
+      if (lane < n_list) s_po[wave][lane] = (uint16_t)(inc - cnt);
+      n_pairs = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+      if (lane == 63) s_po[wave][n_list] = (uint16_t)inc;
+      // list positions before li_min hold entries behind this lane's last
+      // contributor (the list is ascending in t)
+      int li_min = 0;
+      if (t_min > 0) {
+        int lo = 0, hi = n_list;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if ((int)s_list[wave][mid] < t_min) lo = mid + 1;
+          else hi = mid;
         }
-        n_pairs += (uint32_t)__popcll(em);
+        li_min = lo;
       }
-      m[W] = mw;
+      lane_bits<WORDS>(s_em[wave], n_list, li_min, m);
+      if (!((alive >> lane) & 1ull)) {
+#pragma unroll
+        for (int W = 0; W < WORDS; ++W) m[W] = 0u;
+      }
     }
-    if (lane == 0) s_po[wave][n_list] = (uint16_t)n_pairs;
-    __syncthreads();  // every wavefront is past its list build: boxes are dead
     int a = 0;        // first list entry of the current segment
     while (a < n_list) {
       const uint32_t base = s_po[wave][a];
@@ -504,6 +615,13 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
         }
         e_end = lo;
       }
+      // zero the segment's slots: pixels that fail the exact test or do not
+      // composite an entry leave theirs untouched
+      const uint32_t seg_pairs = (uint32_t)s_po[wave][e_end] - base;
+      for (uint32_t s = lane; s < seg_pairs; s += 64) s_pair[wave][s] = make_float2(0.f, 0.f);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       // 2. per-pixel walk over entries [a, e_end), back to front
 #pragma unroll
       for (int W = 0; W < WORDS; ++W) {
@@ -520,23 +638,25 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
             const float4 g0 = s_g0[t];
             const float2 g1 = s_g1[t];
             const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
-            const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
-            const float alpha = fminf(0.999f, raw);
-            const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
-            T *= ra;
-            const float fac = alpha * T;
-            float v_alpha = ra * tf_term;
+            if (!(power > g1.y || power < RS_LOG2_MIN_ALPHA)) {
+              const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
+              const float alpha = fminf(0.999f, raw);
+              const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
+              T *= ra;
+              const float fac = alpha * T;
+              float v_alpha = ra * tf_term;
 #pragma unroll
-            for (int k = 0; k < CDIM; ++k) {
-              const float ck = s_col[t][k];
-              v_alpha += (ck * T - buffer[k] * ra) * v_rc[k];
-              buffer[k] += ck * fac;
+              for (int k = 0; k < CDIM; ++k) {
+                const float ck = s_col[t][k];
+                v_alpha += (ck * T - buffer[k] * ra) * v_rc[k];
+                buffer[k] += ck * fac;
+              }
+              // reference: the sigma terms only where alpha was not clamped
+              const float v_sigma = raw <= 0.999f ? -raw * v_alpha : 0.f;
+              const uint32_t slot = (uint32_t)s_po[wave][li] - base +
+                                    (uint32_t)__popcll(s_em[wave][li] & lt_mask);
+              s_pair[wave][slot] = make_float2(fac, v_sigma);
             }
-            // reference: the sigma terms only where alpha was not clamped
-            const float v_sigma = raw <= 0.999f ? -raw * v_alpha : 0.f;
-            const uint32_t slot = (uint32_t)s_po[wave][li] - base +
-                                  (uint32_t)__popcll(s_em[wave][li] & lt_mask);
-            s_u.pair[wave][slot] = make_float2(fac, v_sigma);
           }
         }
       }
@@ -562,7 +682,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
           while (rb != 0u) {
             const int pl = 16 * oq + __builtin_ctz(rb);
             rb &= rb - 1u;
-            const float2 pr = s_u.pair[wave][slot++];
+            const float2 pr = s_pair[wave][slot++];
             const int pix = wave * 64 + pl;
             const float dx = g0.x - ((float)(tx * TILE + pix % TILE) + 0.5f);
             const float dy = g0.y - ((float)(ty * TILE + pix / TILE) + 0.5f);
