@@ -679,26 +679,59 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
           const uint64_t below = oq == 0 ? 0ull : (em & (~0ull >> (64 - 16 * oq)));
           uint32_t slot = (uint32_t)s_po[wave][li] - base + (uint32_t)__popcll(below);
           uint32_t rb = (uint32_t)(em >> (16 * oq)) & 0xffffu;
-          while (rb != 0u) {
-            const int pl = 16 * oq + __builtin_ctz(rb);
-            rb &= rb - 1u;
-            const float2 pr = s_pair[wave][slot++];
-            const int pix = wave * 64 + pl;
-            const float dx = g0.x - ((float)(tx * TILE + pix % TILE) + 0.5f);
-            const float dy = g0.y - ((float)(ty * TILE + pix / TILE) + 0.5f);
-            const float vs = pr.y;
-            const float mx = vs * dx, my = vs * dy;
-            acc[0] += mx;
-            acc[1] += my;
-            acc[2] += mx * dx;
-            acc[3] += mx * dy;
-            acc[4] += my * dy;
+          if (TILE == 16) {
+            // the lane's 16 pixels are one row: dy is constant, so the dy
+            // moments follow from sum(v_sigma) and sum(v_sigma dx)
+            const float gxr = g0.x - ((float)(tx * TILE) + 0.5f);
+            const float dy = g0.y - ((float)(ty * TILE + wave * ROWS + oq) + 0.5f);
+            const float* vrc = &s_vrc[wave * 64 + 16 * oq][0];
+            float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+            while (rb != 0u) {
+              const int jc = __builtin_ctz(rb);
+              rb &= rb - 1u;
+              const float2 pr = s_pair[wave][slot++];
+              const float dx = gxr - (float)jc;
+              const float vs = pr.y;
+              const float mx = vs * dx;
+              s0 += vs;
+              s1 += mx;
+              s2 = fmaf(mx, dx, s2);
 #pragma unroll
-            for (int k = 0; k < CDIM; ++k) acc[5 + k] += pr.x * s_vrc[pix][k];
-            acc[5 + CDIM] += vs;
-            if (absg) {
-              acc[NV] += fabsf(q.x * mx + q.y * my);
-              acc[NV + 1] += fabsf(q.y * mx + q.z * my);
+              for (int k = 0; k < CDIM; ++k) acc[5 + k] = fmaf(pr.x, vrc[jc * CDIM + k], acc[5 + k]);
+              if (absg) {
+                const float my = vs * dy;
+                acc[NV] += fabsf(q.x * mx + q.y * my);
+                acc[NV + 1] += fabsf(q.y * mx + q.z * my);
+              }
+            }
+            acc[0] = s1;
+            acc[1] = dy * s0;
+            acc[2] = s2;
+            acc[3] = dy * s1;
+            acc[4] = dy * dy * s0;
+            acc[5 + CDIM] = s0;
+          } else {
+            while (rb != 0u) {
+              const int pl = 16 * oq + __builtin_ctz(rb);
+              rb &= rb - 1u;
+              const float2 pr = s_pair[wave][slot++];
+              const int pix = wave * 64 + pl;
+              const float dx = g0.x - ((float)(tx * TILE + pix % TILE) + 0.5f);
+              const float dy = g0.y - ((float)(ty * TILE + pix / TILE) + 0.5f);
+              const float vs = pr.y;
+              const float mx = vs * dx, my = vs * dy;
+              acc[0] += mx;
+              acc[1] += my;
+              acc[2] += mx * dx;
+              acc[3] += mx * dy;
+              acc[4] += my * dy;
+#pragma unroll
+              for (int k = 0; k < CDIM; ++k) acc[5 + k] += pr.x * s_vrc[pix][k];
+              acc[5 + CDIM] += vs;
+              if (absg) {
+                acc[NV] += fabsf(q.x * mx + q.y * my);
+                acc[NV + 1] += fabsf(q.y * mx + q.z * my);
+              }
             }
           }
         }
