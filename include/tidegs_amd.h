@@ -68,6 +68,56 @@ int tgs_fully_fused_projection_bwd(uint32_t C, uint32_t N, const float* means,
                                    float* v_means, float* v_covars, float* v_quats,
                                    float* v_scales, float* v_viewmats, tgs_stream_t stream);
 
+/* Packed projection: replaces fully_fused_projection_packed_fwd_tensor
+ * (gsplat/cuda/csrc/fully_fused_projection_packed_fwd.cu:184-275), the
+ * projection with the packed radius rule (sqrt(max(0.1, b^2 - det)), :111-119)
+ * whose survivors are written as COO entries in camera-major, Gaussian-ascending
+ * order.  Same two passes as the reference:
+ *   1. tgs_fully_fused_projection_packed_count: per block of 256 Gaussians of
+ *      one camera, block_counts[c * blocks + b] = survivors
+ *      (blocks = tgs_fully_fused_projection_packed_blocks(N));
+ *   2. after an exclusive scan of block_counts into block_offsets (nnz = last
+ *      offset + last count), tgs_fully_fused_projection_packed_fwd writes
+ *      indptr [C+1], camera_ids/gaussian_ids [nnz] (int64), radii [nnz] (int32),
+ *      means2d [nnz,2], depths [nnz], conics [nnz,3], compensations [nnz]
+ *      (nullable). */
+uint32_t tgs_fully_fused_projection_packed_blocks(uint32_t N);
+int tgs_fully_fused_projection_packed_count(uint32_t C, uint32_t N, const float* means,
+                                            const float* covars, const float* quats,
+                                            const float* scales, const float* viewmats,
+                                            const float* Ks, int32_t image_width,
+                                            int32_t image_height, float eps2d, float near_plane,
+                                            float far_plane, float radius_clip,
+                                            int32_t* block_counts, tgs_stream_t stream);
+int tgs_fully_fused_projection_packed_fwd(uint32_t C, uint32_t N, const float* means,
+                                          const float* covars, const float* quats,
+                                          const float* scales, const float* viewmats,
+                                          const float* Ks, int32_t image_width,
+                                          int32_t image_height, float eps2d, float near_plane,
+                                          float far_plane, float radius_clip,
+                                          const int32_t* block_offsets, uint32_t nnz,
+                                          int32_t* indptr, int64_t* camera_ids,
+                                          int64_t* gaussian_ids, int32_t* radii, float* means2d,
+                                          float* depths, float* conics, float* compensations,
+                                          tgs_stream_t stream);
+/* Replaces fully_fused_projection_packed_bwd_tensor
+ * (gsplat/cuda/csrc/fully_fused_projection_packed_bwd.cu:18-260).  With
+ * sparse_grad the VJPs are written per entry ([nnz, .]); otherwise they are
+ * added into [N, .] gradients, which the caller zeroes.  v_viewmats (nullable)
+ * is accumulated. */
+int tgs_fully_fused_projection_packed_bwd(uint32_t C, uint32_t N, uint32_t nnz, const float* means,
+                                          const float* covars, const float* quats,
+                                          const float* scales, const float* viewmats,
+                                          const float* Ks, int32_t image_width,
+                                          int32_t image_height, float eps2d,
+                                          const int64_t* camera_ids, const int64_t* gaussian_ids,
+                                          const float* conics, const float* compensations,
+                                          const float* v_means2d, const float* v_depths,
+                                          const float* v_conics, const float* v_compensations,
+                                          int sparse_grad, float* v_means, float* v_covars,
+                                          float* v_quats, float* v_scales, float* v_viewmats,
+                                          tgs_stream_t stream);
+
 /* ---- spherical harmonics ---------------------------------------------- */
 /* Replaces compute_sh_fwd_tensor (gsplat/cuda/csrc/compute_sh_fwd.cu:31-58).
  * dirs [n,3], coeffs [n,K,3], masks [n] u8/bool or null -> colors [n,3]. */

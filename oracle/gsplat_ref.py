@@ -92,10 +92,13 @@ def project_core(means, Sigma, viewmats, Ks, W, H, eps2d):
 
 def project_fwd(means, quats=None, scales=None, viewmats=None, Ks=None, W=0, H=0,
                 eps2d=0.3, near_plane=0.01, far_plane=1e10, radius_clip=0.0, covars=None,
-                dtype=torch.float64):
-    """gsplat fully_fused_projection forward, non-packed (fwd.cu:18-129).
+                dtype=torch.float64, packed=False):
+    """gsplat fully_fused_projection forward (fwd.cu:18-129), dense [C, N] layout.
 
-    Culled entries get radius 0 and zeros elsewhere.
+    ``packed`` applies the packed kernel's radius rule
+    (fully_fused_projection_packed_fwd.cu:111-119: ``sqrt(max(0.1, b^2 - det))``
+    instead of ``max(0.01, ...)``); every other quantity is the same.  Culled
+    entries get radius 0 and zeros elsewhere.
     """
     means = means.to(dtype)
     viewmats = viewmats.to(dtype)
@@ -106,7 +109,7 @@ def project_fwd(means, quats=None, scales=None, viewmats=None, Ks=None, W=0, H=0
     z = pc[..., 2]
     ok = (z >= near_plane) & (z <= far_plane) & (det > 0)
     bb = 0.5 * (a + d)
-    v1 = bb + torch.sqrt(torch.clamp(bb * bb - det, min=0.01))
+    v1 = bb + torch.sqrt(torch.clamp(bb * bb - det, min=0.1 if packed else 0.01))
     radius = torch.ceil(3.0 * torch.sqrt(v1))
     ok &= ~(radius <= radius_clip)
     mx, my = mean2d[..., 0], mean2d[..., 1]

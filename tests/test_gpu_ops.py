@@ -72,6 +72,65 @@ def test_projection_fwd_bwd(gpu, calc_comp):
     assert rel_l2(to_np(dv.grad)[:, :3], to_np(v_vm)[:, :3]) < 1e-4
 
 
+@pytest.mark.parametrize("calc_comp,sparse", [(False, False), (True, False), (False, True)])
+def test_projection_packed(gpu, calc_comp, sparse):
+    """fully_fused_projection(packed=True): entries camera-major and Gaussian-
+    ascending, exactly the oracle's survivors under the packed radius rule;
+    values as the dense projection; VJPs summed over a Gaussian's cameras (or
+    per entry as COO tensors with sparse_grad)."""
+    announce(f"projection packed calc_comp={calc_comp} sparse_grad={sparse}")
+    sc, means, quats, scales = _proj_inputs(seed=4)
+    W, H = sc.width, sc.height
+    C = sc.n_cams
+    dm = means.to(gpu).requires_grad_()
+    dq = quats.to(gpu).requires_grad_()
+    ds = scales.to(gpu).requires_grad_()
+    cam_ids, g_ids, radii, m2d, depths, conics, comps = ops.fully_fused_projection(
+        dm, None, dq, ds, sc.viewmats.to(gpu), sc.Ks.to(gpu), W, H, packed=True,
+        sparse_grad=sparse, calc_compensations=calc_comp)
+    o = G.project_fwd(means, quats, scales, sc.viewmats, sc.Ks, W, H, packed=True)
+    o_radii = to_np(o[0])
+    oc, on = np.nonzero(o_radii > 0)  # camera-major, ascending
+    np.testing.assert_array_equal(to_np(cam_ids), oc)
+    np.testing.assert_array_equal(to_np(g_ids), on)
+    assert cam_ids.dtype == torch.int64 and radii.dtype == torch.int32 and oc.size > 1000
+    r = to_np(radii)
+    assert np.abs(r - o_radii[oc, on]).max() <= 1 and (r == o_radii[oc, on]).mean() > 0.998
+    assert rel_l2(to_np(m2d), to_np(o[1])[oc, on]) < 1e-6
+    assert rel_l2(to_np(depths), to_np(o[2])[oc, on]) < 1e-6
+    assert rel_l2(to_np(conics), to_np(o[3])[oc, on]) < 1e-5
+    if calc_comp:
+        assert rel_l2(to_np(comps), to_np(o[4])[oc, on]) < 1e-5
+    else:
+        assert comps is None
+    g = torch.Generator().manual_seed(5)
+    w_m = torch.randn(m2d.shape, generator=g)
+    w_d = torch.randn(depths.shape, generator=g)
+    w_c = torch.randn(conics.shape, generator=g)
+    w_k = torch.randn(depths.shape, generator=g) if calc_comp else None
+    L = (m2d * w_m.to(gpu)).sum() + (depths * w_d.to(gpu)).sum() + (conics * w_c.to(gpu)).sum()
+    if calc_comp:
+        L = L + (comps * w_k.to(gpu)).sum()
+    L.backward()
+    # oracle: the same cotangents scattered to the dense [C, N] layout
+    Nn = means.shape[0]
+    dense = lambda w, k: torch.zeros((C, Nn) + k, dtype=w.dtype).index_put_(  # noqa: E731
+        (torch.from_numpy(oc), torch.from_numpy(on)), w)
+    live = torch.zeros((C, Nn), dtype=torch.int32)
+    live[oc, on] = 1
+    v_means, v_quats, v_scales, _, _ = G.project_bwd(
+        means, quats, scales, sc.viewmats, sc.Ks, W, H, 0.3, live, o[3], dense(w_m, (2,)),
+        dense(w_d, ()), dense(w_c, (3,)), compensations=o[4] if calc_comp else None,
+        v_compensations=dense(w_k, ()) if calc_comp else None)
+    gm, gq, gs = dm.grad, dq.grad, ds.grad
+    if sparse:
+        assert gm.is_sparse
+        gm, gq, gs = gm.coalesce().to_dense(), gq.coalesce().to_dense(), gs.coalesce().to_dense()
+    assert rel_l2(to_np(gm), v_means) < 1e-4
+    assert rel_l2(to_np(gq), v_quats) < 1e-4
+    assert rel_l2(to_np(gs), v_scales) < 1e-4
+
+
 def test_projection_covars(gpu):
     announce("projection covars")
     sc, means, quats, scales = _proj_inputs(seed=1, C=2)

@@ -87,6 +87,45 @@ def test_projection_forward_closed_forms():
             assert abs(radii[c, n].item() - r) <= 1
 
 
+def test_packed_projection_radius_rule():
+    """Packed radius (fully_fused_projection_packed_fwd.cu:111-119): the same 3-sigma
+    radius of the largest eigenvalue of the blurred 2D covariance, with the
+    discriminant floored at 0.1 instead of 0.01; every other output equal."""
+    means, quats, scales, viewmats, Ks = _rand_scene()
+    W, H, eps = 128, 96, 0.3
+    dense = G.project_fwd(means, quats, scales, viewmats, Ks, W, H, eps2d=eps)
+    packed = G.project_fwd(means, quats, scales, viewmats, Ks, W, H, eps2d=eps, packed=True)
+    rd, rp = dense[0], packed[0]
+    both = (rd > 0) & (rp > 0)
+    assert both.sum() > 100
+    assert bool((rp[both] >= rd[both]).all())  # larger floor, never a smaller radius
+    assert bool(((rd > 0) <= (rp > 0)).all())   # the packed set holds every dense survivor
+    for k in range(1, 5):
+        assert torch.equal(dense[k][both], packed[k][both])
+    R, t = viewmats[:, :3, :3], viewmats[:, :3, 3]
+    pc = torch.einsum("cij,nj->cni", R, means) + t[:, None]
+    Sigma = G.covar_from_quat_scale(quats, scales)
+    checked = 0
+    for c in range(viewmats.shape[0]):
+        for n in torch.nonzero(rp[c]).flatten()[:80].tolist():
+            x, y, z = pc[c, n].tolist()
+            fx, fy = Ks[c, 0, 0].item(), Ks[c, 1, 1].item()
+            limx, limy = 1.3 * 0.5 * W / fx, 1.3 * 0.5 * H / fy
+            tx = z * min(limx, max(-limx, x / z))
+            ty = z * min(limy, max(-limy, y / z))
+            J = np.array([[fx / z, 0, -fx * tx / z ** 2], [0, fy / z, -fy * ty / z ** 2]])
+            covb = J @ (R[c].numpy() @ Sigma[n].numpy() @ R[c].numpy().T) @ J.T + eps * np.eye(2)
+            lam = np.linalg.eigvalsh(covb)
+            disc = (0.5 * (lam[1] - lam[0])) ** 2  # b^2 - det of the blurred covariance
+            if disc >= 0.1:
+                assert abs(rp[c, n].item() - math.ceil(3 * math.sqrt(lam[1]))) <= 1
+                checked += 1
+            else:
+                bb = 0.5 * (lam[0] + lam[1])
+                assert abs(rp[c, n].item() - math.ceil(3 * math.sqrt(bb + math.sqrt(0.1)))) <= 1
+    assert checked > 20
+
+
 def test_projection_culls():
     means = torch.tensor([[0.0, 0.0, -1.0], [0.0, 0.0, 0.005], [500.0, 0.0, 4.0],
                           [0.0, 0.0, 4.0]], dtype=torch.float64)

@@ -38,6 +38,17 @@ SIGNATURES = {
         ctypes.c_int,
         [U32, U32, P, P, P, P, P, P, I32, I32, F32, P, P, P, P, P, P, P, P, P, P, P, P, P],
     ),
+    "tgs_fully_fused_projection_packed_blocks": (U32, [U32]),
+    "tgs_fully_fused_projection_packed_count": (
+        ctypes.c_int, [U32, U32, P, P, P, P, P, P, I32, I32, F32, F32, F32, F32, P, P]),
+    "tgs_fully_fused_projection_packed_fwd": (
+        ctypes.c_int,
+        [U32, U32, P, P, P, P, P, P, I32, I32, F32, F32, F32, F32, P, U32, P, P, P, P, P, P, P,
+         P, P]),
+    "tgs_fully_fused_projection_packed_bwd": (
+        ctypes.c_int,
+        [U32, U32, U32, P, P, P, P, P, P, I32, I32, F32, P, P, P, P, P, P, P, P, ctypes.c_int,
+         P, P, P, P, P, P]),
     "tgs_compute_sh_fwd": (ctypes.c_int, [U32, U32, I32, P, P, P, P, P]),
     "tgs_compute_sh_bwd": (ctypes.c_int, [U32, U32, I32, P, P, P, P, P, P, P]),
     "tgs_bit_width": (U32, [U32]),

@@ -116,6 +116,10 @@ struct ProjResult {
   int radius;  // 0 = culled
 };
 
+// PACKED selects the radius rule of the packed projection
+// (fully_fused_projection_packed_fwd.cu:111-119: sqrt(max(0.1, b^2 - det)))
+// instead of the dense one (fully_fused_projection_fwd.cu:99-103: 0.01).
+template <bool PACKED = false>
 __device__ __forceinline__ ProjResult project_forward(const float p[3], const m3& Sigma,
                                                       const Cam& cam, int W, int H, float eps2d,
                                                       float near_plane, float far_plane,
@@ -166,7 +170,7 @@ __device__ __forceinline__ ProjResult project_forward(const float p[3], const m3
   out.conic[2] = a * inv_det;
 
   const float bb = 0.5f * (a + d);
-  const float v1 = bb + sqrtf(fmaxf(0.01f, bb * bb - det));
+  const float v1 = bb + sqrtf(fmaxf(PACKED ? 0.1f : 0.01f, bb * bb - det));
   const float radius = ceilf(3.f * sqrtf(v1));
   if (radius <= radius_clip) return out;
 

@@ -88,6 +88,96 @@ class _FullyFusedProjection(torch.autograd.Function):
                 None, None, None)
 
 
+class _FullyFusedProjectionPacked(torch.autograd.Function):
+    """Packed projection (fully_fused_projection_packed_fwd.cu / _bwd.cu): the
+    surviving (camera, Gaussian) entries as COO arrays."""
+
+    @staticmethod
+    def forward(ctx, means, covars, quats, scales, viewmats, Ks, width, height, eps2d,
+                near_plane, far_plane, radius_clip, sparse_grad, calc_compensations):
+        C, Nn = viewmats.shape[0], means.shape[0]
+        dev = means.device
+        s = _stream()
+        lib = N.load()
+        nb = int(lib.tgs_fully_fused_projection_packed_blocks(Nn))
+        n_blocks = max(C * nb, 1)
+        counts = torch.zeros(n_blocks, dtype=torch.int32, device=dev)
+        offsets = torch.zeros(n_blocks, dtype=torch.int32, device=dev)
+        args = (N.ptr(means), N.ptr(covars), N.ptr(quats), N.ptr(scales), N.ptr(viewmats),
+                N.ptr(Ks), int(width), int(height), float(eps2d), float(near_plane),
+                float(far_plane), float(radius_clip))
+        nnz = 0
+        if C * Nn:
+            N.call("tgs_fully_fused_projection_packed_count", C, Nn, *args, N.ptr(counts), s)
+            ws = torch.empty(int(lib.tgs_scan_workspace_size(n_blocks)), dtype=torch.uint8,
+                             device=dev)
+            N.call("tgs_exclusive_scan_u32", N.ptr(counts), N.ptr(offsets), n_blocks, N.ptr(ws),
+                   ws.numel(), s)
+            # host read of the entry count, as the reference's block_accum[-1].item()
+            nnz = int((offsets[-1] + counts[-1]).item())
+        indptr = torch.empty(C + 1, dtype=torch.int32, device=dev)
+        camera_ids = torch.empty(nnz, dtype=torch.int64, device=dev)
+        gaussian_ids = torch.empty(nnz, dtype=torch.int64, device=dev)
+        radii = torch.empty(nnz, dtype=torch.int32, device=dev)
+        means2d = torch.empty((nnz, 2), dtype=torch.float32, device=dev)
+        depths = torch.empty(nnz, dtype=torch.float32, device=dev)
+        conics = torch.empty((nnz, 3), dtype=torch.float32, device=dev)
+        comps = torch.zeros(nnz, dtype=torch.float32, device=dev) if calc_compensations else None
+        N.call("tgs_fully_fused_projection_packed_fwd", C, Nn, *args, N.ptr(offsets), nnz,
+               N.ptr(indptr), N.ptr(camera_ids), N.ptr(gaussian_ids), N.ptr(radii),
+               N.ptr(means2d), N.ptr(depths), N.ptr(conics), N.ptr(comps), s)
+        ctx.save_for_backward(means, covars, quats, scales, viewmats, Ks, camera_ids,
+                              gaussian_ids, conics, comps)
+        ctx.width, ctx.height, ctx.eps2d = int(width), int(height), float(eps2d)
+        ctx.sparse_grad = bool(sparse_grad)
+        ctx.mark_non_differentiable(indptr, camera_ids, gaussian_ids, radii)
+        return indptr, camera_ids, gaussian_ids, radii, means2d, depths, conics, comps
+
+    @staticmethod
+    def backward(ctx, v_indptr, v_camera_ids, v_gaussian_ids, v_radii, v_means2d, v_depths,
+                 v_conics, v_comps):
+        (means, covars, quats, scales, viewmats, Ks, camera_ids, gaussian_ids, conics,
+         comps) = ctx.saved_tensors
+        C, Nn = viewmats.shape[0], means.shape[0]
+        nnz = camera_ids.numel()
+        dev = means.device
+
+        def _c(t, shape):
+            return torch.zeros(shape, dtype=torch.float32, device=dev) if t is None else \
+                t.contiguous()
+
+        v_means2d = _c(v_means2d, (nnz, 2))
+        v_depths = _c(v_depths, (nnz,))
+        v_conics = _c(v_conics, (nnz, 3))
+        v_comps = v_comps.contiguous() if (v_comps is not None and comps is not None) else None
+        rows = nnz if ctx.sparse_grad else Nn
+        v_means = torch.zeros((rows, 3), dtype=torch.float32, device=dev)
+        v_covars = torch.zeros((rows, 6), dtype=torch.float32, device=dev) \
+            if covars is not None else None
+        v_quats = torch.zeros((rows, 4), dtype=torch.float32, device=dev) if covars is None else None
+        v_scales = torch.zeros((rows, 3), dtype=torch.float32, device=dev) if covars is None else None
+        v_viewmats = torch.zeros_like(viewmats) if ctx.needs_input_grad[4] else None
+        N.call("tgs_fully_fused_projection_packed_bwd", C, Nn, nnz, N.ptr(means), N.ptr(covars),
+               N.ptr(quats), N.ptr(scales), N.ptr(viewmats), N.ptr(Ks), ctx.width, ctx.height,
+               ctx.eps2d, N.ptr(camera_ids), N.ptr(gaussian_ids), N.ptr(conics), N.ptr(comps),
+               N.ptr(v_means2d), N.ptr(v_depths), N.ptr(v_conics), N.ptr(v_comps),
+               int(ctx.sparse_grad), N.ptr(v_means), N.ptr(v_covars), N.ptr(v_quats),
+               N.ptr(v_scales), N.ptr(v_viewmats), _stream())
+        if ctx.sparse_grad:
+            # gsplat's sparse gradients: COO tensors over the Gaussian rows
+            idx = gaussian_ids[None]
+
+            def _sp(v, shape):
+                return None if v is None else torch.sparse_coo_tensor(idx, v, shape)
+
+            v_means = _sp(v_means, means.shape)
+            v_covars = _sp(v_covars, covars.shape) if covars is not None else None
+            v_quats = _sp(v_quats, quats.shape) if quats is not None else None
+            v_scales = _sp(v_scales, scales.shape) if scales is not None else None
+        return (v_means, v_covars, v_quats, v_scales, v_viewmats, None, None, None, None, None,
+                None, None, None, None)
+
+
 def fully_fused_projection(
     means: Tensor,
     covars: Optional[Tensor] = None,
@@ -105,18 +195,18 @@ def fully_fused_projection(
     sparse_grad: bool = False,
     calc_compensations: bool = False,
 ) -> Tuple[Tensor, ...]:
-    """EWA projection of 3D Gaussians (gsplat fully_fused_projection, non-packed).
+    """EWA projection of 3D Gaussians (gsplat fully_fused_projection).
 
-    Returns ``(radii [C,N] i32, means2d [C,N,2], depths [C,N], conics [C,N,3],
-    compensations [C,N] or None)`` (``engine.py:480``).
+    Non-packed: ``(radii [C,N] i32, means2d [C,N,2], depths [C,N], conics [C,N,3],
+    compensations [C,N] or None)`` (``engine.py:480``).  Packed: the surviving
+    entries under the packed radius rule, camera-major and Gaussian-ascending,
+    as gsplat 1.0's 7-tuple ``(camera_ids [nnz] i64, gaussian_ids [nnz] i64,
+    radii [nnz] i32, means2d [nnz,2], depths [nnz], conics [nnz,3],
+    compensations [nnz] or None)`` (``base_engine.py:112-121,329-340``).
+    ``sparse_grad`` (packed only) returns the Gaussian gradients as COO tensors.
     """
-    if packed:
-        raise NotImplementedError(
-            "fully_fused_projection(packed=True) is not provided by tidegs_amd yet; "
-            "use packed=False (the per-camera TideGS render path)"
-        )
-    if sparse_grad:
-        raise NotImplementedError("sparse_grad requires packed=True")
+    if sparse_grad and not packed:
+        raise ValueError("sparse_grad requires packed=True")
     assert means.dim() == 2 and means.shape[-1] == 3, means.shape
     if covars is None:
         assert quats is not None and scales is not None, "need covars or quats + scales"
@@ -128,6 +218,12 @@ def fully_fused_projection(
     Ks = Ks.contiguous()
     N.require_cuda(means, covars, quats, scales, viewmats, Ks,
                    names=["means", "covars", "quats", "scales", "viewmats", "Ks"])
+    if packed:
+        _, camera_ids, gaussian_ids, radii, means2d, depths, conics, comps = \
+            _FullyFusedProjectionPacked.apply(means, covars, quats, scales, viewmats, Ks, width,
+                                              height, eps2d, near_plane, far_plane, radius_clip,
+                                              sparse_grad, calc_compensations)
+        return camera_ids, gaussian_ids, radii, means2d, depths, conics, comps
     return _FullyFusedProjection.apply(means, covars, quats, scales, viewmats, Ks, width, height,
                                        eps2d, near_plane, far_plane, radius_clip,
                                        calc_compensations)
