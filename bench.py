@@ -93,6 +93,8 @@ WORKLOADS = {
     "cfg2": "cfg2: 1M Gaussians, 1 cam 1920x1080, rasterizer fwd+bwd",
     "cfg4": "cfg4: 16M-Gaussian aerial city, 4 oblique cams x 1920x1080, fwd+bwd+Adam",
     "cfg5": "cfg5: resident [32M,59] optimizer step, 30% rows visible",
+    "resident": "resident-set swap: 4M-row working set of 4096-row blocks (half kept, half "
+                "streamed in UNIFIED order), 30% of blocks packed for writeback + bounds",
 }
 
 
@@ -286,6 +288,136 @@ def bench_optimizer(args, dev):
     }
 
 
+def bench_resident(args, dev):
+    """Resident-set materialization and writeback (the Triton movers of
+    double_buffer_gpu.py / gpu_working_set.py): a 4M-row working set (padded
+    256-byte rows) of 4096-row blocks drawn from a 16M-row scene.  One step =
+    copy the kept half of the blocks from the previous buffer, unpack the
+    streamed half from packed UNIFIED rows already in HBM (the H2D upload is
+    PCIe and outside the step), rebuild the block-start table, pack 30% of the
+    blocks for writeback and take their xyz bounds.  Kernels are timed with
+    events on the launch stream."""
+    import numpy as np
+    import torch
+
+    from tidegs_amd.working_set import BlockLayout, ResidentBuffer, ResidentWorkingSet
+
+    bs = 4096
+    rows = args.n
+    n_blocks = -(-rows // bs)
+    num_total = 4 * n_blocks * bs
+    ws = ResidentWorkingSet(num_total, block_size=bs, device=dev, row_pitch=64)
+    rng = np.random.default_rng(0)
+    prev_ids = sorted(rng.choice(num_total // bs, n_blocks, replace=False).tolist())
+    prev = ResidentBuffer()
+    ws.allocate(prev, n_blocks * bs)
+    prev.table.normal_()
+    prev.table.as_strided((n_blocks * bs, 64), (64, 1))[:, 59:].zero_()
+    prev.local_to_global_idx.copy_(torch.cat([torch.arange(b * bs, (b + 1) * bs)
+                                              for b in prev_ids]))
+    prev.block_to_local_slice = {b: slice(i * bs, (i + 1) * bs) for i, b in enumerate(prev_ids)}
+    kept = sorted(rng.choice(prev_ids, n_blocks // 2, replace=False).tolist())
+    fresh = sorted(set(range(num_total // bs)) - set(prev_ids))
+    streamed = sorted(rng.choice(fresh, n_blocks - len(kept), replace=False).tolist())
+    order = kept + streamed
+    packed = torch.randn((len(streamed) * bs, 59), device=dev)
+    dirty = sorted(rng.choice(order, int(0.3 * n_blocks), replace=False).tolist())
+    tgt = ResidentBuffer()
+    ws.allocate(tgt, len(order) * bs)
+    tgt.block_to_local_slice = {b: slice(i * bs, (i + 1) * bs) for i, b in enumerate(order)}
+    kept_rows, streamed_rows, dirty_rows = len(kept) * bs, len(streamed) * bs, len(dirty) * bs
+    from tidegs_amd import _native as N
+
+    def step():
+        ws.copy_resident_blocks(prev, tgt, kept, tgt.block_to_local_slice)
+        ws.unpack_streamed_rows(packed, BlockLayout.UNIFIED, tgt, kept_rows, block_ids=streamed)
+        tgt._block_starts = ws.build_block_starts(tgt.block_to_local_slice)
+        ws.stage_updated_blocks(tgt, dirty, to_host=False)
+        ws.stage_block_bounds(tgt, dirty, to_host=False)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+
+    # each kernel alone, events right around its launch (index arrays prebuilt)
+    def i64(v):
+        return torch.tensor(list(v), dtype=torch.int64, device=dev)
+
+    kept_src = i64(prev.block_to_local_slice[b].start for b in kept)
+    kept_dst = i64(tgt.block_to_local_slice[b].start for b in kept)
+    streamed_ids = i64(streamed)
+    dirty_src = i64(tgt.block_to_local_slice[b].start for b in dirty)
+    dirty_cnt = i64([bs] * len(dirty))
+    dirty_out = i64(range(0, len(dirty) * bs, bs))
+    out = torch.empty((len(dirty) * bs, 59), device=dev)
+    bounds = torch.empty((len(dirty), 6), device=dev)
+    tid = torch.empty(num_total // bs, dtype=torch.int64, device=dev)
+    order_ids = i64(order)
+    order_starts = i64(tgt.block_to_local_slice[b].start for b in order)
+    st = N.stream_handle(dev)
+    launches = {
+        "copy": lambda: N.call("tgs_ws_copy_rows", N.ptr(prev.table), 64,
+                               N.ptr(prev.local_to_global_idx), N.ptr(kept_src), N.ptr(kept_dst),
+                               len(kept), kept_rows, bs, N.ptr(tgt.table), 64,
+                               N.ptr(tgt.local_to_global_idx), st),
+        "unpack": lambda: N.call("tgs_ws_unpack_rows", N.ptr(packed), 1, streamed_rows,
+                                 N.ptr(tgt.table), 64, kept_rows, N.ptr(streamed_ids),
+                                 len(streamed), bs, N.ptr(tgt.local_to_global_idx), st),
+        "starts": lambda: N.call("tgs_ws_build_block_starts", N.ptr(order_ids),
+                                 N.ptr(order_starts), len(order), N.ptr(tid), tid.numel(), st),
+        "pack": lambda: N.call("tgs_ws_pack_rows", N.ptr(tgt.table), 64, N.ptr(dirty_src),
+                               N.ptr(dirty_cnt), N.ptr(dirty_out), len(dirty), bs, N.ptr(out), st),
+        "bounds": lambda: N.call("tgs_ws_block_bounds", N.ptr(tgt.table), 64, N.ptr(dirty_src),
+                                 N.ptr(dirty_cnt), len(dirty), bs, N.ptr(bounds), st),
+    }
+    # algorithmic bytes: 59 floats read + 59 written per row, +8 B id read/write
+    byt = {"copy": kept_rows * (236 * 2 + 16), "unpack": streamed_rows * (236 * 2 + 8),
+           "starts": 8 * (num_total // bs) + 16 * len(order),
+           "pack": dirty_rows * 236 * 2, "bounds": dirty_rows * 12}
+    stages = {}
+    for k, fn in launches.items():
+        times = []
+        for _ in range(7):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b))
+        k_ms = sorted(times)[len(times) // 2]
+        stages[k] = {"ms": round(k_ms, 4), "bytes": byt[k],
+                     "GBs": round(byt[k] / (k_ms * 1e-3) / 1e9, 1)}
+    dom = max(("copy", "unpack", "pack"), key=lambda k: stages[k]["ms"])
+    return {
+        "metric": "ms/resident-set swap (copy kept + unpack streamed + pack dirty + bounds) "
+                  "at a 4M-row working set",
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) rows, random block sets)",
+        "config": {"workload": WORKLOADS["resident"], "rows": len(order) * bs,
+                   "kept_blocks": len(kept), "streamed_blocks": len(streamed),
+                   "dirty_blocks": len(dirty)},
+        "roofline": {"kernel": f"ws_move_rows ({dom})", "bound": "hbm",
+                     "achieved": stages[dom]["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(stages[dom]["GBs"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "stages": stages,
+        "cpu_baseline": None,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -315,6 +447,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload == "cfg5":
         line = bench_optimizer(args, dev)
+    elif args.workload == "resident":
+        line = bench_resident(args, dev)
     else:
         line = bench_step(args, dev)
     print(json.dumps(line), flush=True)

@@ -359,6 +359,68 @@ int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched, const int32
                          const float* splat_grads, float* grads, uint32_t grad_stride,
                          tgs_stream_t stream);
 
+/* ---- resident-set materialization and writeback ------------------------- */
+/* The working set is one fp32 table in CACHE column order with row pitch 59
+ * (dense) or 64 (padded; padding columns are written as zeros) plus an int64
+ * global id per row, instead of the six component tensors of TideGS's
+ * GPUBuffer (strategies/tide_engine/double_buffer_gpu.py:258-311).  Source
+ * and destination ranges must not overlap.  Block segments follow the
+ * reference's row rule: row r of a num_rows range lies in segment
+ * r / block_rows at offset r % block_rows (only the last segment may be
+ * partial). */
+/* Copy kept blocks between two tables, ids included (replaces
+ * _copy_resident_rows_kernel, double_buffer_gpu.py:41-128, launched by
+ * _copy_resident_blocks :811-872): dst[dst_starts[s] + i] =
+ * src[src_starts[s] + i] for segment s; src_gids/dst_gids both null or both
+ * set.  n_blocks = length of the starts arrays. */
+int tgs_ws_copy_rows(const float* src, uint32_t src_pitch, const int64_t* src_gids,
+                     const int64_t* src_starts, const int64_t* dst_starts, uint32_t n_blocks,
+                     int64_t num_rows, uint32_t block_rows, float* dst, uint32_t dst_pitch,
+                     int64_t* dst_gids, tgs_stream_t stream);
+/* Cold-block ids (replaces _fill_cold_global_ids_kernel,
+ * double_buffer_gpu.py:130-149, :928-963): dst_gids[target_offset + r] =
+ * block_ids[r / block_rows] * block_rows + r % block_rows. */
+int tgs_ws_fill_global_ids(const int64_t* block_ids, uint32_t n_blocks, int64_t* dst_gids,
+                           int64_t target_offset, int64_t num_rows, uint32_t block_rows,
+                           tgs_stream_t stream);
+/* Unpack streamed rows (replaces _unpack_streamed_rows_kernel,
+ * double_buffer_gpu.py:151-210, launched at :1060-1082): packed [num_rows,59]
+ * in CACHE (source_layout 0) or UNIFIED (1: xyz|opacity|scaling|rotation|dc|
+ * rest, :714-735) order -> dst rows target_offset.. in CACHE order.  With
+ * block_ids and dst_gids set, the cold-id fill above is done in the same pass. */
+int tgs_ws_unpack_rows(const float* packed, int source_layout, int64_t num_rows, float* dst,
+                       uint32_t dst_pitch, int64_t target_offset, const int64_t* block_ids,
+                       uint32_t n_blocks, uint32_t block_rows, int64_t* dst_gids,
+                       tgs_stream_t stream);
+/* Pack dirty rows for writeback (replaces _pack_resident_rows_kernel,
+ * strategies/tide_engine/gpu_working_set.py:33-87, launched by
+ * stage_updated_blocks :895-988): out[(out_starts[b] + i) * 59 + c] =
+ * src[src_starts[b] + i][c] for i < min(row_counts[b], block_rows). */
+int tgs_ws_pack_rows(const float* src, uint32_t src_pitch, const int64_t* src_starts,
+                     const int64_t* row_counts, const int64_t* out_starts, uint32_t n_blocks,
+                     uint32_t block_rows, float* out, tgs_stream_t stream);
+/* Per-block xyz bounds (replaces _resident_block_bounds_kernel,
+ * gpu_working_set.py:89-116, launched by stage_block_bounds :990-1062):
+ * bounds[b] = {min x,y,z, max x,y,z} over rows starts[b] ..
+ * starts[b] + min(lengths[b], block_rows) of a table whose xyz are columns
+ * 0..2 (pitch 3 = a bare xyz array, 59 or 64); an empty block gives
+ * {1e20 x3, -1e20 x3}. */
+int tgs_ws_block_bounds(const float* table, uint32_t pitch, const int64_t* starts,
+                        const int64_t* lengths, uint32_t n_blocks, uint32_t block_rows,
+                        float* bounds, tgs_stream_t stream);
+/* Compact block-start table (replaces _build_block_starts,
+ * double_buffer_gpu.py:212-233): block_starts[num_blocks] = -1, then
+ * block_starts[block_ids[i]] = local_starts[i] for ids in range. */
+int tgs_ws_build_block_starts(const int64_t* block_ids, const int64_t* local_starts,
+                              uint32_t n_loaded, int64_t* block_starts, uint32_t num_blocks,
+                              tgs_stream_t stream);
+/* Global -> working-set-local ids (replaces _global_ids_to_local,
+ * double_buffer_gpu.py:236-255): floor(g / block_size) selects the block;
+ * ids whose block is out of range or not loaded give -1. */
+int tgs_ws_global_to_local(const int64_t* global_ids, uint64_t n, const int64_t* block_starts,
+                           uint32_t num_blocks, uint32_t block_size, int64_t* local_ids,
+                           tgs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

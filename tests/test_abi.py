@@ -79,3 +79,28 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert "null pointer" in _native.last_error()
     with pytest.raises(RuntimeError, match="null pointer"):
         _native.call("tgs_compute_sh_fwd", 4, 16, 3, None, None, None, None, None)
+
+
+def test_working_set_argument_checks_without_a_gpu():
+    # Host-side validation only: every call below returns before any launch.
+    from tidegs_amd import _native
+
+    lib = _native.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: the checks fail first
+    assert lib.tgs_ws_copy_rows(None, 59, None, None, None, 0, 0, 4096, None, 59, None, None) == 0
+    assert lib.tgs_ws_copy_rows(None, 59, None, None, None, 1, 10, 4096, None, 59, None, None) == -1
+    assert "null pointer" in _native.last_error()
+    assert lib.tgs_ws_copy_rows(fake, 60, None, fake, fake, 1, 10, 4096, fake, 59, None, None) == -1
+    assert "pitch" in _native.last_error()
+    # 9000 rows of 4096-row blocks need 3 starts
+    assert lib.tgs_ws_copy_rows(fake, 64, None, fake, fake, 2, 9000, 4096, fake, 64, None, None) == -1
+    assert "3 blocks" in _native.last_error()
+    assert lib.tgs_ws_copy_rows(fake, 64, fake, fake, fake, 3, 9000, 4096, fake, 64, None, None) == -1
+    assert "id arrays" in _native.last_error()
+    assert lib.tgs_ws_unpack_rows(fake, 2, 10, fake, 64, 0, None, 0, 4096, None, None) == -1
+    assert "source_layout" in _native.last_error()
+    assert lib.tgs_ws_unpack_rows(fake, 1, 10, fake, 64, 0, fake, 0, 4096, fake, None) == -1
+    assert lib.tgs_ws_fill_global_ids(fake, 1, fake, 0, 5000, 4096, None) == -1
+    assert lib.tgs_ws_pack_rows(fake, 59, fake, fake, fake, 0, 4096, fake, None) == 0
+    assert lib.tgs_ws_block_bounds(fake, 60, fake, fake, 1, 4096, fake, None) == -1
+    assert lib.tgs_ws_global_to_local(fake, 5, fake, 0, 4096, fake, None) == -1

@@ -8,6 +8,8 @@ Drop-in surfaces (same names and call conventions as the reference):
 * ``GPUResidentAdam`` (+ ``GPUResidentSophia``)
 * ``TideStep``: the fused per-batch render/backward/optimizer step over a
   resident ``[N,59]`` Gaussian table
+* ``ResidentWorkingSet``: GPU materialization and writeback of the resident
+  block set (the Triton movers of TideGS's double-buffered working set)
 
 All compute runs in hand-written HIP kernels in ``libtidegs_amd.so`` behind a
 plain C ABI (``include/tidegs_amd.h``); PyTorch only provides device memory and
@@ -23,6 +25,7 @@ from .gsplat_ops import (
 )
 from .clm_ops import FusedSSIMMap, fused_ssim
 from .resident_optim import GPUResidentAdam, GPUResidentSophia
+from .working_set import BlockLayout, ResidentBuffer, ResidentWorkingSet
 
 __all__ = [
     "fully_fused_projection",
@@ -35,4 +38,7 @@ __all__ = [
     "FusedSSIMMap",
     "GPUResidentAdam",
     "GPUResidentSophia",
+    "ResidentWorkingSet",
+    "ResidentBuffer",
+    "BlockLayout",
 ]

@@ -118,6 +118,13 @@ SIGNATURES = {
          F32, F32, F32, F32, F32, ctypes.c_int, P, P],
     ),
     "tgs_block_touch_counts": (ctypes.c_int, [I64, P, ctypes.c_int, P, P, I64, P, P]),
+    "tgs_ws_copy_rows": (ctypes.c_int, [P, U32, P, P, P, U32, I64, U32, P, U32, P, P]),
+    "tgs_ws_fill_global_ids": (ctypes.c_int, [P, U32, P, I64, I64, U32, P]),
+    "tgs_ws_unpack_rows": (ctypes.c_int, [P, ctypes.c_int, I64, P, U32, I64, P, U32, U32, P, P]),
+    "tgs_ws_pack_rows": (ctypes.c_int, [P, U32, P, P, P, U32, U32, P, P]),
+    "tgs_ws_block_bounds": (ctypes.c_int, [P, U32, P, P, U32, U32, P, P]),
+    "tgs_ws_build_block_starts": (ctypes.c_int, [P, P, U32, P, U32, P]),
+    "tgs_ws_global_to_local": (ctypes.c_int, [P, U64, P, U32, U32, P, P]),
 }
 
 
