@@ -421,6 +421,19 @@ int tgs_ws_global_to_local(const int64_t* global_ids, uint64_t n, const int64_t*
                            uint32_t num_blocks, uint32_t block_size, int64_t* local_ids,
                            tgs_stream_t stream);
 
+/* ---- on-disk block store (host code, no GPU) ------------------------------ */
+/* Parallel reads of n blocks of the base/patch files (replaces the per-block
+ * f.seek + f.read + torch.cat of storage/log_storage_manager.py:208-291 and
+ * storage/block_reader.py:55-87): block i is nbytes[i] bytes at
+ * file_offsets[i] of the open descriptor fds[i], read into HOST memory at
+ * (char*)dst + dst_offsets[i] (normally pinned staging) by up to n_threads
+ * threads.  A block that ends
+ * past its file's end is an error (TGS_ERR_ARG); a failed pread returns its
+ * errno. */
+int tgs_io_read_blocks(uint32_t n, const int32_t* fds, const int64_t* file_offsets,
+                       const int64_t* nbytes, void* dst, const int64_t* dst_offsets,
+                       uint32_t n_threads);
+
 #ifdef __cplusplus
 }
 #endif

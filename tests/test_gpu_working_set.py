@@ -344,3 +344,37 @@ def test_full_size_materialize_writeback_bounds(gpu):
     hi = torch.tensor([float(b * bs + ws.block_length(b) - 1) for b in ids])[:, None] \
         + torch.tensor([0.1, 0.2, 0.3])
     assert torch.equal(cpu[:, :3], lo) and torch.equal(cpu[:, 3:], hi)
+
+
+def test_materialize_from_block_store(gpu, tmp_path):
+    """Stream blocks of an on-disk store (base file + two patches) into the
+    resident table through the native reader, the pinned upload and the GPU
+    unpack; every row equals the oracle's per-block file read."""
+    from oracle import block_store_ref as B
+    from tidegs_amd.block_store import BlockStore, BlockStoreReader
+
+    announce("ws materialize from block store")
+    rng = np.random.default_rng(29)
+    bs, n_rows = 1024, 1024 * 300 - 77
+    nb = -(-n_rows // bs)
+    store = BlockStore(tmp_path, block_size=bs, num_blocks=nb)
+    store.write_base(rng.standard_normal((n_rows, 59)).astype(np.float32))
+    for _ in range(2):
+        store.write_patch({int(b): torch.from_numpy(
+            rng.standard_normal((min(bs, n_rows - b * bs), 59)).astype(np.float32))
+            for b in rng.choice(nb, 40, replace=False)})
+    visible = sorted(set(rng.choice(nb, 120, replace=False).tolist()) | {nb - 1})
+    ws = ResidentWorkingSet(n_rows, block_size=bs, device=gpu)
+    tgt = ws.materialize(None, visible, set(), set(), True, BlockStoreReader(store, n_rows))
+    torch.cuda.synchronize()
+    paths = {f: str(p) for f, p in store.file_paths.items()}
+    table = to_np(tgt.table)
+    gids = to_np(tgt.local_to_global_idx)
+    for b in visible:
+        loc = store.index[b]
+        want = B.read_block(paths, (loc.file_id, loc.offset, loc.size), b, bs, 59)
+        sl = tgt.block_to_local_slice[b]
+        np.testing.assert_array_equal(table[sl], want)
+        np.testing.assert_array_equal(gids[sl], np.arange(b * bs, b * bs + want.shape[0]))
+    assert not bool(padding(tgt.table).any())
+    store.close()

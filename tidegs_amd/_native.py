@@ -125,6 +125,7 @@ SIGNATURES = {
     "tgs_ws_block_bounds": (ctypes.c_int, [P, U32, P, P, U32, U32, P, P]),
     "tgs_ws_build_block_starts": (ctypes.c_int, [P, P, U32, P, U32, P]),
     "tgs_ws_global_to_local": (ctypes.c_int, [P, U64, P, U32, U32, P, P]),
+    "tgs_io_read_blocks": (ctypes.c_int, [U32, P, P, P, P, P, U32]),
 }
 
 
