@@ -421,6 +421,39 @@ int tgs_ws_global_to_local(const int64_t* global_ids, uint64_t n, const int64_t*
                            uint32_t num_blocks, uint32_t block_size, int64_t* local_ids,
                            tgs_stream_t stream);
 
+/* ---- Morton-sorted base file (streaming initializer) ---------------------- */
+/* Replace the CPU passes of streaming_ply_to_ssd_base
+ * (storage/streaming_ply_init.py:541-696) for a scene held in HBM; the
+ * rows come out in the stable Morton order the reference's bucketed
+ * external sort produces (:257-538), with the same per-bucket log-scales.
+ * xyz [n,3] fp32.  scene bounds -> bounds[6] = {min x,y,z, max x,y,z}
+ * (scratch: 6 u32). */
+int tgs_init_scene_bounds(const float* xyz, uint64_t n, uint32_t* scratch, float* bounds,
+                          tgs_stream_t stream);
+/* 30-bit Morton codes (streaming_ply_init.py:154-168) against bounds[6]. */
+int tgs_init_morton_codes(const float* xyz, uint64_t n, const float* bounds, uint32_t* codes,
+                          tgs_stream_t stream);
+/* Bucket sizes of the top 10 (counts0 [1024]) and top 20 (counts1 [1<<20])
+ * code bits; both are zeroed first. */
+int tgs_init_prefix_counts(const uint32_t* codes, uint64_t n, uint32_t* counts0,
+                           uint32_t* counts1, tgs_stream_t stream);
+/* flags[i] = 1 where sorted row i starts a new sorted bucket ("leaf"): the
+ * 10-bit bucket unless big0[bucket] (it exceeds the sort memory, :332-350),
+ * then the 20-bit child unless big1[child], else the whole code (:469-538). */
+int tgs_init_leaf_flags(const uint32_t* sorted_codes, uint64_t n, const uint8_t* big0,
+                        const uint8_t* big1, int32_t* flags, tgs_stream_t stream);
+/* Per leaf (leaf_incl = inclusive scan of the flags, perm = sorted vertex
+ * ids): stats[leaf*8 + 0..2] = min xyz, 3..5 = max xyz (fp32 bits), 6 = rows,
+ * 7 = the leaf's first code. */
+int tgs_init_leaf_stats(const int64_t* leaf_incl, const uint32_t* sorted_codes,
+                        const uint32_t* perm, const float* xyz, uint64_t n, uint64_t n_leaves,
+                        uint32_t* stats, tgs_stream_t stream);
+/* Base-file rows [n,59] in sorted order (:234-248 with the leaf log-scale of
+ * :361-367): xyz | leaf_scales[leaf] x3 | 1,0,0,0 | opacity_logit | dc | 0 x45. */
+int tgs_init_pack_rows(const uint32_t* perm, const int64_t* leaf_incl, const float* xyz,
+                       const float* dc, const float* leaf_scales, float opacity_logit, uint64_t n,
+                       float* table, tgs_stream_t stream);
+
 /* ---- on-disk block store (host code, no GPU) ------------------------------ */
 /* Parallel reads of n blocks of the base/patch files (replaces the per-block
  * f.seek + f.read + torch.cat of storage/log_storage_manager.py:208-291 and

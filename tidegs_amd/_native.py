@@ -126,6 +126,12 @@ SIGNATURES = {
     "tgs_ws_build_block_starts": (ctypes.c_int, [P, P, U32, P, U32, P]),
     "tgs_ws_global_to_local": (ctypes.c_int, [P, U64, P, U32, U32, P, P]),
     "tgs_io_read_blocks": (ctypes.c_int, [U32, P, P, P, P, P, U32]),
+    "tgs_init_scene_bounds": (ctypes.c_int, [P, U64, P, P, P]),
+    "tgs_init_morton_codes": (ctypes.c_int, [P, U64, P, P, P]),
+    "tgs_init_prefix_counts": (ctypes.c_int, [P, U64, P, P, P]),
+    "tgs_init_leaf_flags": (ctypes.c_int, [P, U64, P, P, P, P]),
+    "tgs_init_leaf_stats": (ctypes.c_int, [P, P, P, P, U64, U64, P, P]),
+    "tgs_init_pack_rows": (ctypes.c_int, [P, P, P, P, P, F32, U64, P, P]),
 }
 
 
