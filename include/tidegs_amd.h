@@ -454,6 +454,20 @@ int tgs_init_pack_rows(const uint32_t* perm, const int64_t* leaf_incl, const flo
                        const float* dc, const float* leaf_scales, float opacity_logit, uint64_t n,
                        float* table, tgs_stream_t stream);
 
+/* ---- block frustum culling --------------------------------------------- */
+/* Bounding spheres of blocks (storage/gaussian_block.py:285-296, :322-325):
+ * bounds [nb,6] (min xyz, max xyz) -> centers [nb,3] = (min+max)/2,
+ * radii [nb] = (|max-min| / 2) * 1.15, in the reference's float32 order. */
+int tgs_cull_block_spheres(const float* bounds, uint32_t nb, float* centers, float* radii,
+                           tgs_stream_t stream);
+/* 6-plane test of FrustumCuller.cull / cull_subset (gaussian_block.py:356-449)
+ * for C <= 32 cameras at once: planes [C,6,4] normalized (A,B,C,D);
+ * masks[i] bit c = every signed distance of block (block_ids ? block_ids[i] :
+ * i) to camera c's planes is >= -radius; n entries. */
+int tgs_cull_blocks(const float* centers, const float* radii, const int64_t* block_ids,
+                    uint32_t n, const float* planes, uint32_t C, uint32_t* masks,
+                    tgs_stream_t stream);
+
 /* ---- on-disk block store (host code, no GPU) ------------------------------ */
 /* Parallel reads of n blocks of the base/patch files (replaces the per-block
  * f.seek + f.read + torch.cat of storage/log_storage_manager.py:208-291 and

@@ -1,0 +1,103 @@
+"""GPU block frustum culling (tidegs_amd.block_culling) against the CPU
+restatement of TideGS's FrustumCuller (oracle/culling_ref.py): spheres
+bitwise, visible lists identical for batches of cameras, subsets, and after
+bounds updates."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import culling_ref as K
+from tests.gpu_util import announce
+from tidegs_amd.block_culling import FrustumCuller, camera_view_projection, extract_frustum_planes
+
+pytestmark = pytest.mark.gpu
+
+
+def _blocks(seed, n, lo=-4.0, hi=4.0, ext=(0.05, 0.8)):
+    rng = np.random.default_rng(seed)
+    mins = rng.uniform(lo, hi, size=(n, 3)).astype(np.float32)
+    e = rng.uniform(ext[0], ext[1], size=(n, 3)).astype(np.float32)
+    return np.concatenate([mins, mins + e], axis=1)
+
+
+def _look_at_camera(center, target):
+    """3DGS-convention (R, T): R = camera-to-world rotation, T = -R^T C."""
+    z = target - center
+    z = z / np.linalg.norm(z)
+    x = np.cross(z, np.array([0.0, 0.0, 1.0]))
+    x = x / np.linalg.norm(x)
+    y = np.cross(z, x)
+    W = np.stack([x, y, z])  # world -> camera rows (OpenCV: x right, y down, z forward)
+    return W.T, -W @ center
+
+
+def test_reference_subset_equals_full(gpu):
+    announce("culling: reference subset-equals-full case")
+    b = _blocks(7, 128)
+    culler = FrustumCuller(b, scene_radius=10.0, device=gpu)
+    eye = np.eye(4, dtype=np.float32)
+    full = culler.cull(np.zeros(3, np.float32), eye, eye)
+    c, r = K.spheres(b)
+    assert full == K.cull(c, r, K.planes(eye, eye))
+    assert culler.cull_subset(np.zeros(3), eye, eye, np.arange(128)) == full
+    assert culler.cull_subset(np.zeros(3), eye, eye, set(range(128))) == full
+    np.testing.assert_array_equal(culler.block_centers, c)
+    np.testing.assert_array_equal(culler.block_radii, r)
+
+
+def test_batch_of_cameras_matches_oracle(gpu):
+    announce("culling: 250k blocks x 20 cameras")
+    b = _blocks(3, 250_000, lo=-500.0, hi=500.0, ext=(1.0, 30.0))
+    culler = FrustumCuller(b, device=gpu)
+    c, r = K.spheres(b)
+    rng = np.random.default_rng(5)
+    views, projs = [], []
+    for i in range(20):
+        a = 2 * np.pi * i / 20
+        center = np.array([700 * np.cos(a), 700 * np.sin(a), 150.0 + 10 * i])
+        R, T = _look_at_camera(center, rng.uniform(-100, 100, 3))
+        _, v, p = camera_view_projection(R, T, np.deg2rad(50 + i), 1920, 1080, scene_radius=900)
+        views.append(v)
+        projs.append(p)
+    lists = culler.cull_batch(views, projs)  # 32 + remainder launches
+    total = 0
+    for v, p, got in zip(views, projs, lists):
+        want = K.cull(c, r, K.planes(v, p))
+        assert got == want
+        total += len(got)
+    assert 0 < total < 20 * 250_000
+    # subsets in arbitrary order keep their order
+    ids = rng.permutation(250_000)[:5000]
+    got = culler.cull_subset(None, views[3], projs[3], ids)
+    assert got == K.cull(c, r, K.planes(views[3], projs[3]), block_ids=ids)
+    # front-to-back order of the visible blocks
+    pos = camera_view_projection(*_look_at_camera(np.array([700.0, 0, 150]), np.zeros(3)),
+                                 np.deg2rad(50), 1920, 1080)[0]
+    vis = lists[0][:300]
+    order = culler.get_visibility_order(vis, pos)
+    d = np.sum((c[vis] - pos) ** 2, axis=1)
+    assert order == [vis[i] for i in np.argsort(d, kind="stable")]
+
+
+def test_update_block_bounds_then_cull(gpu):
+    announce("culling: bounds update")
+    b = _blocks(9, 4000)
+    culler = FrustumCuller(b, device=gpu)
+    rng = np.random.default_rng(1)
+    ids = rng.choice(4000, 300, replace=False)
+    new = _blocks(10, 300, lo=-1.0, hi=1.0)
+    assert culler.update_block_bounds(ids, new) == 300
+    b2 = b.copy()
+    b2[ids] = new
+    c, r = K.spheres(b2)
+    np.testing.assert_array_equal(culler.block_bounds, b2)
+    eye = np.eye(4, dtype=np.float32)
+    assert culler.cull(None, eye, eye) == K.cull(c, r, K.planes(eye, eye))
+    assert culler.block_radius >= float(r.max()) - 1e-6
+    with pytest.raises(ValueError, match="out-of-range"):
+        culler.cull_subset(None, eye, eye, [4000])
+    with pytest.raises(NotImplementedError):
+        culler.cull(None, eye, eye, use_6plane=False)
+    with pytest.raises(ValueError, match="cameras per launch"):
+        culler.cull_masks(np.zeros((33, 6, 4), np.float32))
+    assert np.array_equal(extract_frustum_planes(eye, eye), K.planes(eye, eye))

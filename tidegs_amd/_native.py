@@ -132,6 +132,8 @@ SIGNATURES = {
     "tgs_init_leaf_flags": (ctypes.c_int, [P, U64, P, P, P, P]),
     "tgs_init_leaf_stats": (ctypes.c_int, [P, P, P, P, U64, U64, P, P]),
     "tgs_init_pack_rows": (ctypes.c_int, [P, P, P, P, P, F32, U64, P, P]),
+    "tgs_cull_block_spheres": (ctypes.c_int, [P, U32, P, P, P]),
+    "tgs_cull_blocks": (ctypes.c_int, [P, P, P, U32, P, U32, P, P]),
 }
 
 
