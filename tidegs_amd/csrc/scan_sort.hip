@@ -247,10 +247,21 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_hist_kernel(const K* __res
   for (int w = 0; w < SORT_THREADS / 64; ++w) s_h[w][threadIdx.x] = 0;
   __syncthreads();
   const TileRange tr = radix_tile(sg, blockIdx.x);
+  // A wavefront whose keys share one digit (common for the high digits of
+  // sorted-ish keys) adds its count once instead of 64 conflicting atomics.
 #pragma unroll 4
   for (int r = 0; r < SORT_ITEMS; ++r) {
     const uint32_t i = (uint32_t)r * SORT_THREADS + threadIdx.x;
-    if (i < tr.count) atomicAdd(&s_h[wave][digit_of(keys[tr.start + i], shift, mask)], 1u);
+    const bool valid = i < tr.count;
+    const uint32_t d = valid ? digit_of(keys[tr.start + i], shift, mask) : 0u;
+    const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)d);
+    const uint64_t vm = tgs_ballot(valid);
+    const uint64_t same = tgs_ballot(valid && d == d0);
+    if (same == vm) {
+      if ((threadIdx.x & 63) == 0 && vm) atomicAdd(&s_h[wave][d0], (uint32_t)__popcll(vm));
+    } else if (valid) {
+      atomicAdd(&s_h[wave][d], 1u);
+    }
   }
   __syncthreads();
   uint32_t c = 0;
@@ -306,11 +317,14 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter_kernel(
     const bool valid = li < tr.count;
     const uint32_t d = digit_of(k[r], shift, mask);
     uint64_t peers = tgs_ballot(valid);
+    const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)d);
+    if (tgs_ballot(valid && d == d0) != peers) {  // else every valid lane shares d0
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const bool bit = (d >> b) & 1u;
-      const uint64_t m = tgs_ballot(bit);
-      peers &= bit ? m : ~m;
+      for (int b = 0; b < 8; ++b) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t m = tgs_ballot(bit);
+        peers &= bit ? m : ~m;
+      }
     }
     const uint32_t before = s_wh[wave][d];
     __builtin_amdgcn_wave_barrier();

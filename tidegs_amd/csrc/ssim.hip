@@ -301,107 +301,87 @@ __global__ void __launch_bounds__(TL_THREADS) tide_loss_kernel(int H, int W,
   for (int c = 0; c < 3; ++c) {
     const float* gtc = gtb + c * HW;
     __syncthreads();
-    // inputs on the 52x52 region: thread (ty, tx) fills rows ty+32i, columns tx+32j
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = ty + TL_T * i;
+    // inputs on the 52x52 region, consecutive threads on consecutive columns
+    for (int o = tid; o < TL_D2 * TL_D2; o += TL_THREADS) {
+      const int r = o / TL_D2, col = o - r * TL_D2;
       const int yy = y0 + r - 2 * SS_R;
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int col = tx + TL_T * jj;
-        if (r < TL_D2 && col < TL_D2) {
-          const int xx = x0 + col - 2 * SS_R;
-          float u = 0.f, w = 0.f;
-          if (xx >= 0 && yy >= 0 && xx < W && yy < H) {
-            const int pix = yy * W + xx;
-            u = img[pix * 3 + c];
-            // gt / gt_div, rounded like the division: product plus one
-            // residual correction
-            const float g = gtc[pix];
-            float q = g * rdiv;
-            q = fmaf(fmaf(-q, gt_div, g), rdiv, q);
-            w = fminf(fmaxf(q, 0.f), 1.f);
-          }
-          sx[r][col] = u;
-          sy[r][col] = w;
-        }
+      const int xx = x0 + col - 2 * SS_R;
+      float u = 0.f, w = 0.f;
+      if (xx >= 0 && yy >= 0 && xx < W && yy < H) {
+        const int pix = yy * W + xx;
+        u = img[pix * 3 + c];
+        // gt / gt_div, rounded like the division: product plus one
+        // residual correction
+        const float g = gtc[pix];
+        float q = g * rdiv;
+        q = fmaf(fmaf(-q, gt_div, g), rdiv, q);
+        w = fminf(fmaxf(q, 0.f), 1.f);
       }
+      sx[r][col] = u;
+      sy[r][col] = w;
     }
     __syncthreads();
     const float x_own = sx[ty + 2 * SS_R][tx + 2 * SS_R];
     const float y_own = sy[ty + 2 * SS_R][tx + 2 * SS_R];
     if (inside) l1_acc += fabsf(x_own - y_own);
     // horizontal pass of x, y, x^2, y^2, xy: 52 rows x 42 columns
+    for (int o = tid; o < TL_D2 * TL_D1; o += TL_THREADS) {
+      const int r = o / TL_D1, col = o - r * TL_D1;
+      float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f, q4 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = ty + TL_T * i;
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int col = tx + TL_T * jj;
-        if (r < TL_D2 && col < TL_D1) {
-          float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f, q4 = 0.f;
-#pragma unroll
-          for (int t = 0; t < 11; ++t) {
-            const float uu = sx[r][col + t], ww = sy[r][col + t], k = c_gauss[t];
-            q0 += k * uu;
-            q1 += k * ww;
-            q2 += k * (uu * uu);
-            q3 += k * (ww * ww);
-            q4 += k * (uu * ww);
-          }
-          hq[0][r][col] = q0;
-          hq[1][r][col] = q1;
-          hq[2][r][col] = q2;
-          hq[3][r][col] = q3;
-          hq[4][r][col] = q4;
-        }
+      for (int t = 0; t < 11; ++t) {
+        const float uu = sx[r][col + t], ww = sy[r][col + t], k = c_gauss[t];
+        q0 += k * uu;
+        q1 += k * ww;
+        q2 += k * (uu * uu);
+        q3 += k * (ww * ww);
+        q4 += k * (uu * ww);
       }
+      hq[0][r][col] = q0;
+      hq[1][r][col] = q1;
+      hq[2][r][col] = q2;
+      hq[3][r][col] = q3;
+      hq[4][r][col] = q4;
     }
     __syncthreads();
     // vertical pass on the 42x42 region: SSIM and the scaled partial maps (the
     // inputs are dead: the dm maps take their place)
 #pragma unroll 1
-    for (int i = 0; i < 2; ++i) {
-      const int r = ty + TL_T * i;
-#pragma unroll 1
-      for (int jj = 0; jj < 2; ++jj) {
-        const int col = tx + TL_T * jj;
-        if (r < TL_D1 && col < TL_D1) {
-          float f[5];
+    for (int o = tid; o < TL_D1 * TL_D1; o += TL_THREADS) {
+      const int r = o / TL_D1, col = o - r * TL_D1;
+      float f[5];
 #pragma unroll
-          for (int k = 0; k < 5; ++k) {
-            float acc = 0.f;
+      for (int k = 0; k < 5; ++k) {
+        float acc = 0.f;
 #pragma unroll
-            for (int t = 0; t < 11; ++t) acc += c_gauss[t] * hq[k][r + t][col];
-            f[k] = acc;
-          }
-          const float mu1 = f[0], mu2 = f[1];
-          const float sigma1_sq = f[2] - mu1 * mu1;
-          const float sigma2_sq = f[3] - mu2 * mu2;
-          const float sigma12 = f[4] - mu1 * mu2;
-          const float Cc = 2.f * mu1 * mu2 + C1;
-          const float D = 2.f * sigma12 + C2;
-          const float A = mu1 * mu1 + mu2 * mu2 + C1;
-          const float Bb = sigma1_sq + sigma2_sq + C2;
-          const int yy = y0 + r - SS_R, xx = x0 + col - SS_R;
-          const bool in_img = xx >= 0 && yy >= 0 && xx < W && yy < H;
-          float d0 = 0.f, d1 = 0.f, d2 = 0.f;
-          if (in_img) {
-            // the partial maps of clm_kernels/ssim.cu:240-262 from two reciprocals
-            const float rA = 1.f / A, rB = 1.f / Bb;
-            const float rAB = rA * rB;
-            const float CD = Cc * D;
-            d0 = 2.f * rAB * (mu2 * D - mu2 * Cc + mu1 * CD * (rB - rA));
-            d1 = -CD * rAB * rB;
-            d2 = 2.f * Cc * rAB;
-            if (r >= SS_R && r < SS_R + TL_T && col >= SS_R && col < SS_R + TL_T)
-              m_acc += CD * rAB;
-          }
-          sdm[0][r][col] = g_ssim * d0;
-          sdm[1][r][col] = g_ssim * d1;
-          sdm[2][r][col] = g_ssim * d2;
-        }
+        for (int t = 0; t < 11; ++t) acc += c_gauss[t] * hq[k][r + t][col];
+        f[k] = acc;
       }
+      const float mu1 = f[0], mu2 = f[1];
+      const float sigma1_sq = f[2] - mu1 * mu1;
+      const float sigma2_sq = f[3] - mu2 * mu2;
+      const float sigma12 = f[4] - mu1 * mu2;
+      const float Cc = 2.f * mu1 * mu2 + C1;
+      const float D = 2.f * sigma12 + C2;
+      const float A = mu1 * mu1 + mu2 * mu2 + C1;
+      const float Bb = sigma1_sq + sigma2_sq + C2;
+      const int yy = y0 + r - SS_R, xx = x0 + col - SS_R;
+      const bool in_img = xx >= 0 && yy >= 0 && xx < W && yy < H;
+      float d0 = 0.f, d1 = 0.f, d2 = 0.f;
+      if (in_img) {
+        // the partial maps of clm_kernels/ssim.cu:240-262 from two reciprocals
+        const float rA = 1.f / A, rB = 1.f / Bb;
+        const float rAB = rA * rB;
+        const float CD = Cc * D;
+        d0 = 2.f * rAB * (mu2 * D - mu2 * Cc + mu1 * CD * (rB - rA));
+        d1 = -CD * rAB * rB;
+        d2 = 2.f * Cc * rAB;
+        if (r >= SS_R && r < SS_R + TL_T && col >= SS_R && col < SS_R + TL_T)
+          m_acc += CD * rAB;
+      }
+      sdm[0][r][col] = g_ssim * d0;
+      sdm[1][r][col] = g_ssim * d1;
+      sdm[2][r][col] = g_ssim * d2;
     }
     __syncthreads();
     // backward: horizontal pass (42 rows x 32 columns) ...
