@@ -249,11 +249,19 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_hist_kernel(const K* __res
   const TileRange tr = radix_tile(sg, blockIdx.x);
   // A wavefront whose keys share one digit (common for the high digits of
   // sorted-ish keys) adds its count once instead of 64 conflicting atomics.
-#pragma unroll 4
+  // all of the thread's keys are loaded before any is counted, so the tile's
+  // loads are in flight together
+  K kr[SORT_ITEMS];
+#pragma unroll
+  for (int r = 0; r < SORT_ITEMS; ++r) {
+    const uint32_t i = (uint32_t)r * SORT_THREADS + threadIdx.x;
+    kr[r] = i < tr.count ? keys[tr.start + i] : (K)0;
+  }
+#pragma unroll
   for (int r = 0; r < SORT_ITEMS; ++r) {
     const uint32_t i = (uint32_t)r * SORT_THREADS + threadIdx.x;
     const bool valid = i < tr.count;
-    const uint32_t d = valid ? digit_of(keys[tr.start + i], shift, mask) : 0u;
+    const uint32_t d = valid ? digit_of(kr[r], shift, mask) : 0u;
     const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)d);
     const uint64_t vm = tgs_ballot(valid);
     const uint64_t same = tgs_ballot(valid && d == d0);
