@@ -738,8 +738,10 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
 #pragma unroll
         for (int k = 0; k < NA; ++k) {
           if (k < NV || absg) {
-            acc[k] += tgs_dpp<0xB1>(acc[k]);  // quad_perm [1,0,3,2]
-            acc[k] += tgs_dpp<0x4E>(acc[k]);  // quad_perm [2,3,0,1]
+            // full quad permutes: every source lane exists, so bound_ctrl only
+            // lets the compiler fold each move into its add
+            acc[k] += tgs_dpp<0xB1, 0xf, 0xf, true>(acc[k]);  // quad_perm [1,0,3,2]
+            acc[k] += tgs_dpp<0x4E, 0xf, 0xf, true>(acc[k]);  // quad_perm [2,3,0,1]
           }
         }
         if (oq == 0 && oe < gn) {

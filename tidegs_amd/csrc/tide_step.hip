@@ -397,24 +397,46 @@ __global__ void __launch_bounds__(256) tide_isect_emit_kernel(
 }
 
 // isect_offset_encode (isect_tiles.cu:234-301) over camera|tile keys.
+#define OFFSET_KEYS 8  // sorted keys per thread of the offset encoder
+
 __global__ void __launch_bounds__(256) tide_offset_encode_kernel(
     uint32_t n_isects, const uint32_t* __restrict__ keys, uint32_t C, uint32_t n_tiles,
-    uint32_t tile_n_bits, int32_t* __restrict__ offsets) {
-  const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= n_isects) return;
+    uint32_t tile_n_bits, bool vec, int32_t* __restrict__ offsets) {
+  const uint32_t base = (blockIdx.x * blockDim.x + threadIdx.x) * OFFSET_KEYS;
+  if (base >= n_isects) return;
   const uint32_t total = C * n_tiles;
   auto bucket = [&](uint32_t k) {
     const uint32_t b = (k >> tile_n_bits) * n_tiles + (k & ((1u << tile_n_bits) - 1u));
     return b < total ? b : total - 1;
   };
-  const uint32_t cur = bucket(keys[idx]);
-  if (idx == 0)
-    for (uint32_t i = 0; i <= cur; ++i) offsets[i] = 0;
-  if (idx == n_isects - 1)
-    for (uint32_t i = cur + 1; i < total; ++i) offsets[i] = (int32_t)n_isects;
-  if (idx > 0) {
-    const uint32_t prev = bucket(keys[idx - 1]);
-    for (uint32_t i = prev + 1; i <= cur; ++i) offsets[i] = (int32_t)idx;
+  uint32_t kk[OFFSET_KEYS];
+  if (vec && base + OFFSET_KEYS <= n_isects) {  // keys 16-byte aligned
+    const uint4 a = *reinterpret_cast<const uint4*>(keys + base);
+    const uint4 b = *reinterpret_cast<const uint4*>(keys + base + 4);
+    kk[0] = a.x; kk[1] = a.y; kk[2] = a.z; kk[3] = a.w;
+    kk[4] = b.x; kk[5] = b.y; kk[6] = b.z; kk[7] = b.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < OFFSET_KEYS; ++j) kk[j] = base + j < n_isects ? keys[base + j] : 0u;
+  }
+  // tiles (prev, cur] start at the first key of cur; the first key fills the
+  // tiles up to its own, the last key the tiles after it
+  uint32_t prev = base > 0 ? bucket(keys[base - 1]) : 0u;
+  if (base == 0) {
+    const uint32_t first = bucket(kk[0]);
+    for (uint32_t i = 0; i <= first; ++i) offsets[i] = 0;
+    prev = first;
+  }
+#pragma unroll
+  for (int j = 0; j < OFFSET_KEYS; ++j) {
+    const uint32_t idx = base + j;
+    if (idx < n_isects) {
+      const uint32_t cur = bucket(kk[j]);
+      for (uint32_t i = prev + 1; i <= cur; ++i) offsets[i] = (int32_t)idx;
+      prev = cur;
+      if (idx == n_isects - 1)
+        for (uint32_t i = cur + 1; i < total; ++i) offsets[i] = (int32_t)n_isects;
+    }
   }
 }
 
@@ -693,8 +715,10 @@ extern "C" int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, u
   TGS_CHECK_ARG(offsets && (n_isects == 0 || keys), "tide_offset_encode: null");
   TGS_CHECK_ARG(total < (1ull << 31), "tide_offset_encode: too many buckets");
   if (n_isects == 0) return tgs_fill_u32(offsets, total, 0u, stream);
-  hipLaunchKernelGGL(tide_offset_encode_kernel, dim3(tgs_blocks(n_isects, 256)), dim3(256), 0,
-                     stream, n_isects, keys, C, tile_width * tile_height, tile_n_bits, offsets);
+  hipLaunchKernelGGL(tide_offset_encode_kernel,
+                     dim3(tgs_blocks((n_isects + OFFSET_KEYS - 1) / OFFSET_KEYS, 256)), dim3(256), 0,
+                     stream, n_isects, keys, C, tile_width * tile_height, tile_n_bits,
+                     ((uintptr_t)keys & 15u) == 0, offsets);
   TGS_RETURN_LAUNCH("tgs_tide_offset_encode");
 }
 
