@@ -335,12 +335,15 @@ int tgs_tide_isect_ids(uint32_t n_isects, const uint32_t* keys, const int32_t* f
                        const float* splats, int64_t* isect_ids, tgs_stream_t stream);
 /* Rasterize forward/backward over packed splats (tile 16, 3 channels);
  * images / v_images [C,H,W,3], alphas [C,H,W], last_ids [C,H,W];
- * splat_grads [V,9] accumulated (zero first): {mean2d 2, conic 3, color 3, opacity}. */
+ * splat_grads [V,9] accumulated (zero first): {mean2d 2, conic 3, color 3, opacity}.
+ * The forward also zeroes clear[0..clear_words) (nullable; 16-byte aligned,
+ * clear_words a multiple of 4), normally the backward's splat_grads: the
+ * stores overlap the compositing instead of taking a pass of their own. */
 int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const float* backgrounds, uint32_t W,
                            uint32_t H, uint32_t tile_width, uint32_t tile_height,
                            const int32_t* tile_offsets, const int32_t* flatten_ids,
                            uint32_t n_isects, float* images, float* alphas, int32_t* last_ids,
-                           tgs_stream_t stream);
+                           float* clear, uint64_t clear_words, tgs_stream_t stream);
 int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const float* backgrounds, uint32_t W,
                            uint32_t H, uint32_t tile_width, uint32_t tile_height,
                            const int32_t* tile_offsets, const int32_t* flatten_ids,

@@ -101,7 +101,8 @@ SIGNATURES = {
     "tgs_tide_isect_emit": (ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P]),
     "tgs_tide_offset_encode": (ctypes.c_int, [U32, P, U32, U32, U32, U32, P, P]),
     "tgs_tide_isect_ids": (ctypes.c_int, [U32, P, P, P, P, P]),
-    "tgs_tide_rasterize_fwd": (ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P]),
+    "tgs_tide_rasterize_fwd": (
+        ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, U64, P]),
     "tgs_tide_rasterize_bwd": (
         ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, P]),
     "tgs_tide_project_bwd": (

@@ -320,11 +320,22 @@ __global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
     RasterGeom G, Src src, const float* __restrict__ backgrounds,
     const int32_t* __restrict__ tile_offsets, const int32_t* __restrict__ flatten_ids,
     float* __restrict__ render_colors, float* __restrict__ render_alphas,
-    int32_t* __restrict__ last_ids) {
+    int32_t* __restrict__ last_ids, float4* __restrict__ clear = nullptr, uint64_t clear_n4 = 0) {
   constexpr int BLOCK = TILE * TILE;
   constexpr int WAVES = BLOCK / 64;
   constexpr int ROWS = 64 / TILE;  // pixel rows per wavefront
   constexpr int BATCH = RF_BATCH < BLOCK ? RF_BATCH : BLOCK;
+  if (clear_n4) {
+    // Side job: zero a buffer (the backward's gradient records) while the
+    // compositing keeps the vector units busy; each workgroup stores its own
+    // slice of clear_n4 16-byte words.
+    const uint64_t groups = (uint64_t)gridDim.x * gridDim.y * gridDim.z;
+    const uint64_t g = ((uint64_t)blockIdx.x * gridDim.y + blockIdx.y) * gridDim.z + blockIdx.z;
+    const uint64_t per = (clear_n4 + groups - 1) / groups;
+    const uint64_t end = min(clear_n4, (g + 1) * per);
+    for (uint64_t w = g * per + threadIdx.x; w < end; w += BLOCK)
+      clear[w] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   constexpr int WORDS = BATCH / 32;
   __shared__ float4 s_g0[BATCH];
   __shared__ float2 s_g1[BATCH];

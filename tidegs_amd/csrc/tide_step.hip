@@ -737,15 +737,20 @@ extern "C" int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const flo
                                       uint32_t tile_height, const int32_t* tile_offsets,
                                       const int32_t* flatten_ids, uint32_t n_isects,
                                       float* images, float* alphas, int32_t* last_ids,
-                                      hipStream_t stream) {
-  if (C == 0 || W == 0 || H == 0) return TGS_OK;
+                                      float* clear, uint64_t clear_words, hipStream_t stream) {
+  TGS_CHECK_ARG(clear_words % 4 == 0 && (clear_words == 0 || clear) &&
+                    ((uintptr_t)clear & 15u) == 0,
+                "tide_rasterize_fwd: clear needs a 16-byte aligned buffer of 4k words");
+  if (C == 0 || W == 0 || H == 0) return clear_words ? tgs_fill_u32(clear, clear_words, 0u, stream)
+                                                     : TGS_OK;
   TGS_CHECK_ARG(tile_offsets && images && alphas && last_ids, "tide_rasterize_fwd: null");
   TGS_CHECK_ARG(n_isects == 0 || (splats && flatten_ids), "tide_rasterize_fwd: null splats");
   TGS_CHECK_ARG(tile_width * 16 >= W && tile_height * 16 >= H, "tide_rasterize_fwd: tile grid");
   const RasterGeom G{C, W, H, tile_width, tile_height, n_isects};
   hipLaunchKernelGGL((raster_fwd_kernel<3, 16, PackedSplats>), dim3(C, tile_height, tile_width),
                      dim3(256), 0, stream, G, PackedSplats{(const float4*)splats}, backgrounds,
-                     tile_offsets, flatten_ids, images, alphas, last_ids);
+                     tile_offsets, flatten_ids, images, alphas, last_ids, (float4*)clear,
+                     (uint64_t)clear_words / 4);
   TGS_RETURN_LAUNCH("tgs_tide_rasterize_fwd");
 }
 

@@ -300,10 +300,13 @@ class TideStep:
         alphas = self._buf("alphas", C * H * W, torch.float32)
         last_ids = self._buf("last_ids", C * H * W, torch.int32)
         bg = self.backgrounds
+        # the backward's per-entry gradient records, zeroed by the forward launch
+        sg_words = (max(V, 1) * 9 + 3) // 4 * 4
+        sgrads = self._buf("splat_grads", sg_words, torch.float32)
         self._begin("raster_fwd")
         N.call("tgs_tide_rasterize_fwd", C, N.ptr(splats), N.ptr(bg), W, H, tw, th,
                N.ptr(offsets), N.ptr(fids), n_isects, N.ptr(images), N.ptr(alphas),
-               N.ptr(last_ids), s)
+               N.ptr(last_ids), N.ptr(sgrads), sg_words, s)
         self._end()
         sums = self._buf("loss_sums", 2 * C, torch.float64)
         v_images = self._buf("v_images", C * H * W * 3, torch.float32)
@@ -312,8 +315,6 @@ class TideStep:
         N.call("tgs_tide_loss", C, H, W, N.ptr(images), N.ptr(gt), self.gt_div,
                self.lambda_dssim, N.ptr(sums), N.ptr(v_images), s)
         self._end()
-        sgrads = self._buf("splat_grads", max(V, 1) * 9, torch.float32)
-        N.call("tgs_fill_u32", N.ptr(sgrads), max(V, 1) * 9, 0, s)
         self._begin("raster_bwd")
         N.call("tgs_tide_rasterize_bwd", C, N.ptr(splats), N.ptr(bg), W, H, tw, th,
                N.ptr(offsets), N.ptr(fids), n_isects, N.ptr(alphas), N.ptr(last_ids),
