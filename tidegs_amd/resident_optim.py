@@ -174,11 +174,20 @@ class GPUResidentAdam:
         self._allocated_slots = target
 
     def _clear_slots(self, slots: List[int]) -> None:
+        """Zero the moments of the given slots: one fill per run of consecutive slots."""
         row_words = self.block_size * self.STATE_PITCH
         s = N.stream_handle(self.device)
-        for slot in slots:
+        ordered = sorted(set(int(x) for x in slots))
+        i = 0
+        while i < len(ordered):
+            j = i
+            while j + 1 < len(ordered) and ordered[j + 1] == ordered[j] + 1:
+                j += 1
+            first, count = ordered[i], j - i + 1
             for buf in (self._exp_avg, self._exp_avg_sq):
-                N.call("tgs_fill_u32", buf.data_ptr() + slot * row_words * 4, row_words, 0, s)
+                N.call("tgs_fill_u32", buf.data_ptr() + first * row_words * 4, count * row_words, 0,
+                       s)
+            i = j + 1
 
     def set_resident_blocks(self, block_ids: List[int]) -> None:
         next_resident = {int(b) for b in block_ids}
