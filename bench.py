@@ -34,6 +34,9 @@ BYTES = {
     "raster_bwd": lambda s: s["C"] * s["P"] * 20 + s["I"] * 52 + s["V"] * 36,
     "project_bwd": lambda s: s["T"] * (4 + 4 + 4 + 236 + 236) + s["V"] * (4 + 36),
     "adam": lambda s: s["T"] * 1656,
+    # fused: the row read once, p/m/v written, m/v read; no gradient rows
+    "project_bwd_update": lambda s: (s["T"] * (4 + 4 + 4 + 236 + 2 * 236 + 3 * 236)
+                                     + s["V"] * (4 + 36)),
 }
 
 
@@ -130,7 +133,7 @@ def bench_step(args, dev):
     # the resident table in its MI355X layout: rows padded to 256 bytes
     table = scenes.padded_table(sc.params.contiguous())
     del sc.params
-    ts = TideStep(table, sc.width, sc.height, batch_size=C)
+    ts = TideStep(table, sc.width, sc.height, batch_size=C, fuse_update=not args.split_update)
 
     for _ in range(args.warmup):
         ts.step(sc.viewmats, sc.Ks, sc.gt)
@@ -175,7 +178,7 @@ def bench_step(args, dev):
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(d["GBs"] / HBM_PEAK_GBS, 4),
                     "traffic": profiled_traffic(dominant) if default_cfg else None}
-    bwd_names = ("raster_bwd", "project_bwd")
+    bwd_names = ("raster_bwd", "project_bwd", "project_bwd_update")
     bwd_ms = sum(kernels[k]["ms"] for k in bwd_names if k in kernels)
     bwd_bytes = sum(kernels[k]["bytes"] for k in bwd_names if k in kernels)
     metric = {"cfg3": METRIC,
@@ -198,7 +201,8 @@ def bench_step(args, dev):
                    "gaussians": ts.params.shape[0], "cameras": C, "width": sc.width,
                    "height": sc.height, "visible_entries": stats.entries,
                    "touched_rows": stats.touched_rows, "isects": stats.n_isects,
-                   "isects_per_tile": round(stats.n_isects / (C * ts.tw * ts.th), 1)},
+                   "isects_per_tile": round(stats.n_isects / (C * ts.tw * ts.th), 1),
+                   "optimizer_update": "split" if args.split_update else "fused"},
         "bwd_hbm_GBs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1) if bwd_ms else None,
         "roofline": roofline,
         "stage_ms": stage_ms,
@@ -595,6 +599,9 @@ def main():
     ap.add_argument("--height", type=int, default=1080)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-timing", action="store_true")
+    ap.add_argument("--split-update", action="store_true",
+                    help="cfg3/cfg4: optimizer update as its own launch over materialised "
+                         "gradient rows instead of inside the projection backward")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run 3 plain device copies of MIB MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")

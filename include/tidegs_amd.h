@@ -361,6 +361,30 @@ int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched, const int32
                          float near_plane, float far_plane, float radius_clip, int32_t sh_degree,
                          const float* splat_grads, float* grads, uint32_t grad_stride,
                          tgs_stream_t stream);
+/* tgs_tide_project_bwd and the resident optimizer update of the same rows in
+ * one launch (TideGS runs them as two stages: engine.py:2434-2469 gradient
+ * scatter, then gpu_resident_optimizer.py:16-70 / runtime.py:1741-1791 the
+ * update): the gradient rows never reach memory.  Each row's 59 gradients
+ * get tgs_resident_adam_step's update (optimizer 0; bias_correction1 and
+ * denom_scale per slot) or tgs_resident_sophia_step's (optimizer 1, with rho
+ * and update_hessian) against the moment tables exp_avg / exp_avg_sq
+ * [slots * block_size, state_pitch], slot lookup through the block layout
+ * (block_starts/ends/slots, n_layout) as in those entry points.  lrs[6] are
+ * the learning rates of the CACHE column groups (xyz, log-scale, quat,
+ * opacity, SH dc, SH rest).  params (row pitch row_stride <= 64) is read and
+ * updated in place.  The touched rows must be unique and ascending (as
+ * tgs_tide_compact writes them); a row outside every resident block keeps
+ * its values and sets *error_flag.  block_size <= 2^22. */
+int tgs_tide_project_bwd_update(
+    uint32_t n_touched, const int32_t* touched, const int32_t* visit_base, const int32_t* visits,
+    const uint32_t* masks, uint32_t C, float* params, uint32_t row_stride, const float* viewmats,
+    const float* Ks, const float* campos, int32_t W, int32_t H, float eps2d, float near_plane,
+    float far_plane, float radius_clip, int32_t sh_degree, const float* splat_grads,
+    const int64_t* block_starts, const int64_t* block_ends, const int64_t* block_slots,
+    int64_t n_layout, int64_t block_size, const float* bias_correction1, const float* denom_scale,
+    float* exp_avg, float* exp_avg_sq, uint32_t state_pitch, const float* lrs, int32_t optimizer,
+    float beta1, float beta2, float eps, float batch_size, float rho, int32_t update_hessian,
+    int32_t* error_flag, tgs_stream_t stream);
 
 /* ---- resident-set materialization and writeback ------------------------- */
 /* The working set is one fp32 table in CACHE column order with row pitch 59

@@ -104,3 +104,27 @@ def test_working_set_argument_checks_without_a_gpu():
     assert lib.tgs_ws_pack_rows(fake, 59, fake, fake, fake, 0, 4096, fake, None) == 0
     assert lib.tgs_ws_block_bounds(fake, 60, fake, fake, 1, 4096, fake, None) == -1
     assert lib.tgs_ws_global_to_local(fake, 5, fake, 0, 4096, fake, None) == -1
+
+
+def test_fused_update_argument_checks_without_a_gpu():
+    # tgs_tide_project_bwd_update validates its arguments before any launch
+    from tidegs_amd import _native
+
+    _native.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: the checks fail first
+    lrs = (ctypes.c_float * 6)()
+
+    def call(n, optimizer=0, row_stride=64, block_size=4096, ptr=fake, bias=fake):
+        return _native.load().tgs_tide_project_bwd_update(
+            n, ptr, ptr, ptr, ptr, 2, ptr, row_stride, ptr, ptr, ptr, 64, 48, 0.3, 0.01, 1e10, 0.0,
+            3, ptr, ptr, ptr, ptr, 4, block_size, bias, bias, ptr, ptr, 64, lrs, optimizer,
+            0.9, 0.999, 1e-15, 2.0, 0.04, 1, ptr, None)
+
+    assert call(0) == 0
+    assert call(0, optimizer=2) == -1
+    assert "optimizer must be" in _native.last_error()
+    assert call(5, ptr=None) == -1 and "null" in _native.last_error()
+    assert call(5, bias=None) == -1 and "bias table" in _native.last_error()
+    assert call(5, optimizer=1, bias=None, row_stride=65) == -1  # Sophia needs no bias tables
+    assert "row_stride" in _native.last_error()
+    assert call(5, block_size=1 << 23) == -1 and "block_size" in _native.last_error()

@@ -108,3 +108,72 @@ def test_tide_step_optimizer_untouched_rows_bitwise(gpu, pitch):
                               to_np(g).astype(np.float64), 0.0, 0.0, lr_cols, b1, b2,
                               1e-15 / np.sqrt(2), 2.0, 1 - b1, np.sqrt(1 - b2))
     np.testing.assert_allclose(to_np(params)[to_np(t)], p_ref, rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("optimizer,pitch,block_size", [("adam", 64, 1024), ("adam", 59, 1000),
+                                                        ("sophia", 64, 1024)])
+def test_fused_update_matches_two_launch_step(gpu, optimizer, pitch, block_size):
+    """tgs_tide_project_bwd_update (projection backward with the optimizer
+    update in the same launch) against tgs_tide_project_bwd +
+    GPUResidentAdam/Sophia.step over the materialised gradient rows, on the
+    same per-entry splat gradients (the rasterizer backward accumulates those
+    with float atomics, so two separate steps differ in their last bits and
+    Adam's normalised update amplifies that for near-zero gradients).  Three
+    steps; parameters and moments agree (both kernels inline one update with
+    pinned rounding, so they are expected bitwise equal; the bound allows a
+    few ulps), the optimizer's stats are equal, and rows no
+    camera sees keep their bits.  Blocks of 1000/1024 rows make wavefront runs
+    cross resident blocks (the non-power-of-two size takes the layout search)."""
+    announce(f"tide step fused update {optimizer} pitch={pitch} block={block_size}")
+    from tidegs_amd import _native as N
+
+    sc = _scene(seed=4, n=20000, C=3)
+
+    def table():
+        p = sc.params.to(gpu).contiguous()
+        return scenes.padded_table(p) if pitch == 64 else p
+
+    kw = dict(batch_size=3, block_size=block_size, optimizer=optimizer)
+    fused = TideStep(table(), sc.width, sc.height, **kw)
+    split = TideStep(table(), sc.width, sc.height, fuse_update=False, **kw)
+    before = fused.params.clone()
+    idle = np.ones(sc.params.shape[0], dtype=bool)  # rows that no camera saw in any step
+    s = N.stream_handle(gpu)
+    vm = sc.viewmats.to(gpu, torch.float32).contiguous()  # alive across the launches
+    Ks = sc.Ks.to(gpu, torch.float32).contiguous()
+    for it in range(1, 4):
+        touched, grads, stats = split.forward_backward(sc.viewmats, sc.Ks, sc.gt)
+        L = split.last
+        idle &= to_np(L["masks"])[: sc.params.shape[0]] == 0
+        T = touched.numel()
+        counts = fused.optimizer.launch_touch_counts(fused.gaussians, touched)
+        torch.cuda.synchronize()
+        args, fstats = fused.optimizer.fused_update_args(it, fused.gaussians, T, counts)
+        N.call("tgs_tide_project_bwd_update", T, N.ptr(touched), N.ptr(L["visit_base"]),
+               N.ptr(L["visits"]), N.ptr(L["masks"]), sc.n_cams, N.ptr(fused.params),
+               fused.row_stride, N.ptr(vm), N.ptr(Ks), N.ptr(L["campos"]), sc.width, sc.height,
+               fused.eps2d, fused.near, fused.far, 0.0, fused.sh_degree, N.ptr(L["splat_grads"]),
+               *args, s)
+        sstats = split.optimizer_step(touched, grads)
+        assert fstats == sstats and fstats["touched_rows"] == T > 0
+        pf, ps = to_np(fused.params), to_np(split.params)
+        print(f"  step {it}: {int((pf != ps).sum())} of {pf.size} parameters differ")
+        np.testing.assert_allclose(pf, ps, rtol=2e-6, atol=1e-9)
+    of, os_ = fused.optimizer, split.optimizer
+    np.testing.assert_allclose(to_np(of._exp_avg), to_np(os_._exp_avg), rtol=1e-5, atol=1e-12)
+    np.testing.assert_allclose(to_np(of._exp_avg_sq), to_np(os_._exp_avg_sq), rtol=1e-5,
+                               atol=1e-18)
+    assert of.get_stats() == os_.get_stats()
+    assert idle.any()
+    np.testing.assert_array_equal(to_np(fused.params)[idle], to_np(before)[idle])
+    if pitch == 64:  # the padding columns keep their bits (zeros)
+        full = fused.params.as_strided((sc.params.shape[0], 64), (64, 1))
+        assert not bool(full[:, 59:].any())
+    # step() wires the same launch: one more batch each way, same bookkeeping
+    fused._iteration = split._iteration
+    a = fused.step(sc.viewmats, sc.Ks, sc.gt)
+    b = split.step(sc.viewmats, sc.Ks, sc.gt)
+    assert a.optimizer == b.optimizer and a.optimizer["touched_rows"] == a.touched_rows
+    np.testing.assert_allclose(a.losses(sc.width, sc.height), b.losses(sc.width, sc.height),
+                               rtol=1e-5)
+    assert fused.last["grads"] is None and of.get_stats() == os_.get_stats()

@@ -108,6 +108,10 @@ SIGNATURES = {
     "tgs_tide_project_bwd": (
         ctypes.c_int,
         [U32, P, P, P, P, U32, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, I32, P, P, U32, P]),
+    "tgs_tide_project_bwd_update": (
+        ctypes.c_int,
+        [U32, P, P, P, P, U32, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, I32, P,
+         P, P, P, I64, I64, P, P, P, P, U32, P, I32, F32, F32, F32, F32, F32, I32, P, P]),
     "tgs_resident_adam_step": (
         ctypes.c_int,
         [I64, P, ctypes.c_int, P, P, P, I64, I64, P, P, ctypes.c_int, P, P, P, P, P, P, P,

@@ -23,12 +23,15 @@
 //   tide_project_bwd one thread per touched row walks its visits in camera
 //                    order, accumulates the projection/SH/activation VJPs and
 //                    writes the row's 59 gradients once (no atomics and no
-//                    read-modify-write of the compact gradient).
+//                    read-modify-write of the compact gradient); the fused
+//                    variant applies the resident optimizer update to the
+//                    row in the same launch instead of writing the gradients.
 // Resident table columns (TideGS CACHE order, storage/block_reader.py:35-44):
 //   xyz 0..2 | log-scale 3..5 | quat 6..9 (w,x,y,z) | opacity logit 10 | SH 11..58
 // with SH coefficient k, channel c at column 11 + 3k + c.
 #include "projection.cuh"
 #include "raster.cuh"
+#include "resident_optim.cuh"
 #include "sh.cuh"
 
 #define TIDE_ROW 59
@@ -454,19 +457,14 @@ __global__ void __launch_bounds__(256) tide_isect_ids_kernel(
 // ---------------------------------------------------------------------------
 // Backward: one thread per touched row.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) tide_project_bwd_kernel(
-    uint32_t n_touched, const int32_t* __restrict__ touched,
-    const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
-    const uint32_t* __restrict__ masks, TideCams tc, const float* __restrict__ params,
-    uint32_t row_stride, int W, int H, float eps2d, float near_plane, float far_plane,
-    float radius_clip, int sh_degree, const float* __restrict__ splat_grads,
-    float* __restrict__ grads, uint32_t grad_stride) {
-  __shared__ CamLDS s_cam;
-  load_cams_lds(tc, s_cam);
-  __syncthreads();
-  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_touched) return;
-  const float* row = params + (uint64_t)touched[t] * row_stride;
+// The 59 gradients (CACHE order) of touched row t, whose table row is `r`.
+__device__ __forceinline__ void tide_row_grads(
+    uint32_t t, int32_t r, const int32_t* __restrict__ visit_base,
+    const int32_t* __restrict__ visits, const uint32_t* __restrict__ masks, const CamLDS& s_cam,
+    const float* params, uint32_t row_stride, int W, int H, float eps2d, float near_plane,
+    float far_plane, float radius_clip, int sh_degree, const float* __restrict__ splat_grads,
+    float out[TIDE_ROW]) {
+  const float* row = params + (uint64_t)r * row_stride;
   const float p[3] = {row[0], row[1], row[2]};
   const float s[3] = {expf(row[3]), expf(row[4]), expf(row[5])};
   float qn[4], qinv;
@@ -491,7 +489,7 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
   // visits in camera order = the set bits of the row's visibility mask; the
   // render projection is recomputed (bit-identical to the forward's) instead
   // of reading the conic and radius back from the splat records
-  uint32_t mask = masks[touched[t]];
+  uint32_t mask = masks[r];
   const int32_t* vis = visits + visit_base[t];
   for (int j = 0; mask != 0u; ++j) {
     const uint32_t c = (uint32_t)__builtin_ctz(mask);
@@ -531,7 +529,6 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
   float vq[4], vs[3];
   covar_vjp_quat_scale(qn, s, v_S, vq, vs);
   const float dot = vq[0] * qn[0] + vq[1] * qn[1] + vq[2] * qn[2] + vq[3] * qn[3];
-  float* out = grads + (uint64_t)t * grad_stride;
   out[0] = v_p[0];
   out[1] = v_p[1];
   out[2] = v_p[2];
@@ -543,8 +540,148 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
   out[10] = v_op * (1.f - opac) * opac;
 #pragma unroll
   for (int k = 0; k < 48; ++k) out[11 + k] = v_sh[k];
+}
+
+__global__ void __launch_bounds__(256) tide_project_bwd_kernel(
+    uint32_t n_touched, const int32_t* __restrict__ touched,
+    const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
+    const uint32_t* __restrict__ masks, TideCams tc, const float* __restrict__ params,
+    uint32_t row_stride, int W, int H, float eps2d, float near_plane, float far_plane,
+    float radius_clip, int sh_degree, const float* __restrict__ splat_grads,
+    float* __restrict__ grads, uint32_t grad_stride) {
+  __shared__ CamLDS s_cam;
+  load_cams_lds(tc, s_cam);
+  __syncthreads();
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_touched) return;
+  float g[TIDE_ROW];
+  tide_row_grads(t, touched[t], visit_base, visits, masks, s_cam, params, row_stride, W, H, eps2d,
+                 near_plane, far_plane, radius_clip, sh_degree, splat_grads, g);
+  float* out = grads + (uint64_t)t * grad_stride;
+#pragma unroll
+  for (int k = 0; k < TIDE_ROW; ++k) out[k] = g[k];
   // zero the padding of a padded row so that the whole row is written
   for (uint32_t k = TIDE_ROW; k < grad_stride; ++k) out[k] = 0.f;
+}
+
+// Projection backward fused with the resident optimizer update of the same
+// rows (the step's last two stages in one launch; the compact gradient rows
+// never reach memory).  Phase 1 is tide_project_bwd per thread, with the
+// row's 59 gradients parked in LDS (lane = row).  Phase 2 walks the
+// wavefront's 64 touched rows (sorted) with lane = column: runs of up to
+// FUSED_ROWS rows inside one resident block share one buffer descriptor per
+// table, every row a scalar byte offset from it, and each element gets the
+// resident optimizer's update (optim_update, the same as
+// tgs_resident_adam_step / tgs_resident_sophia_step).  Rows are unique, so a
+// row's parameters are read (phase 1) and written (phase 2) by one
+// wavefront only.
+#define FUSED_PITCH 61  // odd LDS pitch: both phases' accesses are conflict-free
+#define FUSED_ROWS 16   // rows in flight per wavefront in phase 2
+
+struct TideOptim {
+  OptimLayout L;
+  const float* bias1;        // [slots] (Adam)
+  const float* denom_scale;  // [slots] (Adam)
+  float* m;                  // [slots * block_size, state_pitch]
+  float* v;
+  float lr[6];  // xyz, log-scale, quat, opacity, SH dc, SH rest (CACHE column order)
+  float beta1, beta2, eps, batch_size, rho;
+  int update_h;
+  int state_pitch;
+  int* error_flag;
+};
+
+template <bool SOPHIA>
+__global__ void __launch_bounds__(256) tide_project_bwd_optim_kernel(
+    uint32_t n_touched, const int32_t* __restrict__ touched,
+    const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
+    const uint32_t* __restrict__ masks, TideCams tc, float* __restrict__ params,
+    uint32_t row_stride, int W, int H, float eps2d, float near_plane, float far_plane,
+    float radius_clip, int sh_degree, const float* __restrict__ splat_grads, TideOptim O) {
+  __shared__ CamLDS s_cam;
+  __shared__ float s_g[4][64 * FUSED_PITCH];
+  load_cams_lds(tc, s_cam);
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t t0 = blockIdx.x * blockDim.x + (uint32_t)wv * 64u;  // the wavefront's first row
+  const uint32_t t = t0 + (uint32_t)lane;
+  float* sg = s_g[wv];
+  int32_t my_row = 0;
+  if (t < n_touched) {
+    my_row = touched[t];
+    float g[TIDE_ROW];
+    tide_row_grads(t, my_row, visit_base, visits, masks, s_cam, params, row_stride, W, H, eps2d,
+                   near_plane, far_plane, radius_clip, sh_degree, splat_grads, g);
+#pragma unroll
+    for (int k = 0; k < TIDE_ROW; ++k) sg[lane * FUSED_PITCH + k] = g[k];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (t0 >= n_touched) return;
+  const int n_w = n_touched - t0 < 64u ? (int)(n_touched - t0) : 64;
+
+  const bool act = lane < TIDE_ROW;
+  const int PW = (int)row_stride, SW = O.state_pitch;
+  const int64_t PB = (int64_t)PW * 4, SB = (int64_t)SW * 4;
+  const uint32_t voff_p = lane < PW ? (uint32_t)lane * 4u : TGS_OFF_NONE;
+  const uint32_t voff_s = lane < SW ? (uint32_t)lane * 4u : TGS_OFF_NONE;
+  const int comp = lane < 3 ? 0 : lane < 6 ? 1 : lane < 10 ? 2 : lane < 11 ? 3 : lane < 14 ? 4 : 5;
+  const float lr_lane = act ? O.lr[comp] : 0.f;
+  const float one_m_b1 = 1.0f - O.beta1;
+  const float one_m_b2 = 1.0f - O.beta2;
+  // a run is a prefix of strictly increasing rows inside one resident block
+  const int32_t prev_row = __shfl_up(my_row, 1);
+  const bool rising = lane == 0 || my_row > prev_row;
+  BlockCache bc;
+  for (int u0 = 0; u0 < n_w;) {
+    const int n = n_w - u0 < FUSED_ROWS ? n_w - u0 : FUSED_ROWS;
+    const int64_t r_first = (int64_t)__builtin_amdgcn_readlane(my_row, u0);
+    if (!bc.lookup(O.L, r_first)) {
+      // a touched row outside every resident block: the host checks this flag
+      // and raises (the reference raises on a missing slot,
+      // gpu_resident_optimizer.py:275-279); the row keeps its values
+      if (lane == 0) atomicOr(O.error_flag, 1);
+      ++u0;
+      continue;
+    }
+    // the leading rows from u0 that rise and lie in this block
+    const bool in_run = lane >= u0 && lane < u0 + n && (int64_t)my_row < bc.end &&
+                        (lane == u0 || rising);
+    const int k = __builtin_ctzll(~(__ballot(in_run) >> u0));  // >= 1: lane u0 is in
+    const int64_t r_last = (int64_t)__builtin_amdgcn_readlane(my_row, u0 + k - 1);
+    const int64_t span = r_last - r_first + 1;
+    const int64_t srow = bc.slot * O.L.block_size + (r_first - bc.start);
+    const auto rp = tgs_rsrc(params + r_first * PW, span * PB);
+    const auto rm = tgs_rsrc(O.m + srow * SW, span * SB);
+    const auto rv = tgs_rsrc(O.v + srow * SW, span * SB);
+    const float sc = SOPHIA ? lr_lane : lr_lane / tgs_readlane_f32(O.bias1[bc.slot], 0);
+    const float dsc = SOPHIA ? 1.f : tgs_readlane_f32(O.denom_scale[bc.slot], 0);
+    float gv[FUSED_ROWS], mv[FUSED_ROWS], vv[FUSED_ROWS], pv[FUSED_ROWS];
+#pragma unroll
+    for (int u = 0; u < FUSED_ROWS; ++u) {
+      if (u < k) {
+        const uint32_t d = (uint32_t)(__builtin_amdgcn_readlane(my_row, u0 + u) - (int32_t)r_first);
+        gv[u] = act ? sg[(u0 + u) * FUSED_PITCH + lane] : 0.f;
+        mv[u] = tgs_bload(rm, voff_s, d * (uint32_t)SB);
+        vv[u] = tgs_bload(rv, voff_s, d * (uint32_t)SB);
+        pv[u] = tgs_bload(rp, voff_p, d * (uint32_t)PB);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < FUSED_ROWS; ++u) {
+      if (u < k) {
+        const uint32_t d = (uint32_t)(__builtin_amdgcn_readlane(my_row, u0 + u) - (int32_t)r_first);
+        float m1 = mv[u], v1 = vv[u], p1 = pv[u];
+        optim_update<SOPHIA>(gv[u], m1, v1, p1, sc, dsc, O.beta1, O.beta2, one_m_b1, one_m_b2,
+                             O.eps, O.batch_size, O.rho, O.update_h);
+        tgs_bstore(act ? m1 : mv[u], rm, voff_s, d * (uint32_t)SB);
+        tgs_bstore(act ? v1 : vv[u], rv, voff_s, d * (uint32_t)SB);
+        tgs_bstore(act ? p1 : pv[u], rp, voff_p, d * (uint32_t)PB);
+      }
+    }
+    u0 += k;
+  }
 }
 
 // Camera centres: the translation of inverse(viewmat) for an affine world->camera
@@ -772,6 +909,67 @@ extern "C" int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const flo
                      PackedSplats{(const float4*)splats}, PackedGrads{splat_grads}, backgrounds,
                      tile_offsets, flatten_ids, alphas, last_ids, v_images, (const float*)nullptr);
   TGS_RETURN_LAUNCH("tgs_tide_rasterize_bwd");
+}
+
+extern "C" int tgs_tide_project_bwd_update(
+    uint32_t n_touched, const int32_t* touched, const int32_t* visit_base, const int32_t* visits,
+    const uint32_t* masks, uint32_t C, float* params, uint32_t row_stride, const float* viewmats,
+    const float* Ks, const float* campos, int32_t W, int32_t H, float eps2d, float near_plane,
+    float far_plane, float radius_clip, int32_t sh_degree, const float* splat_grads,
+    const int64_t* block_starts, const int64_t* block_ends, const int64_t* block_slots,
+    int64_t n_layout, int64_t block_size, const float* bias_correction1, const float* denom_scale,
+    float* exp_avg, float* exp_avg_sq, uint32_t state_pitch, const float* lrs, int32_t optimizer,
+    float beta1, float beta2, float eps, float batch_size, float rho, int32_t update_hessian,
+    int32_t* error_flag, hipStream_t stream) {
+  const char* name = "tgs_tide_project_bwd_update";
+  int rc = check_cams(C);
+  if (rc) return rc;
+  TGS_CHECK_ARG(optimizer == 0 || optimizer == 1, "%s: optimizer must be 0 (Adam) or 1 (Sophia)",
+                name);
+  if (n_touched == 0) return TGS_OK;
+  TGS_CHECK_ARG(touched && visit_base && visits && masks && params && viewmats && Ks && campos &&
+                    splat_grads && block_starts && block_ends && block_slots && exp_avg &&
+                    exp_avg_sq && lrs && error_flag,
+                "%s: null", name);
+  TGS_CHECK_ARG(optimizer == 1 || (bias_correction1 && denom_scale), "%s: null bias table", name);
+  TGS_CHECK_ARG(sh_degree >= 0 && sh_degree <= 3, "tide step: sh_degree must be in [0,3]");
+  TGS_CHECK_ARG(row_stride >= TIDE_ROW && row_stride <= 64 && state_pitch >= TIDE_ROW &&
+                    state_pitch <= 64,
+                "%s: row_stride and state_pitch must be in [%d, 64]", name, TIDE_ROW);
+  // a run of rows inside one block is addressed by 32-bit byte offsets
+  TGS_CHECK_ARG(n_layout >= 1 && block_size >= 1 && block_size <= (1 << 22),
+                "%s: need a non-empty layout and 1 <= block_size <= 2^22", name);
+  int shift = -1;
+  if ((block_size & (block_size - 1)) == 0)
+    for (shift = 0; ((int64_t)1 << shift) < block_size; ++shift) {
+    }
+  TideCams tc{viewmats, Ks, campos, C};
+  TideOptim O;
+  O.L = OptimLayout{block_starts, block_ends, block_slots, n_layout, block_size, shift};
+  O.bias1 = bias_correction1;
+  O.denom_scale = denom_scale;
+  O.m = exp_avg;
+  O.v = exp_avg_sq;
+  for (int k = 0; k < 6; ++k) O.lr[k] = lrs[k];
+  O.beta1 = beta1;
+  O.beta2 = beta2;
+  O.eps = eps;
+  O.batch_size = batch_size;
+  O.rho = rho;
+  O.update_h = update_hessian;
+  O.state_pitch = (int)state_pitch;
+  O.error_flag = error_flag;
+#define TIDE_FUSED_LAUNCH(SOPHIA)                                                                 \
+  hipLaunchKernelGGL(tide_project_bwd_optim_kernel<SOPHIA>, dim3(tgs_blocks(n_touched, 256)),     \
+                     dim3(256), 0, stream, n_touched, touched, visit_base, visits, masks, tc,      \
+                     params, row_stride, W, H, eps2d, near_plane, far_plane, radius_clip,          \
+                     sh_degree, splat_grads, O)
+  if (optimizer == 1)
+    TIDE_FUSED_LAUNCH(true);
+  else
+    TIDE_FUSED_LAUNCH(false);
+#undef TIDE_FUSED_LAUNCH
+  TGS_RETURN_LAUNCH(name);
 }
 
 extern "C" int tgs_tide_project_bwd(uint32_t n_touched, const int32_t* touched,

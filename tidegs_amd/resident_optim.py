@@ -416,6 +416,73 @@ class GPUResidentAdam:
             "cold_rows": int(cold_rows),
         }
 
+    # ---- update fused into the gradient launch --------------------------------
+    # A caller that computes the touched rows' gradients on the GPU can apply
+    # the update inside that launch (tgs_tide_project_bwd_update) instead of
+    # materialising the gradients for step().  The host bookkeeping is step()'s:
+    # launch_touch_counts() once the touched rows exist, fused_update_args()
+    # before the fused launch.
+    _FUSED_LR_ORDER = ("xyz", "scaling", "rotation", "opacity", "features_dc", "features_rest")
+
+    def _fused_mode(self, iteration: int) -> Tuple[int, float, int]:
+        """(optimizer id, rho, update_hessian) of tgs_tide_project_bwd_update."""
+        return 0, 0.0, 1
+
+    def launch_touch_counts(self, gaussians, local_rows: torch.Tensor) -> torch.Tensor:
+        """Per-block touched-row counts of ``local_rows`` (ascending, unique),
+        computed on the device stream and copied to pinned host memory without
+        waiting.  The returned host tensor is valid once the stream has passed
+        this point (after the caller's next synchronisation)."""
+        manager = gaussians.gpu_working_set_manager
+        layout, arr, starts, ends, slots = self._layout_tables(manager)
+        local_rows = local_rows.contiguous()
+        if local_rows.dtype not in (torch.int32, torch.int64):
+            raise RuntimeError("[GPUResidentAdam] touched rows must be int32 or int64")
+        n = len(arr)
+        dev = getattr(self, "_fused_counts", None)
+        if dev is None or dev.numel() < n:
+            pin = self.device.type == "cuda"
+            self._fused_counts = dev = torch.empty(n, dtype=torch.int64, device=self.device)
+            self._fused_counts_host = torch.empty(n, dtype=torch.int64, pin_memory=pin)
+        N.call("tgs_block_touch_counts", local_rows.numel(), N.ptr(local_rows),
+               1 if local_rows.dtype == torch.int64 else 0, N.ptr(starts), N.ptr(ends), n,
+               N.ptr(dev), N.stream_handle(self.device))
+        host = self._fused_counts_host[:n]
+        host.copy_(dev[:n], non_blocking=True)
+        return host
+
+    def fused_update_args(self, iteration: int, gaussians, n_rows: int,
+                          counts_host: torch.Tensor) -> Tuple[tuple, Dict[str, Any]]:
+        """Advance the touched slots' steps and bias terms (as step() does) and
+        return the optimizer arguments of tgs_tide_project_bwd_update (from
+        ``block_starts`` to ``error_flag``) and step()'s stats dict."""
+        manager = gaussians.gpu_working_set_manager
+        layout, arr, starts, ends, slots = self._layout_tables(manager)
+        counts = counts_host.numpy()
+        if counts.shape[0] != len(arr) or int(counts.sum()) != int(n_rows):
+            raise RuntimeError(
+                "[GPUResidentAdam] a touched row lies outside every resident block of the layout")
+        component_lrs = self._normalize_columns_lr(getattr(gaussians.optimizer, "columns_lr", None))
+        beta1, beta2 = gaussians.optimizer.param_groups[0]["betas"]
+        beta1, beta2 = float(beta1), float(beta2)
+        eps = float(gaussians.optimizer.param_groups[0]["eps"])
+        hit, cold_rows = self._update_touched_slot_metadata(arr, counts, beta1, beta2)
+        mode, rho, update_h = self._fused_mode(iteration)
+        lrs = (ctypes.c_float * 6)(*[component_lrs[name] for name in self._FUSED_LR_ORDER])
+        self._fused_lrs = lrs  # kept alive until the next call
+        args = (N.ptr(starts), N.ptr(ends), N.ptr(slots), len(layout), self.block_size,
+                N.ptr(self._bias_correction1), N.ptr(self._denom_scale), N.ptr(self._exp_avg),
+                N.ptr(self._exp_avg_sq), self.STATE_PITCH, lrs, mode, beta1, beta2, eps,
+                float(self.batch_size), rho, update_h, N.ptr(self._error_flag))
+        self._stats["optimizer_rows_touched_total"] += int(n_rows)
+        self._update_state_stats()
+        return args, {
+            "updated_blocks": int(hit.size),
+            "updated_block_ids": arr[hit, 2].tolist(),
+            "touched_rows": int(n_rows),
+            "cold_rows": int(cold_rows),
+        }
+
     def get_stats(self) -> Dict[str, Any]:
         self._check_error()
         self._update_state_stats()
@@ -435,6 +502,9 @@ class GPUResidentSophia(GPUResidentAdam):
         super().__init__(batch_size, block_size, capacity_blocks, device)
         self.rho = float(rho)
         self.hessian_interval = max(1, int(hessian_interval))
+
+    def _fused_mode(self, iteration: int) -> Tuple[int, float, int]:
+        return 1, self.rho, 1 if (int(iteration) % self.hessian_interval) == 0 else 0
 
     def step(self, iteration: int, gaussians, sparse_grad_local_ids: torch.Tensor,
              sparse_grad_components: Dict[str, torch.Tensor]) -> Dict[str, Any]:

@@ -14,10 +14,14 @@ whole batch: parameters do not change between the cameras of a batch, so the
 gradients are the same, and each touched row accumulates its cameras in the
 reference's camera order.
 
-Host synchronisations per step: the visibility totals, the intersection
-count, and the per-block touch counts of the optimizer (the reference has the
-same three kinds, ``isect_tiles.cu:166``, ``base_engine.py:407``,
-``gpu_resident_optimizer.py:296``).
+Host synchronisations per step: the visibility totals and the intersection
+count; the optimizer's per-block touch counts are launched after the first and
+read after the second (the reference syncs for all three,
+``isect_tiles.cu:166``, ``base_engine.py:407``, ``gpu_resident_optimizer.py:296``).
+By default the optimizer update runs inside the projection-backward launch
+(``tgs_tide_project_bwd_update``), so the compact gradient rows never reach
+memory; ``fuse_update=False`` keeps the two-launch form (gradient rows, then
+``GPUResidentAdam.step``).
 """
 from __future__ import annotations
 
@@ -103,7 +107,8 @@ class TideStep:
                  eps2d: float = 0.3, near_plane: float = 0.01, far_plane: float = 1e10,
                  radius_clip: float = 0.0, lambda_dssim: float = 0.2,
                  backgrounds: Optional[torch.Tensor] = None, optimizer: str = "adam",
-                 sophia_rho: float = 0.04, gt_div: float = 255.0, keep_isect_ids: bool = False):
+                 sophia_rho: float = 0.04, gt_div: float = 255.0, keep_isect_ids: bool = False,
+                 fuse_update: bool = True):
         if params.dim() != 2 or params.shape[1] != ROW or params.dtype != torch.float32:
             raise ValueError("params must be a float32 [N, 59] table (CACHE column order)")
         if not params.is_cuda or params.stride(1) != 1 or not ROW <= params.stride(0) <= 64:
@@ -123,6 +128,9 @@ class TideStep:
         self.gt_div = float(gt_div)
         self.backgrounds = backgrounds
         self.keep_isect_ids = bool(keep_isect_ids)  # materialise gsplat's isect keys (tests)
+        # step(): optimizer update inside the projection-backward launch (True)
+        # or as its own launch over materialised gradient rows (False)
+        self.fuse_update = bool(fuse_update)
         n = params.shape[0]
         # TideGS hyper-parameter scaling (gaussian_model.py:855-888)
         if columns_lr is None:
@@ -184,6 +192,12 @@ class TideStep:
     # ---- stages -----------------------------------------------------------
     def forward_backward(self, viewmats: torch.Tensor, Ks: torch.Tensor, gt: torch.Tensor):
         """Everything up to the compact gradients; returns (touched, grads, stats)."""
+        return self._run(viewmats, Ks, gt, update=False)
+
+    def _run(self, viewmats: torch.Tensor, Ks: torch.Tensor, gt: torch.Tensor, update: bool):
+        """The batch's stages.  With ``update`` the last stage applies the
+        optimizer to the touched rows in the projection-backward launch
+        (tgs_tide_project_bwd_update) and no gradient rows are returned."""
         C = viewmats.shape[0]
         if not 1 <= C <= 32:
             raise ValueError("1..32 cameras per batch")
@@ -224,6 +238,10 @@ class TideStep:
         tot = totals.cpu().tolist()  # sync 1
         V = tot[C + 1]
         T = tot[C]
+        if update and T:
+            # per-block touch counts for the optimizer's slot bookkeeping,
+            # on the host by sync 2
+            counts_host = self.optimizer.launch_touch_counts(self.gaussians, touched[:T])
 
         # 2. projection + SH colours for every (camera, visible row), one pass over
         #    the touched rows; depth keys and tile rectangles for the sort
@@ -321,15 +339,30 @@ class TideStep:
                N.ptr(v_images), N.ptr(sgrads), s)
         self._end()
 
-        # 5. per touched row: projection + SH + activation backward
-        grads = self._buf("grads", max(T, 1) * GRAD_PITCH, torch.float32).view(-1, GRAD_PITCH)
-        grads = grads[:T, :ROW]
-        self._begin("project_bwd")
-        N.call("tgs_tide_project_bwd", T, N.ptr(touched), N.ptr(visit_base), N.ptr(visits),
-               N.ptr(masks), C, N.ptr(P), self.row_stride, N.ptr(viewmats), N.ptr(Ks),
-               N.ptr(campos), W, H, self.eps2d, self.near, self.far, 0.0, self.sh_degree,
-               N.ptr(sgrads), N.ptr(grads), GRAD_PITCH, s)
-        self._end()
+        # 5. per touched row: projection + SH + activation backward (and, with
+        #    update, the resident optimizer step of the row in the same launch)
+        grads = None
+        opt_stats: dict = {}
+        if update:
+            if T:
+                self._iteration += 1
+                opt_args, opt_stats = self.optimizer.fused_update_args(
+                    self._iteration, self.gaussians, T, counts_host)
+                self._begin("project_bwd_update")
+                N.call("tgs_tide_project_bwd_update", T, N.ptr(touched), N.ptr(visit_base),
+                       N.ptr(visits), N.ptr(masks), C, N.ptr(P), self.row_stride,
+                       N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H, self.eps2d, self.near,
+                       self.far, 0.0, self.sh_degree, N.ptr(sgrads), *opt_args, s)
+                self._end()
+        else:
+            grads = self._buf("grads", max(T, 1) * GRAD_PITCH, torch.float32).view(-1, GRAD_PITCH)
+            grads = grads[:T, :ROW]
+            self._begin("project_bwd")
+            N.call("tgs_tide_project_bwd", T, N.ptr(touched), N.ptr(visit_base), N.ptr(visits),
+                   N.ptr(masks), C, N.ptr(P), self.row_stride, N.ptr(viewmats), N.ptr(Ks),
+                   N.ptr(campos), W, H, self.eps2d, self.near, self.far, 0.0, self.sh_degree,
+                   N.ptr(sgrads), N.ptr(grads), GRAD_PITCH, s)
+            self._end()
         if self._timing:
             self.last_visible_entries = int((splats[: V * 12].view(-1, 12)[:, 7] > 0).sum())
         self.last = dict(masks=masks, entries=entries[:V], cam_offsets=cam_offsets,
@@ -341,7 +374,7 @@ class TideStep:
                          last_ids=last_ids.view(C, H, W), v_images=v_images.view(C, H, W, 3),
                          splat_grads=sgrads[: V * 9].view(-1, 9), grads=grads, campos=campos)
         stats = StepStats(n_cameras=C, visible_per_camera=tot[:C], touched_rows=T, entries=V,
-                          n_isects=n_isects, loss_sums=sums.view(C, 2))
+                          n_isects=n_isects, loss_sums=sums.view(C, 2), optimizer=opt_stats)
         return touched[:T], grads, stats
 
     def optimizer_step(self, touched: torch.Tensor, grads: torch.Tensor) -> dict:
@@ -359,10 +392,13 @@ class TideStep:
         self._timing = bool(timing)
         self._events = []
         try:
-            touched, grads, stats = self.forward_backward(viewmats, Ks, gt)
-            if self._timing:
-                self.optimizer.kernel_hooks = (lambda: self._begin("adam"), self._end)
-            stats.optimizer = self.optimizer_step(touched, grads) if touched.numel() else {}
+            if self.fuse_update:
+                _, _, stats = self._run(viewmats, Ks, gt, update=True)
+            else:
+                touched, grads, stats = self._run(viewmats, Ks, gt, update=False)
+                if self._timing:
+                    self.optimizer.kernel_hooks = (lambda: self._begin("adam"), self._end)
+                stats.optimizer = self.optimizer_step(touched, grads) if touched.numel() else {}
             if self._timing:
                 self._collect()
         finally:
