@@ -576,7 +576,7 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
 // row's parameters are read (phase 1) and written (phase 2) by one
 // wavefront only.
 #define FUSED_PITCH 61  // odd LDS pitch: both phases' accesses are conflict-free
-#define FUSED_ROWS 16   // rows in flight per wavefront in phase 2
+#define FUSED_ROWS 32   // rows in flight per wavefront in phase 2
 
 struct TideOptim {
   OptimLayout L;
