@@ -260,7 +260,7 @@ extern "C" int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, f
 #define TL_D2 (TL_T + 4 * SS_R)   // 52: input region
 #define TL_THREADS (TL_T * TL_T)  // 1024
 
-__global__ void __launch_bounds__(TL_THREADS) tide_loss_kernel(int H, int W,
+__global__ void __launch_bounds__(TL_THREADS, 8) tide_loss_kernel(int H, int W,
                                                                const float* __restrict__ images_hwc,
                                                                const float* __restrict__ gt_chw,
                                                                float gt_div, float C1, float C2,
@@ -288,9 +288,10 @@ __global__ void __launch_bounds__(TL_THREADS) tide_loss_kernel(int H, int W,
   const int bidx = blockIdx.z;
   const int x0 = blockIdx.x * TL_T, y0 = blockIdx.y * TL_T;
   const int tid = threadIdx.x;
-  const int ty = tid / TL_T, tx = tid % TL_T;
-  const int px = x0 + tx, py = y0 + ty;
-  const bool inside = px < W && py < H;
+  // output pixels of thread tid < 512: rows 2 rb2 + {0, 1} of column tx2
+  const int rb2 = (tid % (TL_T * TL_T / 2)) / TL_T, tx2 = tid % TL_T;
+  const int px2 = x0 + tx2, py2 = y0 + 2 * rb2;
+  const bool in2[2] = {px2 < W && py2 < H, px2 < W && py2 + 1 < H};
   const int HW = H * W;
   const float* img = images_hwc + (int64_t)bidx * HW * 3;
   const float* gtb = gt_chw + (int64_t)bidx * HW * 3;
@@ -321,101 +322,145 @@ __global__ void __launch_bounds__(TL_THREADS) tide_loss_kernel(int H, int W,
       sy[r][col] = w;
     }
     __syncthreads();
-    const float x_own = sx[ty + 2 * SS_R][tx + 2 * SS_R];
-    const float y_own = sy[ty + 2 * SS_R][tx + 2 * SS_R];
-    if (inside) l1_acc += fabsf(x_own - y_own);
-    // horizontal pass of x, y, x^2, y^2, xy: 52 rows x 42 columns
-    for (int o = tid; o < TL_D2 * TL_D1; o += TL_THREADS) {
-      const int r = o / TL_D1, col = o - r * TL_D1;
-      float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f, q4 = 0.f;
+    // threads below 512 keep the inputs of their two output pixels (rows
+    // 2 rb2 and 2 rb2 + 1 of column tx2) for the gradient at the end
+    float x_own[2] = {0.f, 0.f}, y_own[2] = {0.f, 0.f};
+    if (tid < TL_T * TL_T / 2) {
 #pragma unroll
-      for (int t = 0; t < 11; ++t) {
-        const float uu = sx[r][col + t], ww = sy[r][col + t], k = c_gauss[t];
-        q0 += k * uu;
-        q1 += k * ww;
-        q2 += k * (uu * uu);
-        q3 += k * (ww * ww);
-        q4 += k * (uu * ww);
+      for (int j = 0; j < 2; ++j) {
+        x_own[j] = sx[2 * rb2 + j + 2 * SS_R][tx2 + 2 * SS_R];
+        y_own[j] = sy[2 * rb2 + j + 2 * SS_R][tx2 + 2 * SS_R];
+        if (in2[j]) l1_acc += fabsf(x_own[j] - y_own[j]);
       }
-      hq[0][r][col] = q0;
-      hq[1][r][col] = q1;
-      hq[2][r][col] = q2;
-      hq[3][r][col] = q3;
-      hq[4][r][col] = q4;
     }
-    __syncthreads();
-    // vertical pass on the 42x42 region: SSIM and the scaled partial maps (the
-    // inputs are dead: the dm maps take their place)
-#pragma unroll 1
-    for (int o = tid; o < TL_D1 * TL_D1; o += TL_THREADS) {
-      const int r = o / TL_D1, col = o - r * TL_D1;
-      float f[5];
+    // horizontal pass of x, y, x^2, y^2, xy: 52 rows x 42 columns, three
+    // consecutive columns per work item (13 inputs; each product formed once)
+    for (int o = tid; o < TL_D2 * (TL_D1 / 3); o += TL_THREADS) {
+      const int r = o / (TL_D1 / 3), cb = (o - r * (TL_D1 / 3)) * 3;
+      float u[13], w[13];
+#pragma unroll
+      for (int t = 0; t < 13; ++t) {
+        u[t] = sx[r][cb + t];
+        w[t] = sy[r][cb + t];
+      }
 #pragma unroll
       for (int k = 0; k < 5; ++k) {
-        float acc = 0.f;
+        float v[13];
 #pragma unroll
-        for (int t = 0; t < 11; ++t) acc += c_gauss[t] * hq[k][r + t][col];
-        f[k] = acc;
-      }
-      const float mu1 = f[0], mu2 = f[1];
-      const float sigma1_sq = f[2] - mu1 * mu1;
-      const float sigma2_sq = f[3] - mu2 * mu2;
-      const float sigma12 = f[4] - mu1 * mu2;
-      const float Cc = 2.f * mu1 * mu2 + C1;
-      const float D = 2.f * sigma12 + C2;
-      const float A = mu1 * mu1 + mu2 * mu2 + C1;
-      const float Bb = sigma1_sq + sigma2_sq + C2;
-      const int yy = y0 + r - SS_R, xx = x0 + col - SS_R;
-      const bool in_img = xx >= 0 && yy >= 0 && xx < W && yy < H;
-      float d0 = 0.f, d1 = 0.f, d2 = 0.f;
-      if (in_img) {
-        // the partial maps of clm_kernels/ssim.cu:240-262 from two reciprocals
-        const float rA = 1.f / A, rB = 1.f / Bb;
-        const float rAB = rA * rB;
-        const float CD = Cc * D;
-        d0 = 2.f * rAB * (mu2 * D - mu2 * Cc + mu1 * CD * (rB - rA));
-        d1 = -CD * rAB * rB;
-        d2 = 2.f * Cc * rAB;
-        if (r >= SS_R && r < SS_R + TL_T && col >= SS_R && col < SS_R + TL_T)
-          m_acc += CD * rAB;
-      }
-      sdm[0][r][col] = g_ssim * d0;
-      sdm[1][r][col] = g_ssim * d1;
-      sdm[2][r][col] = g_ssim * d2;
-    }
-    __syncthreads();
-    // backward: horizontal pass (42 rows x 32 columns) ...
+        for (int t = 0; t < 13; ++t)
+          v[t] = k == 0 ? u[t] : k == 1 ? w[t] : k == 2 ? u[t] * u[t] : k == 3 ? w[t] * w[t]
+                                                                               : u[t] * w[t];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = ty + TL_T * i;
-      if (r < TL_D1) {
-        float q0 = 0.f, q1 = 0.f, q2 = 0.f;
+        for (int j = 0; j < 3; ++j) {
+          float q = 0.f;
 #pragma unroll
-        for (int t = 0; t < 11; ++t) {
-          const float k = c_gauss[t];
-          q0 += k * sdm[0][r][tx + t];
-          q1 += k * sdm[1][r][tx + t];
-          q2 += k * sdm[2][r][tx + t];
+          for (int t = 0; t < 11; ++t) q += c_gauss[t] * v[j + t];
+          hq[k][r][cb + j] = q;
         }
-        h2[0][r][tx] = q0;
-        h2[1][r][tx] = q1;
-        h2[2][r][tx] = q2;
       }
     }
     __syncthreads();
-    // ... then vertical, and the gradient of this pixel
-    if (inside) {
-      float f0 = 0.f, f1 = 0.f, f2 = 0.f;
+    // vertical pass on the 42x42 region, two consecutive rows per work item:
+    // SSIM and the scaled partial maps (the inputs are dead: the dm maps take
+    // their place)
+#pragma unroll 1
+    for (int o = tid; o < (TL_D1 / 2) * TL_D1; o += TL_THREADS) {
+      const int rq = o / TL_D1, col = o - rq * TL_D1;
+      const int rb = 2 * rq;
+      float f[2][5];
 #pragma unroll
-      for (int t = 0; t < 11; ++t) {
-        const float k = c_gauss[t];
-        f0 += k * h2[0][ty + t][tx];
-        f1 += k * h2[1][ty + t][tx];
-        f2 += k * h2[2][ty + t][tx];
+      for (int k = 0; k < 5; ++k) {
+        float v[12];
+#pragma unroll
+        for (int t = 0; t < 12; ++t) v[t] = hq[k][rb + t][col];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          float acc = 0.f;
+#pragma unroll
+          for (int t = 0; t < 11; ++t) acc += c_gauss[t] * v[j + t];
+          f[j][k] = acc;
+        }
+        // one map at a time: its sums are complete before the next map's loads
+        // (bounds the registers to 8 waves per SIMD)
+        asm volatile("" : "+v"(f[0][k]), "+v"(f[1][k])::"memory");
       }
-      const float d = x_own - y_own;
-      vimg[(py * W + px) * 3 + c] =
-          f0 + 2.f * x_own * f1 + y_own * f2 + (d > 0.f ? g_l1 : (d < 0.f ? -g_l1 : 0.f));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = rb + j;
+        const float mu1 = f[j][0], mu2 = f[j][1];
+        const float sigma1_sq = f[j][2] - mu1 * mu1;
+        const float sigma2_sq = f[j][3] - mu2 * mu2;
+        const float sigma12 = f[j][4] - mu1 * mu2;
+        const float Cc = 2.f * mu1 * mu2 + C1;
+        const float D = 2.f * sigma12 + C2;
+        const float A = mu1 * mu1 + mu2 * mu2 + C1;
+        const float Bb = sigma1_sq + sigma2_sq + C2;
+        const int yy = y0 + r - SS_R, xx = x0 + col - SS_R;
+        const bool in_img = xx >= 0 && yy >= 0 && xx < W && yy < H;
+        float d0 = 0.f, d1 = 0.f, d2 = 0.f;
+        if (in_img) {
+          // the partial maps of clm_kernels/ssim.cu:240-262 from two
+          // reciprocals; A >= C1 and Bb >= C2 - (rounding) > 0, so the
+          // hardware reciprocal (within 1 ulp) is safe here
+          const float rA = __builtin_amdgcn_rcpf(A), rB = __builtin_amdgcn_rcpf(Bb);
+          const float rAB = rA * rB;
+          const float CD = Cc * D;
+          d0 = 2.f * rAB * (mu2 * D - mu2 * Cc + mu1 * CD * (rB - rA));
+          d1 = -CD * rAB * rB;
+          d2 = 2.f * Cc * rAB;
+          if (r >= SS_R && r < SS_R + TL_T && col >= SS_R && col < SS_R + TL_T)
+            m_acc += CD * rAB;
+        }
+        sdm[0][r][col] = g_ssim * d0;
+        sdm[1][r][col] = g_ssim * d1;
+        sdm[2][r][col] = g_ssim * d2;
+      }
+    }
+    __syncthreads();
+    // backward: horizontal pass (42 rows x 32 columns), two columns per item ...
+    for (int o = tid; o < TL_D1 * (TL_T / 2); o += TL_THREADS) {
+      const int r = o / (TL_T / 2), cb = (o - r * (TL_T / 2)) * 2;
+#pragma unroll
+      for (int m = 0; m < 3; ++m) {
+        float v[12];
+#pragma unroll
+        for (int t = 0; t < 12; ++t) v[t] = sdm[m][r][cb + t];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          float q = 0.f;
+#pragma unroll
+          for (int t = 0; t < 11; ++t) q += c_gauss[t] * v[j + t];
+          h2[m][r][cb + j] = q;
+        }
+      }
+    }
+    __syncthreads();
+    // ... then vertical, two rows per item (threads below 512), and the
+    // gradient of those pixels
+    if (tid < TL_T * TL_T / 2) {
+      float f[2][3];
+#pragma unroll
+      for (int m = 0; m < 3; ++m) {
+        float v[12];
+#pragma unroll
+        for (int t = 0; t < 12; ++t) v[t] = h2[m][2 * rb2 + t][tx2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          float q = 0.f;
+#pragma unroll
+          for (int t = 0; t < 11; ++t) q += c_gauss[t] * v[j + t];
+          f[j][m] = q;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (in2[j]) {
+          const float d = x_own[j] - y_own[j];
+          vimg[((py2 + j) * W + px2) * 3 + c] = f[j][0] + 2.f * x_own[j] * f[j][1] +
+                                                y_own[j] * f[j][2] +
+                                                (d > 0.f ? g_l1 : (d < 0.f ? -g_l1 : 0.f));
+        }
+      }
     }
   }
   const float l1 = tgs_wave_sum(l1_acc);
