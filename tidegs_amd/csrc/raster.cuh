@@ -502,7 +502,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   __shared__ float2 s_pair[WAVES][RB_PAIRS];  // (alpha T, v_sigma)
   __shared__ uint64_t s_em[WAVES][BATCH];         // pixel mask of each list entry
   __shared__ uint16_t s_po[WAVES][BATCH + 1];     // first pair slot of each list entry
-  __shared__ float s_stage[WAVES][16 * NA];
+  __shared__ float s_stage[WAVES][32 * NA];       // one owner group's gradient values
 
   const uint32_t cam = blockIdx.x;
   const uint32_t ty = blockIdx.y, tx = blockIdx.z;
@@ -549,8 +549,8 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   const int32_t wave_bin_final = tgs_wave_max_i32(bin_final);
   const bool absg = sink.absgrad();
   const int nval = absg ? NA : NV;
-  // owner role within a group of 16 entries: entry oe, pixel lanes [16 oq, 16 oq + 16)
-  const int oe = lane >> 2, oq = lane & 3;
+  // owner role within a group of 32 entries: entry oe, pixel bits [32 oh, 32 oh + 32)
+  const int oe = lane >> 1, oh = lane & 1;
 
   for (int32_t b = 0; b < n_batches; ++b) {
     __syncthreads();
@@ -674,56 +674,73 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // 3. owners, groups of 16 entries
-      for (int e0 = a; e0 < e_end; e0 += 16) {
-        const int gn = min(16, e_end - e0);
+      // 3. owners, groups of 32 entries: lanes 2e, 2e+1 own entry e, each
+      //    summing the moments over one half of the strip (pixel bits
+      //    [32h, 32h+32)); one DPP step adds the halves and lane 2e stages
+      //    the entry's gradient values
+      for (int e0 = a; e0 < e_end; e0 += 32) {
+        const int gn = min(32, e_end - e0);
         float acc[NA];
 #pragma unroll
         for (int k = 0; k < NA; ++k) acc[k] = 0.f;
         float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+        int t = 0;
         if (oe < gn) {
           const int li = e0 + oe;
-          const int t = s_list[wave][li];
+          t = s_list[wave][li];
           const float4 g0 = s_g0[t];
           q = staged_conic_rop(g0, s_g1[t]);
           const uint64_t em = s_em[wave][li];
-          const uint64_t below = oq == 0 ? 0ull : (em & (~0ull >> (64 - 16 * oq)));
-          uint32_t slot = (uint32_t)s_po[wave][li] - base + (uint32_t)__popcll(below);
-          uint32_t rb = (uint32_t)(em >> (16 * oq)) & 0xffffu;
+          uint32_t slot = (uint32_t)s_po[wave][li] - base +
+                          (oh == 0 ? 0u : (uint32_t)__popc((uint32_t)em));
+          const uint32_t hb = (uint32_t)(em >> (32 * oh));
           if (TILE == 16) {
-            // the lane's 16 pixels are one row: dy is constant, so the dy
-            // moments follow from sum(v_sigma) and sum(v_sigma dx)
+            // the half is two pixel rows; within a row dy is constant, so
+            // each row's dy moments follow from its sum(v_sigma) and
+            // sum(v_sigma dx)
             const float gxr = g0.x - ((float)(tx * TILE) + 0.5f);
-            const float dy = g0.y - ((float)(ty * TILE + wave * ROWS + oq) + 0.5f);
-            const float* vrc = &s_vrc[wave * 64 + 16 * oq][0];
-            float s0 = 0.f, s1 = 0.f, s2 = 0.f;
-            while (rb != 0u) {
-              const int jc = __builtin_ctz(rb);
-              rb &= rb - 1u;
-              const float2 pr = s_pair[wave][slot++];
-              const float dx = gxr - (float)jc;
-              const float vs = pr.y;
-              const float mx = vs * dx;
-              s0 += vs;
-              s1 += mx;
-              s2 = fmaf(mx, dx, s2);
+            const float dy0 = g0.y - ((float)(ty * TILE + wave * ROWS + 2 * oh) + 0.5f);
+            const float dy1 = g0.y - ((float)(ty * TILE + wave * ROWS + 2 * oh + 1) + 0.5f);
+            float s0[2], s1[2], s2[2];
 #pragma unroll
-              for (int k = 0; k < CDIM; ++k) acc[5 + k] = fmaf(pr.x, vrc[jc * CDIM + k], acc[5 + k]);
-              if (absg) {
-                const float my = vs * dy;
-                acc[NV] += fabsf(q.x * mx + q.y * my);
-                acc[NV + 1] += fabsf(q.y * mx + q.z * my);
+            for (int rr = 0; rr < 2; ++rr) {
+              uint32_t rb = (hb >> (16 * rr)) & 0xffffu;
+              const float* vrc = &s_vrc[wave * 64 + 32 * oh + 16 * rr][0];
+              const float dy = rr == 0 ? dy0 : dy1;
+              float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+              while (rb != 0u) {
+                const int jc = __builtin_ctz(rb);
+                rb &= rb - 1u;
+                const float2 pr = s_pair[wave][slot++];
+                const float dx = gxr - (float)jc;
+                const float vs = pr.y;
+                const float mx = vs * dx;
+                a0 += vs;
+                a1 += mx;
+                a2 = fmaf(mx, dx, a2);
+#pragma unroll
+                for (int k = 0; k < CDIM; ++k)
+                  acc[5 + k] = fmaf(pr.x, vrc[jc * CDIM + k], acc[5 + k]);
+                if (absg) {
+                  const float my = vs * dy;
+                  acc[NV] += fabsf(q.x * mx + q.y * my);
+                  acc[NV + 1] += fabsf(q.y * mx + q.z * my);
+                }
               }
+              s0[rr] = a0;
+              s1[rr] = a1;
+              s2[rr] = a2;
             }
-            acc[0] = s1;
-            acc[1] = dy * s0;
-            acc[2] = s2;
-            acc[3] = dy * s1;
-            acc[4] = dy * dy * s0;
-            acc[5 + CDIM] = s0;
+            acc[0] = s1[0] + s1[1];
+            acc[1] = dy0 * s0[0] + dy1 * s0[1];
+            acc[2] = s2[0] + s2[1];
+            acc[3] = dy0 * s1[0] + dy1 * s1[1];
+            acc[4] = dy0 * dy0 * s0[0] + dy1 * dy1 * s0[1];
+            acc[5 + CDIM] = s0[0] + s0[1];
           } else {
+            uint32_t rb = hb;
             while (rb != 0u) {
-              const int pl = 16 * oq + __builtin_ctz(rb);
+              const int pl = 32 * oh + __builtin_ctz(rb);
               rb &= rb - 1u;
               const float2 pr = s_pair[wave][slot++];
               const int pix = wave * 64 + pl;
@@ -749,13 +766,12 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
 #pragma unroll
         for (int k = 0; k < NA; ++k) {
           if (k < NV || absg) {
-            // full quad permutes: every source lane exists, so bound_ctrl only
-            // lets the compiler fold each move into its add
+            // full quad permute: every source lane exists, so bound_ctrl only
+            // lets the compiler fold the move into the add
             acc[k] += tgs_dpp<0xB1, 0xf, 0xf, true>(acc[k]);  // quad_perm [1,0,3,2]
-            acc[k] += tgs_dpp<0x4E, 0xf, 0xf, true>(acc[k]);  // quad_perm [2,3,0,1]
           }
         }
-        if (oq == 0 && oe < gn) {
+        if (oh == 0 && oe < gn) {
           float* st = s_stage[wave] + oe * nval;
           st[0] = q.x * acc[0] + q.y * acc[1];
           st[1] = q.y * acc[0] + q.z * acc[1];
@@ -773,7 +789,9 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // 4. flush
+        // 4. flush: (entry, value) pairs in value-fastest order, so that each
+        //    atomic instruction covers a few Gaussians' contiguous records
+        //    (the memory system merges the lanes that hit one line)
         const int total = gn * nval;
         for (int L = lane; L < total; L += 64) {
           const int e = absg ? L / NA : L / NV;
@@ -785,6 +803,10 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
+      // every lane has read its pairs before the next segment clears them
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       a = e_end;
     }
   }
