@@ -53,6 +53,22 @@ def profiled_traffic(kernel: str):
     return None
 
 
+# MI355X VALU issue: one wave64 instruction per clock per CU, 256 CUs at 2.4 GHz
+VALU_ISSUE_PER_S = 256 * 2.4e9
+
+
+def profiled_valu(kernel: str):
+    """Wave64 VALU instructions per launch of `kernel` at cfg3 from the committed
+    rocprofv3 SQ_INSTS_VALU summary (profiles/*_lds_atomics.md), or None."""
+    import re
+
+    for f in sorted((ROOT / "profiles").glob("*_lds_atomics.md")):
+        m = re.search(rf"^valu_insts_per_launch {re.escape(kernel)}: (\d+)", f.read_text(), re.M)
+        if m:
+            return int(m.group(1))
+    return None
+
+
 def cpu_baseline(width, height, frac_a=1 / 16, frac_b=1 / 8, seed=0):
     """Time the CPU oracle on one camera of the same workload with a random
     subset of the Gaussians at two subset sizes, fit t = t_pix + f * t_gauss,
@@ -178,6 +194,13 @@ def bench_step(args, dev):
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(d["GBs"] / HBM_PEAK_GBS, 4),
                     "traffic": profiled_traffic(dominant) if default_cfg else None}
+        # the compositing kernels are limited by VALU issue, not HBM: the
+        # profiled instruction count over the issue rate is their floor
+        valu = profiled_valu(dominant) if default_cfg else None
+        if valu:
+            floor_ms = valu / VALU_ISSUE_PER_S * 1e3
+            roofline["valu"] = {"insts_per_launch": valu, "issue_floor_ms": round(floor_ms, 3),
+                                "frac": round(floor_ms / d["ms"], 4)}
     bwd_names = ("raster_bwd", "project_bwd", "project_bwd_update")
     bwd_ms = sum(kernels[k]["ms"] for k in bwd_names if k in kernels)
     bwd_bytes = sum(kernels[k]["bytes"] for k in bwd_names if k in kernels)
