@@ -315,8 +315,9 @@ __device__ __forceinline__ void lane_bits(const uint64_t* s_em, int n_list, int 
 // ---------------------------------------------------------------------------
 #define RF_BATCH 128  // Gaussians staged per batch
 
+// (up to 4 channels the forward fits 64 VGPRs: 8 wavefronts per SIMD)
 template <int CDIM, int TILE, class Src>
-__global__ void __launch_bounds__(TILE* TILE) raster_fwd_kernel(
+__global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kernel(
     RasterGeom G, Src src, const float* __restrict__ backgrounds,
     const int32_t* __restrict__ tile_offsets, const int32_t* __restrict__ flatten_ids,
     float* __restrict__ render_colors, float* __restrict__ render_alphas,
