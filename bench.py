@@ -131,6 +131,18 @@ def _stage_kernels(ts, stats, args, stage_ms, C, P):
     return kernels
 
 
+def _tile_load(ts, stats):
+    """Max and 99th percentile of the intersections per (camera, tile) of the
+    last step, from its bucket offsets."""
+    import torch
+
+    offs = ts.last["offsets"].reshape(-1).to(torch.int64)
+    ends = torch.cat([offs[1:], offs.new_tensor([stats.n_isects])])
+    per_tile = (ends - offs).double()
+    return {"isects_per_tile_max": int(per_tile.max()),
+            "isects_per_tile_p99": round(float(torch.quantile(per_tile, 0.99)), 1)}
+
+
 def bench_step(args, dev):
     """Full TideGS step (cfg3, cfg4) or the rasterizer pair alone (cfg2)."""
     import torch
@@ -225,6 +237,7 @@ def bench_step(args, dev):
                    "height": sc.height, "visible_entries": stats.entries,
                    "touched_rows": stats.touched_rows, "isects": stats.n_isects,
                    "isects_per_tile": round(stats.n_isects / (C * ts.tw * ts.th), 1),
+                   **_tile_load(ts, stats),
                    "optimizer_update": "split" if args.split_update else "fused"},
         "bwd_hbm_GBs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1) if bwd_ms else None,
         "roofline": roofline,
