@@ -259,6 +259,8 @@ extern "C" int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, f
 #define TL_D1 (TL_T + 2 * SS_R)   // 42: dm region
 #define TL_D2 (TL_T + 4 * SS_R)   // 52: input region
 #define TL_THREADS (TL_T * TL_T)  // 1024
+#define TL_HQ_PITCH 53            // >= TL_D1, 2 x 53 = 42 (mod 64)
+#define TL_H2_PITCH 48            // >= TL_T, 2 x 48 = 32 (mod 64)
 
 __global__ void __launch_bounds__(TL_THREADS, 8) tide_loss_kernel(int H, int W,
                                                                const float* __restrict__ images_hwc,
@@ -276,8 +278,12 @@ __global__ void __launch_bounds__(TL_THREADS, 8) tide_loss_kernel(int H, int W,
     float sdm[3][TL_D1][TL_D1];
   } su;
   __shared__ union {
-    float hq[5][TL_D2][TL_D1];
-    float h2[3][TL_D1][TL_T];
+    // row pitches chosen for the vertical passes' reads: consecutive work
+    // items of a wavefront sit two rows apart, and 2 x pitch = 42 (hq) or
+    // 32 (h2) modulo 64 banks puts the wave's second group of lanes on the
+    // banks the first group leaves free
+    float hq[5][TL_D2][TL_HQ_PITCH];
+    float h2[3][TL_D1][TL_H2_PITCH];
   } sv;
   __shared__ float red[2][TL_THREADS / 64];
   auto& sx = su.in.sx;
