@@ -12,13 +12,14 @@
 //   pos = #ends <= row, state_row = slot[pos]*block_size + (row - start[pos]).
 //
 // The reference issues one Triton launch per component (6 per step) plus host
-// searchsorted/index_select.  Here a single launch covers all 59 columns: one
-// wavefront walks a contiguous range of touched rows, four rows in flight,
-// lane l handles column l (59 of 64 lanes busy), and the row -> (slot, state
-// row) lookup is a wave-uniform binary search on the scalar unit that runs
-// only when the (sorted) rows cross into another resident block.  The column -> (component tensor,
-// column) map is fixed per lane, so the same kernel serves six split component
-// tensors or one unified [N,59] table.
+// searchsorted/index_select.  Here a single launch covers all 59 columns: a
+// wavefront takes groups of touched rows (several rows in flight), lane l
+// handles column l (59 of 64 lanes busy), and the row -> (slot, state row)
+// lookup is wave-uniform and runs only when the (sorted) rows cross into
+// another resident block (see BlockCache).  The column -> (component tensor,
+// column) map is fixed per lane, so one kernel family serves six split
+// component tensors or one unified [N,59] table.  The building blocks are
+// shared with the projection backward's fused update (resident_optim.cuh).
 //
 // Sophia (no reference; Liu et al. 2023, arXiv 2305.14342, Alg. 3 with the
 // per-coordinate clip of SURVEY row A14):
