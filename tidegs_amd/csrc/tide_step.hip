@@ -176,6 +176,7 @@ __global__ void __launch_bounds__(VIS_THREADS) tide_compact_kernel(
     int32_t* __restrict__ touched, int32_t* __restrict__ visit_base,
     int32_t* __restrict__ visits, uint32_t* __restrict__ totals) {
   __shared__ uint32_t s_wave[VIS_THREADS / 64][TIDE_MAX_CAMS + 2];
+  extern __shared__ uint32_t s_vis[];  // [waves][64 * C] visit staging
   const uint32_t nb = gridDim.x;
   const uint64_t n = (uint64_t)blockIdx.x * VIS_THREADS + threadIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -207,27 +208,40 @@ __global__ void __launch_bounds__(VIS_THREADS) tide_compact_kernel(
   }
   if (lane == 63) s_wave[wave][C + 1] = inc;
   __syncthreads();
-  if (n >= n_rows || mask == 0) return;
+  if (__builtin_amdgcn_readfirstlane((int)(tb == 0ull))) return;  // no touched row in the wave
 
   auto wave_prefix = [&](uint32_t k) {
     uint32_t s = 0;
     for (int w = 0; w < wave; ++w) s += s_wave[w][k];
     return s;
   };
-  const uint32_t t = offs[(uint64_t)C * nb + blockIdx.x] - total_entries + wave_prefix(C) + trank;
-  const uint32_t vbase = offs[(uint64_t)(C + 1) * nb + blockIdx.x] - total_entries -
-                         total_touched + wave_prefix(C + 1) + (inc - pc);
-  touched[t] = (int32_t)n;
-  visit_base[t] = (int32_t)vbase;
-  uint32_t j = 0;
+  const bool act = n < n_rows && mask != 0u;
+  // the wave's visits are one contiguous range [wv0, wv0 + s_wave[wave][C+1]):
+  // each lane puts its visits into the wave's LDS slice, and the wave stores
+  // the slice with consecutive lanes (whole lines instead of one scattered
+  // word per lane and camera)
+  const uint32_t wv0 = offs[(uint64_t)(C + 1) * nb + blockIdx.x] - total_entries - total_touched +
+                       wave_prefix(C + 1);
+  uint32_t* sv = s_vis + (uint64_t)wave * 64u * C;
+  if (act) {
+    const uint32_t t =
+        offs[(uint64_t)C * nb + blockIdx.x] - total_entries + wave_prefix(C) + trank;
+    touched[t] = (int32_t)n;
+    visit_base[t] = (int32_t)(wv0 + (inc - pc));
+  }
+  uint32_t j = inc - pc;
   for (uint32_t c = 0; c < C; ++c) {
-    if ((mask >> c) & 1u) {
+    if (act && ((mask >> c) & 1u)) {
       const uint32_t e = offs[(uint64_t)c * nb + blockIdx.x] + wave_prefix(c) + rank[c];
       entries[e] = (int32_t)n;
-      visits[vbase + j] = (int32_t)e;
-      ++j;
+      sv[j++] = e;
     }
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint32_t wtot = s_wave[wave][C + 1];
+  for (uint32_t k = (uint32_t)lane; k < wtot; k += 64u) visits[wv0 + k] = (int32_t)sv[k];
   (void)totals;
 }
 
@@ -767,8 +781,9 @@ extern "C" int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* mas
                     cam_offsets,
                 "tide_compact: null");
   const uint32_t nb = tgs_tide_row_blocks(n_rows);
-  hipLaunchKernelGGL(tide_compact_kernel, dim3(nb), dim3(VIS_THREADS), 0, stream, n_rows, C,
-                     masks, offs, entries, touched, visit_base, visits, totals);
+  hipLaunchKernelGGL(tide_compact_kernel, dim3(nb), dim3(VIS_THREADS),
+                     (size_t)VIS_THREADS * C * sizeof(uint32_t), stream, n_rows, C, masks, offs,
+                     entries, touched, visit_base, visits, totals);
   TGS_LAUNCH_CHECK("tgs_tide_compact");
   hipLaunchKernelGGL(tide_totals_kernel, dim3(1), dim3(64), 0, stream, C, nb, counts, offs,
                      totals, cam_offsets, visit_base);
