@@ -352,15 +352,19 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
   float sh[48];
 #pragma unroll
   for (int k = 0; k < 48; ++k) sh[k] = row[11 + k];
-  uint32_t mask = masks[n];
+  const uint32_t mask = masks[n];
   const int32_t* vis = visits + visit_base[t];
-  for (int j = 0; mask != 0u; ++j) {
-    const uint32_t c = (uint32_t)__builtin_ctz(mask);
-    mask &= mask - 1u;
-    const uint32_t e = (uint32_t)vis[j];
-    project_entry(p, Sigma, opac, sh, s_cam.cam[c], s_cam.campos[c], W, H, eps2d, near_plane,
-                  far_plane, radius_clip, sh_degree, tile_size, tw, th, e, splats, depth_keys,
-                  entry_rects);
+  // cameras in lockstep across the wavefront: the camera's constants are an
+  // LDS broadcast, and the lanes seeing camera c write consecutive entries of
+  // its list (coalesced records)
+  int j = 0;
+  for (uint32_t c = 0; c < tc.C; ++c) {
+    if ((mask >> c) & 1u) {
+      const uint32_t e = (uint32_t)vis[j++];
+      project_entry(p, Sigma, opac, sh, s_cam.cam[c], s_cam.campos[c], W, H, eps2d, near_plane,
+                    far_plane, radius_clip, sh_degree, tile_size, tw, th, e, splats, depth_keys,
+                    entry_rects);
+    }
   }
 }
 
@@ -475,9 +479,9 @@ __global__ void __launch_bounds__(256) tide_isect_ids_kernel(
 __device__ __forceinline__ void tide_row_grads(
     uint32_t t, int32_t r, const int32_t* __restrict__ visit_base,
     const int32_t* __restrict__ visits, const uint32_t* __restrict__ masks, const CamLDS& s_cam,
-    const float* params, uint32_t row_stride, int W, int H, float eps2d, float near_plane,
-    float far_plane, float radius_clip, int sh_degree, const float* __restrict__ splat_grads,
-    float out[TIDE_ROW]) {
+    uint32_t n_cams, const float* params, uint32_t row_stride, int W, int H, float eps2d,
+    float near_plane, float far_plane, float radius_clip, int sh_degree,
+    const float* __restrict__ splat_grads, float out[TIDE_ROW]) {
   const float* row = params + (uint64_t)r * row_stride;
   const float p[3] = {row[0], row[1], row[2]};
   const float s[3] = {expf(row[3]), expf(row[4]), expf(row[5])};
@@ -503,12 +507,14 @@ __device__ __forceinline__ void tide_row_grads(
   // visits in camera order = the set bits of the row's visibility mask; the
   // render projection is recomputed (bit-identical to the forward's) instead
   // of reading the conic and radius back from the splat records
-  uint32_t mask = masks[r];
+  // (cameras in lockstep across the wavefront: LDS broadcasts of the camera,
+  // and the lanes seeing camera c read consecutive splat-gradient records)
+  const uint32_t mask = masks[r];
   const int32_t* vis = visits + visit_base[t];
-  for (int j = 0; mask != 0u; ++j) {
-    const uint32_t c = (uint32_t)__builtin_ctz(mask);
-    mask &= mask - 1u;
-    const uint32_t e = (uint32_t)vis[j];
+  int j = 0;
+  for (uint32_t c = 0; c < n_cams; ++c) {
+    if (!((mask >> c) & 1u)) continue;
+    const uint32_t e = (uint32_t)vis[j++];
     const ProjResult pr =
         project_forward(p, Sigma, s_cam.cam[c], W, H, eps2d, near_plane, far_plane, radius_clip);
     if (pr.radius <= 0) continue;  // culled by the render projection: zero gradient
@@ -569,8 +575,8 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_touched) return;
   float g[TIDE_ROW];
-  tide_row_grads(t, touched[t], visit_base, visits, masks, s_cam, params, row_stride, W, H, eps2d,
-                 near_plane, far_plane, radius_clip, sh_degree, splat_grads, g);
+  tide_row_grads(t, touched[t], visit_base, visits, masks, s_cam, tc.C, params, row_stride, W, H,
+                 eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads, g);
   float* out = grads + (uint64_t)t * grad_stride;
 #pragma unroll
   for (int k = 0; k < TIDE_ROW; ++k) out[k] = g[k];
@@ -624,8 +630,8 @@ __global__ void __launch_bounds__(256) tide_project_bwd_optim_kernel(
   if (t < n_touched) {
     my_row = touched[t];
     float g[TIDE_ROW];
-    tide_row_grads(t, my_row, visit_base, visits, masks, s_cam, params, row_stride, W, H, eps2d,
-                   near_plane, far_plane, radius_clip, sh_degree, splat_grads, g);
+    tide_row_grads(t, my_row, visit_base, visits, masks, s_cam, tc.C, params, row_stride, W, H,
+                   eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads, g);
 #pragma unroll
     for (int k = 0; k < TIDE_ROW; ++k) sg[lane * FUSED_PITCH + k] = g[k];
   }
