@@ -504,6 +504,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   __shared__ uint64_t s_em[WAVES][BATCH];         // pixel mask of each list entry
   __shared__ uint16_t s_po[WAVES][BATCH + 1];     // first pair slot of each list entry
   __shared__ float s_stage[WAVES][32 * NA];       // one owner group's gradient values
+  __shared__ int32_t s_gid[WAVES][32];            // and their Gaussian ids
 
   const uint32_t cam = blockIdx.x;
   const uint32_t ty = blockIdx.y, tx = blockIdx.z;
@@ -773,6 +774,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
           }
         }
         if (oh == 0 && oe < gn) {
+          s_gid[wave][oe] = s_id[t];
           float* st = s_stage[wave] + oe * nval;
           st[0] = q.x * acc[0] + q.y * acc[1];
           st[1] = q.y * acc[0] + q.z * acc[1];
@@ -798,7 +800,7 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
           const int e = absg ? L / NA : L / NV;
           const int k = L - e * nval;
           const float v = s_stage[wave][L];
-          if (v != 0.f) tgs_atomic_add(sink.ptr(s_id[s_list[wave][e0 + e]], k), v);
+          if (v != 0.f) tgs_atomic_add(sink.ptr(s_gid[wave][e], k), v);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
