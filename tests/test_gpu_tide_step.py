@@ -185,3 +185,20 @@ def test_fused_update_matches_two_launch_step(gpu, optimizer, pitch, block_size)
     np.testing.assert_allclose(a.losses(sc.width, sc.height), b.losses(sc.width, sc.height),
                                rtol=1e-5)
     assert fused.last["grads"] is None and of.get_stats() == os_.get_stats()
+
+
+def test_fused_step_trains(gpu):
+    """End to end: repeated fused steps (forward, backward, update in the
+    projection-backward launch) fit the targets: the batch loss falls and the
+    table stays finite."""
+    announce("tide step: 40 fused training steps")
+    sc = _scene(seed=5, n=6000, C=3)
+    ts = TideStep(sc.params.to(gpu).contiguous(), sc.width, sc.height, batch_size=sc.n_cams)
+    losses = []
+    for _ in range(40):
+        st = ts.step(sc.viewmats, sc.Ks, sc.gt)
+        losses.append(sum(st.losses(sc.width, sc.height)) / sc.n_cams)
+    print(f"  loss {losses[0]:.5f} -> {losses[-1]:.5f}")
+    assert bool(torch.isfinite(ts.params).all())
+    assert losses[-1] < 0.97 * losses[0]
+    assert sum(losses[-5:]) < sum(losses[:5])
