@@ -597,6 +597,7 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
 // wavefront only.
 #define FUSED_PITCH 61  // odd LDS pitch: both phases' accesses are conflict-free
 #define FUSED_ROWS 32   // rows in flight per wavefront in phase 2
+#define FUSED_THREADS 128  // two wavefronts per workgroup
 
 struct TideOptim {
   OptimLayout L;
@@ -612,14 +613,14 @@ struct TideOptim {
 };
 
 template <bool SOPHIA>
-__global__ void __launch_bounds__(256) tide_project_bwd_optim_kernel(
+__global__ void __launch_bounds__(FUSED_THREADS) tide_project_bwd_optim_kernel(
     uint32_t n_touched, const int32_t* __restrict__ touched,
     const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
     const uint32_t* __restrict__ masks, TideCams tc, float* __restrict__ params,
     uint32_t row_stride, int W, int H, float eps2d, float near_plane, float far_plane,
     float radius_clip, int sh_degree, const float* __restrict__ splat_grads, TideOptim O) {
   __shared__ CamLDS s_cam;
-  __shared__ float s_g[4][64 * FUSED_PITCH];
+  __shared__ float s_g[FUSED_THREADS / 64][64 * FUSED_PITCH];
   load_cams_lds(tc, s_cam);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -980,11 +981,11 @@ extern "C" int tgs_tide_project_bwd_update(
   O.update_h = update_hessian;
   O.state_pitch = (int)state_pitch;
   O.error_flag = error_flag;
-#define TIDE_FUSED_LAUNCH(SOPHIA)                                                                 \
-  hipLaunchKernelGGL(tide_project_bwd_optim_kernel<SOPHIA>, dim3(tgs_blocks(n_touched, 256)),     \
-                     dim3(256), 0, stream, n_touched, touched, visit_base, visits, masks, tc,      \
-                     params, row_stride, W, H, eps2d, near_plane, far_plane, radius_clip,          \
-                     sh_degree, splat_grads, O)
+#define TIDE_FUSED_LAUNCH(SOPHIA)                                                              \
+  hipLaunchKernelGGL(tide_project_bwd_optim_kernel<SOPHIA>,                                     \
+                     dim3(tgs_blocks(n_touched, FUSED_THREADS)), dim3(FUSED_THREADS), 0, stream, \
+                     n_touched, touched, visit_base, visits, masks, tc, params, row_stride, W, H, \
+                     eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads, O)
   if (optimizer == 1)
     TIDE_FUSED_LAUNCH(true);
   else
