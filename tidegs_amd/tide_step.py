@@ -238,10 +238,6 @@ class TideStep:
         tot = totals.cpu().tolist()  # sync 1
         V = tot[C + 1]
         T = tot[C]
-        if update and T:
-            # per-block touch counts for the optimizer's slot bookkeeping,
-            # on the host by sync 2
-            counts_host = self.optimizer.launch_touch_counts(self.gaussians, touched[:T])
 
         # 2. projection + SH colours for every (camera, visible row), one pass over
         #    the touched rows; depth keys and tile rectangles for the sort
@@ -256,6 +252,11 @@ class TideStep:
                self.eps2d, self.near, self.far, 0.0, self.sh_degree, self.TILE, tw, th,
                N.ptr(splats), N.ptr(dkeys), N.ptr(rects), s)
         self._end()
+        if update and T:
+            # per-block touch counts for the optimizer's slot bookkeeping, on
+            # the host by sync 2 (launched after the projection, which needs
+            # the GPU first after sync 1)
+            counts_host = self.optimizer.launch_touch_counts(self.gaussians, touched[:T])
 
         # 3. intersections in the reference's (camera, tile, depth, entry) order:
         #    depth sort of the entries per camera, count + scan, emission in depth
