@@ -313,8 +313,10 @@ int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched, const int32
  * tgs_segmented_sort_pairs_u32 of (depth_keys, entry_rects) per camera:
  *   tgs_tide_isect_count     tiles [V] of the depth-ordered entries;
  *   (tgs_inclusive_scan_i32_i64 -> cum_tiles)
- *   tgs_tide_isect_segments  seg [C+1]: first intersection of each camera
- *                            (seg[C] = n_isects);
+ *   tgs_tide_isect_segments  seg [C+1] (int64): first intersection of each
+ *                            camera (seg[C] = n_isects; the caller must refuse
+ *                            n_isects >= 2^31 before emitting: keys, flatten
+ *                            ids and the bucket offsets are 32-bit);
  *   tgs_tide_isect_emit      keys [n_isects] = camera << tile_n_bits | tile,
  *                            flatten_ids = entry index, in depth order;
  *   (tgs_segmented_sort_pairs_u32 of the tile bits per camera)
@@ -323,7 +325,7 @@ int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched, const int32
 int tgs_tide_isect_count(uint32_t n_entries, const uint64_t* entry_rects, int32_t* tiles,
                          tgs_stream_t stream);
 int tgs_tide_isect_segments(uint32_t C, const int32_t* cam_offsets, const int64_t* cum_tiles,
-                            uint32_t* seg, tgs_stream_t stream);
+                            int64_t* seg, tgs_stream_t stream);
 int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,
                         const uint64_t* entry_rects, const int64_t* cum_tiles,
                         uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,

@@ -39,22 +39,72 @@ def _split(params: torch.Tensor):
 
 def packed_filters(params, viewmats, Ks, W, H, eps2d=0.3, near=0.01, far=1e10, radius_clip=0.0,
                    dtype=torch.float64):
-    """Per-camera ascending row ids visible under the packed-projection rule."""
+    """Per-camera ascending row ids visible under the packed-projection rule.
+
+    A row is in camera c's filter when gsplat's packed projection keeps it
+    (``fully_fused_projection_packed_fwd.cu:50-131``, consumed as the filter at
+    ``base_engine.py:329-425``): the radius of ``gsplat_ref.project_fwd(...,
+    packed=True)`` is positive.  The rows' activations are TideGS's
+    (``base_gaussian_model.py:35-50``: ``exp`` of the log-scales, the
+    quaternion normalised as ``q / max(|q|, 1e-12)``)."""
     xyz, logs, q, _, _ = _split(params.to(dtype))
     qn = q / torch.clamp(q.norm(dim=-1, keepdim=True), min=1e-12)
+    radii = G.project_fwd(xyz, qn, torch.exp(logs), viewmats, Ks, W, H, eps2d=eps2d,
+                          near_plane=near, far_plane=far, radius_clip=radius_clip, dtype=dtype,
+                          packed=True)[0]
+    return [torch.nonzero(radii[c] > 0).flatten() for c in range(radii.shape[0])]
+
+
+def packed_filter_ambiguous(params, viewmats, Ks, W, H, eps2d=0.3, near=0.01, far=1e10,
+                            radius_clip=0.0, rel=2e-5):
+    """[C, N] bool: entries whose packed-filter decision sits within float32
+    rounding of a boundary, evaluated in float64.
+
+    The GPU evaluates the rule in float32; the oracle in float64.  Far from a
+    boundary both give the same decision; within a relative ``rel`` of one they
+    may not.  An entry is flagged when any of these holds:
+
+    * ``z`` within ``rel * (|p| + |t|)`` of the near or far plane;
+    * ``det`` of the blurred covariance within ``rel * a d`` of zero;
+    * ``3 sqrt(v1)`` within a relative ``rel`` of an integer (the radius, a
+      ceiling, may then be one larger or smaller), where that changes the
+      radius-clip or image-border decision;
+    * the mean within ``rel`` (relative to its pixel magnitude) of flipping an
+      image-border test at either candidate radius.
+
+    Any difference between the GPU's filters and ``packed_filters`` must lie
+    inside this set; ``tests/test_oracle_step.py`` checks that float32
+    evaluations of the rule only ever differ from float64 there."""
+    f64 = torch.float64
+    xyz, logs, q, _, _ = _split(params.to(f64))
+    qn = q / torch.clamp(q.norm(dim=-1, keepdim=True), min=1e-12)
     Sigma = G.covar_from_quat_scale(qn, torch.exp(logs))
-    pc, m2d, a, b, d, det, conics, comp = G.project_core(xyz, Sigma, viewmats.to(dtype),
-                                                         Ks.to(dtype), W, H, eps2d)
+    vm, Kd = viewmats.to(f64), Ks.to(f64)
+    pc, m2d, a, b, d, det, _, _ = G.project_core(xyz, Sigma, vm, Kd, W, H, eps2d)
     z = pc[..., 2]
-    ok = (z >= near) & (z <= far) & (det > 0)
+    scale_z = xyz.abs().sum(-1)[None] + vm[:, :3, 3].abs().sum(-1)[:, None] + 1.0
+    amb = ((z - near).abs() <= rel * scale_z) | ((z - far).abs() <= rel * scale_z)
+    amb |= det.abs() <= rel * (a * d).abs()
     bb = 0.5 * (a + d)
-    s = torch.sqrt(torch.clamp(bb * bb - det, min=0.1))
-    radius = torch.ceil(3.0 * torch.sqrt(torch.maximum(bb + s, bb - s)))
-    ok &= ~(radius <= radius_clip)
-    mx, my = m2d[..., 0], m2d[..., 1]
-    ok &= ~((mx + radius <= 0) | (mx - radius >= W) | (my + radius <= 0) | (my - radius >= H))
-    ok &= torch.isfinite(radius)
-    return [torch.nonzero(ok[c]).flatten() for c in range(ok.shape[0])]
+    v1 = bb + torch.sqrt(torch.clamp(bb * bb - det, min=0.1))
+    rr = 3.0 * torch.sqrt(v1)
+    r_lo = torch.ceil(rr * (1 - rel))
+    r_hi = torch.ceil(rr * (1 + rel))
+    fx, fy = Kd[:, 0, 0][:, None], Kd[:, 1, 1][:, None]
+    cx, cy = Kd[:, 0, 2][:, None], Kd[:, 1, 2][:, None]
+    tol_x = rel * ((m2d[..., 0] - cx).abs() + cx.abs() + 1.0)
+    tol_y = rel * ((m2d[..., 1] - cy).abs() + cy.abs() + 1.0)
+    outcomes = []
+    for r in (r_lo, r_hi):
+        for sx in (-1.0, 1.0):
+            for sy in (-1.0, 1.0):
+                mx = m2d[..., 0] + sx * tol_x
+                my = m2d[..., 1] + sy * tol_y
+                out = (mx + r <= 0) | (mx - r >= W) | (my + r <= 0) | (my - r >= H)
+                outcomes.append(out | (r <= radius_clip))
+    stack = torch.stack(outcomes)
+    amb |= stack.any(0) != stack.all(0)
+    return amb & torch.isfinite(rr)
 
 
 def camera_step(params, rows, viewmat, K, gt, W, H, sh_degree=3, background=None, tile=16,
@@ -112,9 +162,16 @@ def camera_step(params, rows, viewmat, K, gt, W, H, sh_degree=3, background=None
 
 
 def batch_grads(params, viewmats, Ks, gts, W, H, sh_degree=3, backgrounds=None,
-                proj_dtype=torch.float64, raster_dtype=np.float32, lambda_dssim=0.2):
-    """touched rows [T], compact grads [T,59], per-camera losses and images."""
-    filters = packed_filters(params, viewmats, Ks, W, H)
+                proj_dtype=torch.float64, raster_dtype=np.float32, lambda_dssim=0.2,
+                filters=None):
+    """touched rows [T], compact grads [T,59], per-camera losses and images.
+
+    ``filters`` (per-camera ascending row ids) replaces the packed-filter
+    evaluation, so that a caller can run the rest of the batch on exactly the
+    filters another implementation chose (identical inputs)."""
+    if filters is None:
+        filters = packed_filters(params, viewmats, Ks, W, H)
+    filters = [torch.as_tensor(f, dtype=torch.long) for f in filters]
     touched = torch.unique(torch.cat(filters)) if filters else torch.empty(0, dtype=torch.long)
     grads = torch.zeros((touched.numel(), 59), dtype=proj_dtype)
     losses, images = [], []

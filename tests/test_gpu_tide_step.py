@@ -136,14 +136,16 @@ def test_fused_update_matches_two_launch_step(gpu, optimizer, pitch, block_size)
     kw = dict(batch_size=3, block_size=block_size, optimizer=optimizer)
     fused = TideStep(table(), sc.width, sc.height, **kw)
     split = TideStep(table(), sc.width, sc.height, fuse_update=False, **kw)
-    # evict and re-admit every block: the state slots come back in another
-    # order, so the block -> slot map is not the identity
+    # evict every block, admit the second half, then all: the first half
+    # lands in the slots after the second half's, so the block -> slot map is
+    # not the identity
     for ts in (fused, split):
         blocks = list(ts.manager.loaded_blocks)
         ts.optimizer.set_resident_blocks([])
+        ts.optimizer.set_resident_blocks(blocks[len(blocks) // 2:])
         ts.optimizer.set_resident_blocks(blocks)
-    slots = [fused.optimizer._block_to_slot[b] for b in fused.manager.loaded_blocks]
-    assert slots != sorted(slots)
+    slots = [fused.optimizer.slot_of(b) for b in fused.manager.loaded_blocks]
+    assert slots != sorted(slots) and sorted(slots) == list(range(len(slots)))
     before = fused.params.clone()
     idle = np.ones(sc.params.shape[0], dtype=bool)  # rows that no camera saw in any step
     s = N.stream_handle(gpu)

@@ -387,11 +387,11 @@ __global__ void __launch_bounds__(256) tide_isect_count_kernel(
 
 __global__ void tide_isect_segments_kernel(uint32_t C, const int32_t* __restrict__ cam_offsets,
                                            const int64_t* __restrict__ cum_tiles,
-                                           uint32_t* __restrict__ seg) {
+                                           int64_t* __restrict__ seg) {
   const uint32_t c = threadIdx.x;
   if (c > C) return;
   const int32_t o = cam_offsets[c];
-  seg[c] = o > 0 ? (uint32_t)cum_tiles[o - 1] : 0u;
+  seg[c] = o > 0 ? cum_tiles[o - 1] : 0;
 }
 
 __global__ void __launch_bounds__(256) tide_isect_emit_kernel(
@@ -839,7 +839,7 @@ extern "C" int tgs_tide_isect_count(uint32_t n_entries, const uint64_t* entry_re
 }
 
 extern "C" int tgs_tide_isect_segments(uint32_t C, const int32_t* cam_offsets,
-                                       const int64_t* cum_tiles, uint32_t* seg,
+                                       const int64_t* cum_tiles, int64_t* seg,
                                        hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;

@@ -91,6 +91,29 @@ class StepStats:
                 for c in range(s.shape[0])]
 
 
+# Index widths of the fused step: entries, visits and the per-block count scan
+# are 32-bit (the scan's total is V + T + V <= (2C + 1) N), and intersection
+# keys, flatten ids and the per-tile offsets are int32 as in the reference's
+# rasterizer (rasterize_to_pixels_fwd.cu: int32 tile ranges).
+MAX_ISECTS = (1 << 31) - 1
+
+
+def check_batch_capacity(n_rows: int, n_cams: int) -> None:
+    """Refuse a batch whose 32-bit entry/visit counts could wrap."""
+    if (2 * int(n_cams) + 1) * int(n_rows) >= (1 << 32):
+        raise ValueError(
+            f"TideStep: {n_rows} rows x {n_cams} cameras exceeds the 32-bit entry counts "
+            f"((2C+1)*N must stay below 2^32); use fewer cameras per batch")
+
+
+def check_isect_count(n_isects: int) -> None:
+    """Refuse an intersection count that does not fit the int32 tile ranges."""
+    if not 0 <= int(n_isects) <= MAX_ISECTS:
+        raise RuntimeError(
+            f"TideStep: {n_isects} intersections in one batch exceed the int32 range of the "
+            f"tile offsets and flatten ids (max {MAX_ISECTS}); use fewer cameras per batch")
+
+
 def _segments(offsets) -> "ctypes.Array":
     """Host uint32 array of segment offsets for tgs_segmented_sort_pairs_u32."""
     return (ctypes.c_uint32 * len(offsets))(*[int(o) for o in offsets])
@@ -204,6 +227,7 @@ class TideStep:
         s = N.stream_handle(self.device)
         P = self.params
         n = P.shape[0]
+        check_batch_capacity(n, C)
         W, H, tw, th = self.W, self.H, self.tw, self.th
         viewmats = viewmats.to(self.device, torch.float32).contiguous()
         Ks = Ks.to(self.device, torch.float32).contiguous()
@@ -266,7 +290,7 @@ class TideStep:
         rects2 = self._buf("entry_rects2", max(V, 1), torch.int64)
         tiles = self._buf("tiles", max(V, 1), torch.int32)
         cum = self._buf("cum_tiles", max(V, 1), torch.int64)
-        seg = self._buf("isect_segs", C + 1, torch.int32)
+        seg = self._buf("isect_segs", C + 1, torch.int64)
         ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(max(V, 1)), torch.uint8)
         self._begin("isect_scan")
         if V:
@@ -286,6 +310,7 @@ class TideStep:
         self._end()
         isect_segs = seg.cpu().tolist()  # sync 2
         n_isects = isect_segs[C]
+        check_isect_count(n_isects)
         tile_bits = (tw * th).bit_length()
         cap = max(n_isects, 1)
         keys = self._buf("keys", cap, torch.int32)
