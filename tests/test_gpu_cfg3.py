@@ -12,19 +12,33 @@ forward + backward + fused resident Adam).
   update that ``bench.py`` times, checked by size-independent properties and
   against the two-launch form on the same per-entry gradients.
 
-Index work: the GPU evaluates the packed-filter rule in float32, the oracle in
-float64.  Filters must agree exactly except on entries whose decision lies
-within float32 rounding of a boundary (``step_ref.packed_filter_ambiguous``);
-the oracle then runs the rest of the batch on the GPU's filters (identical
-inputs), and touched rows, losses, images and gradients are compared there.
-Tolerances: gradients relative L2 <= 1e-4 per parameter group (the north-star
-bound), images relative L2 <= 1e-4 with at most 0.05% of pixels off by more
-than 1e-4 (alpha cut-off flips of the hardware exp2), losses 1e-5 relative.
+Each oracle comparison runs in four stages:
+
+(A) filters: the GPU evaluates the packed rule in float32, the oracle in
+    float64; they must agree exactly except on entries whose decision lies
+    within float32 rounding of a boundary (``step_ref.packed_filter_ambiguous``).
+(B) the render projection: the GPU's splat records (radius, mean, depth,
+    conic, colour, opacity) against the oracle's float64 values on the same
+    rows; radii exact off rounding boundaries, the rest within tolerances.
+(C) everything downstream on identical inputs (the GPU's records and lists):
+    compositing forward, loss and its gradient, compositing backward, and the
+    projection + SH + activation backward into the row gradients, each within
+    relative L2 1e-4 (measured 1e-7..3e-5).
+(D) the oracle end to end from the rows (its own float64 projection).  At
+    1080p a float32 and a float64 forward differ at a few alpha = 1/255
+    cut-offs (a pixel moves by up to 4e-3), and where such a pixel crosses
+    its random target the L1 gradient changes sign: one flip alone moves the
+    loss gradient by 2/sqrt(3 W H) = 8e-4 relative L2 at 1920x1080.  So (D)
+    is bounded loosely (1e-2; 5e-2 for the 320x256 window, where one flip is
+    4e-3) and prints the flips; the 1e-4 bound is held in (C).
+
 """
 import numpy as np
 import pytest
 import torch
 
+from oracle import raster_ref as R
+from oracle import ssim_ref as S
 from oracle import step_ref as SR
 from tests.gpu_util import announce, check_isect_properties, rel_l2, to_np
 from tidegs_amd import _native as N
@@ -50,14 +64,101 @@ def _gpu_filters(ts):
     return [entries[offs[c]:offs[c + 1]].astype(np.int64) for c in range(len(offs) - 1)]
 
 
-def _parity(gpu, params, vm, K, gt, W, H, label):
+def _check_render_projection(ts, params, g_filters, vm, K, W, H):
+    """(B) The GPU's per-entry splat records against the oracle's float64
+    render projection of the same rows: radii equal except where 3 sqrt(v1)
+    sits within float32 rounding of an integer (the ceiling) or the mean
+    within rounding of an image-border cut; on live entries means2d within
+    2e-3 px, depths within 4 ulp of float32, conics within 1e-5 relative L2,
+    colours within 2e-5 and opacities within 1e-6."""
+    sp = to_np(ts.last["splats"])
+    offs = to_np(ts.last["cam_offsets"])
+    for c, rows in enumerate(g_filters):
+        rec = sp[offs[c]:offs[c + 1]]
+        r_o, m_o, d_o, rr = (t.numpy() for t in SR.render_projection(
+            params, torch.from_numpy(rows), vm[c], K[c], W, H))
+        r_g = rec[:, 7].astype(np.int64)
+        diff = np.nonzero(r_g != r_o)[0]
+        r = np.maximum(r_g, r_o)[diff]
+        mx, my = m_o[diff, 0], m_o[diff, 1]
+        slack = np.min(np.abs(np.stack([mx + r, mx - r - W, my + r, my - r - H])), axis=0)
+        ok = (np.abs(rr[diff] - np.round(rr[diff])) <= 1e-5 * rr[diff]) | (slack <= 2e-3)
+        assert np.all(ok), f"camera {c}: radii differ off a boundary at entries {diff[~ok][:8]}"
+        assert diff.size <= max(3, len(rows) // 20_000), diff.size
+        live = (r_g > 0) & (r_o > 0)
+        assert np.abs(rec[live, 0:2] - m_o[live]).max() <= 2e-3
+        d32 = d_o[live].astype(np.float32)
+        assert np.all(np.abs(rec[live, 3] - d32) <= 4 * np.spacing(np.abs(d32)))
+        f = SR._render_entries(params, torch.from_numpy(rows), vm[c], K[c], W, H, 3,
+                               torch.float64)
+        assert rel_l2(rec[live, 4:7], f.conics[0].numpy()[live]) < 1e-5
+        assert np.abs(rec[live, 8:11] - f.colors.numpy()[live]).max() < 2e-5
+        assert np.abs(rec[live, 2] - f.opac.numpy()[live]).max() < 1e-6
+
+
+def _camera_lists(ts, c, n_isects):
+    """Camera c's entry records, per-tile offsets and flatten ids (local
+    entry indices) from the fused step's batched lists."""
+    L = ts.last
+    offs = to_np(L["cam_offsets"])
+    toffs = to_np(L["offsets"]).astype(np.int64)
+    C = len(offs) - 1
+    start = int(toffs[c].reshape(-1)[0])
+    end = int(toffs[c + 1].reshape(-1)[0]) if c + 1 < C else n_isects
+    flat = (to_np(L["flatten_ids"])[start:end] - offs[c]).astype(np.int32)
+    return (to_np(L["splats"])[offs[c]:offs[c + 1]], (toffs[c] - start)[None].astype(np.int32),
+            flat)
+
+
+def _check_downstream(ts, stats, params, g_filters, vm, K, gt, W, H, grads):
+    """(C) Everything after the projection forward on identical inputs (the
+    GPU's splat records and intersection lists): the oracle's compositing
+    forward, loss and loss gradient on the GPU's image, compositing backward
+    on the GPU's loss gradient, and the projection + SH + activation backward
+    on the GPU's splat gradients, each against the GPU's result."""
+    L = ts.last
+    imgs, vimg = to_np(L["images"]), to_np(L["v_images"])
+    sgr = to_np(L["splat_grads"])
+    offs = to_np(L["cam_offsets"])
+    losses = stats.losses(W, H)
+    per_cam = []
+    for c in range(len(g_filters)):
+        rec, toffs, flat = _camera_lists(ts, c, stats.n_isects)
+        splat = (rec[:, 0:2], rec[:, 4:7], rec[:, 8:11], rec[:, 2])
+        img, alphas, last = R.rasterize_fwd(*splat, W, H, 16, toffs, flat)
+        assert rel_l2(imgs[c], img[0]) < 1e-5
+        loss, v_ref = S.tide_loss(imgs[c].transpose(2, 0, 1), to_np(gt[c]), dtype=np.float64)
+        assert abs(loss - losses[c]) < 1e-6
+        assert rel_l2(vimg[c].transpose(2, 0, 1), v_ref) < 1e-5
+        vm2, vcon, vcol, vop, _ = R.rasterize_bwd(*splat, W, H, 16, toffs, flat, alphas, last,
+                                                  vimg[c][None])
+        mine = sgr[offs[c]:offs[c + 1]]
+        for name, got, ref in (("means2d", mine[:, 0:2], vm2), ("conics", mine[:, 2:5], vcon),
+                               ("colors", mine[:, 5:8], vcol), ("opacities", mine[:, 8], vop)):
+            err = rel_l2(got, ref)
+            print(f"  camera {c} splat grad {name}: rel_l2={err:.2e}")
+            assert err < 1e-4, (c, name, err)
+        per_cam.append((mine[:, 0:2], mine[:, 2:5], mine[:, 5:8], mine[:, 8]))
+    touched, og = SR.batch_row_grads(params, vm, K, W, H, [torch.from_numpy(f) for f in g_filters],
+                                     per_cam)
+    np.testing.assert_array_equal(to_np(ts.last["touched"]), to_np(touched))
+    g, og = to_np(grads), to_np(og)
+    for name, sl in GROUPS.items():
+        err = rel_l2(g[:, sl], og[:, sl])
+        print(f"  row grad {name} (identical splat grads): rel_l2={err:.2e}")
+        assert err < 1e-4, (name, err)
+
+
+def _parity(gpu, params, vm, K, gt, W, H, label, end_to_end_bound):
     """forward_backward on the GPU (resident table at the bench's 256-byte row
-    pitch) against the step oracle on the GPU's filters."""
+    pitch) against the step oracle: (A) filters, (B) render projection, (C)
+    the rest on identical inputs, (D) the oracle end to end."""
     table = scenes.padded_table(params.to(gpu).contiguous())
     C = vm.shape[0]
     ts = TideStep(table, W, H, batch_size=C)
     touched, grads, stats = ts.forward_backward(vm, K, gt)
     torch.cuda.synchronize()
+    # (A) filters: exact off float32 rounding boundaries
     g_filters = _gpu_filters(ts)
     o_filters = SR.packed_filters(params, vm, K, W, H)
     amb = SR.packed_filter_ambiguous(params, vm, K, W, H).numpy()
@@ -76,18 +177,30 @@ def _parity(gpu, params, vm, K, gt, W, H, label):
           f"{stats.n_isects} isects; filter flips at float32 boundaries: {flips} "
           f"(ambiguous entries {int(amb.sum())})")
     assert stats.entries > 50_000 and flips <= max(3, stats.entries // 20_000)
+    _check_render_projection(ts, params, g_filters, vm, K, W, H)       # (B)
+    _check_downstream(ts, stats, params, g_filters, vm, K, gt, W, H, grads)  # (C)
+    # (D) the oracle end to end from the row parameters (its own float64
+    # projection, intersected on the GPU's float32 means/radii/depths)
+    isect_inputs = []
+    for c in range(C):
+        rec = _camera_lists(ts, c, stats.n_isects)[0]
+        isect_inputs.append((rec[:, 0:2], rec[:, 7], rec[:, 3]))
     o_touched, o_grads, o_losses, o_images, _ = SR.batch_grads(
-        params, vm, K, gt, W, H, filters=[torch.from_numpy(f) for f in g_filters])
+        params, vm, K, gt, W, H, filters=[torch.from_numpy(f) for f in g_filters],
+        isect_inputs=isect_inputs)
     np.testing.assert_array_equal(to_np(touched), to_np(o_touched))
     imgs = to_np(ts.last["images"])
+    sign_flips = 0
     for c in range(C):
         _image_close(imgs[c].reshape(-1, 3), o_images[c].reshape(-1, 3))
+        target = np.clip(to_np(gt[c]).transpose(1, 2, 0) / 255.0, 0, 1)
+        sign_flips += int((np.sign(imgs[c] - target) != np.sign(o_images[c] - target)).sum())
     np.testing.assert_allclose(stats.losses(W, H), o_losses, rtol=1e-5)
     g, og = to_np(grads), to_np(o_grads)
     for name, sl in GROUPS.items():
         err = rel_l2(g[:, sl], og[:, sl])
-        print(f"  grad {name}: rel_l2={err:.2e}")
-        assert err < 1e-4, (name, err)
+        print(f"  row grad {name} (end to end): rel_l2={err:.2e}; L1 sign flips {sign_flips}")
+        assert err < end_to_end_bound, (name, err)
 
 
 def test_cfg3_subset_vs_oracle(gpu):
@@ -98,7 +211,8 @@ def test_cfg3_subset_vs_oracle(gpu):
     params = sc.params[rows].contiguous()
     cams = [0, 9]
     gt = torch.rand((2, 3, sc.height, sc.width), generator=g) * 255.0
-    _parity(gpu, params, sc.viewmats[cams], sc.Ks[cams], gt, sc.width, sc.height, "cfg3 subset")
+    _parity(gpu, params, sc.viewmats[cams], sc.Ks[cams], gt, sc.width, sc.height, "cfg3 subset",
+            end_to_end_bound=1e-2)
 
 
 def test_cfg3_dense_window_vs_oracle(gpu):
@@ -112,7 +226,8 @@ def test_cfg3_dense_window_vs_oracle(gpu):
     K[:, 1, 2] -= y0
     g = torch.Generator().manual_seed(8)
     gt = torch.rand((2, 3, H, W), generator=g) * 255.0
-    _parity(gpu, sc.params, sc.viewmats[cams], K, gt, W, H, "cfg3 dense window")
+    _parity(gpu, sc.params, sc.viewmats[cams], K, gt, W, H, "cfg3 dense window",
+            end_to_end_bound=5e-2)
 
 
 def test_cfg3_full_step(gpu):

@@ -5,6 +5,8 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import raster_ref as R
+from oracle import ssim_ref as S
 from oracle import step_ref as SR
 from tidegs_amd import scenes
 
@@ -184,3 +186,46 @@ def test_packed_filter_ambiguity_covers_float32_rounding():
     frac = float(amb.double().mean())
     print(f"  float32 vs float64 filter differences: {n_diff}; ambiguous fraction {frac:.2e}")
     assert frac < 2e-3
+
+
+def test_isect_inputs_override_reproduces_default():
+    """batch_grads with the intersection step fed its own float32 (mean,
+    radius, depth) values -- what the GPU parity tests pass in, with the GPU's
+    values -- reproduces the default run exactly; render_projection gives
+    those values."""
+    sc, p = _tiny_scene()
+    base = SR.batch_grads(p, sc.viewmats, sc.Ks, sc.gt, sc.width, sc.height)
+    inputs = []
+    for c, rows in enumerate(base[4]):
+        radii, m2d, depths, rr = SR.render_projection(p, rows, sc.viewmats[c], sc.Ks[c],
+                                                      sc.width, sc.height)
+        assert torch.equal(radii, torch.where(radii > 0, torch.ceil(rr), 0).to(radii.dtype))
+        inputs.append((m2d.float().numpy(), radii.numpy(), depths.float().numpy()))
+    again = SR.batch_grads(p, sc.viewmats, sc.Ks, sc.gt, sc.width, sc.height,
+                           filters=base[4], isect_inputs=inputs)
+    assert torch.equal(base[0], again[0]) and torch.equal(base[1], again[1])
+    assert base[2] == again[2]
+
+
+def test_batch_row_grads_from_splat_grads_match_batch_grads():
+    """batch_row_grads (row gradients from given splat gradients, the oracle
+    half the GPU parity tests feed with the GPU's splat gradients) equals
+    batch_grads when given the oracle's own splat gradients."""
+    sc, p = _tiny_scene()
+    W, H = sc.width, sc.height
+    touched, grads, _, _, filters = SR.batch_grads(p, sc.viewmats, sc.Ks, sc.gt, W, H)
+    per_cam = []
+    for c, rows in enumerate(filters):
+        f = SR._render_entries(p, rows, sc.viewmats[c], sc.Ks[c], W, H, 3, torch.float64)
+        _, ids, flat = R.isect_tiles(f.m2d.float().numpy(), f.radii.numpy(),
+                                     f.depths.float().numpy(), 16, -(-W // 16), -(-H // 16))
+        offs = R.isect_offset_encode(ids, 1, -(-W // 16), -(-H // 16))
+        splat = (f.m2d.numpy().reshape(-1, 2), f.conics[0].numpy(), f.colors.numpy(),
+                 f.opac.numpy())
+        img, alphas, last = R.rasterize_fwd(*splat, W, H, 16, offs, flat)
+        _, v = S.tide_loss(img[0].transpose(2, 0, 1), sc.gt[c].numpy(), dtype=np.float64)
+        v = np.ascontiguousarray(v.transpose(1, 2, 0))[None]
+        per_cam.append(R.rasterize_bwd(*splat, W, H, 16, offs, flat, alphas, last, v)[:4])
+    t2, g2 = SR.batch_row_grads(p, sc.viewmats, sc.Ks, W, H, filters, per_cam)
+    assert torch.equal(touched, t2)
+    assert torch.allclose(grads, g2, rtol=1e-12, atol=1e-18)
