@@ -157,6 +157,17 @@ size_t tgs_radix_sort_workspace_size(uint64_t n);
 int tgs_radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
                          uint64_t n, int begin_bit, int end_bit, void* workspace,
                          size_t workspace_bytes, int* selector, tgs_stream_t stream);
+/* No counterpart in the reference: tgs_radix_sort_pairs without a workspace
+ * argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops that forbid hipMalloc).  Its temporary storage
+ * is a file-scope device array of 16.0 MiB per GPU, held until the process
+ * ends; n may be at most 2^25 (33,554,432) keys, larger n returns
+ * TGS_ERR_ARG with an error text.  Calls no allocator.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (concurrent streams
+ * or threads) race. */
+int tgs_radix_sort_pairs_noalloc(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt,
+                                 uint32_t* vals_alt, uint64_t n, int begin_bit, int end_bit,
+                                 int* selector, tgs_stream_t stream);
 /* Segmented stable sort of uint32 keys with 4- or 8-byte values (the
  * camera-grouped sorts of the fused step; a plain sort is one segment): each
  * segment [seg_offsets[s], seg_offsets[s+1]) is sorted on key bits

@@ -65,6 +65,10 @@ SIGNATURES = {
         ctypes.c_int,
         [P, P, P, P, U64, ctypes.c_int, ctypes.c_int, P, SZ, ctypes.POINTER(ctypes.c_int), P],
     ),
+    "tgs_radix_sort_pairs_noalloc": (
+        ctypes.c_int,
+        [P, P, P, P, U64, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int), P],
+    ),
     "tgs_segmented_sort_workspace_size": (SZ, [U64, U32]),
     "tgs_segmented_sort_pairs_u32": (
         ctypes.c_int,

@@ -15,6 +15,8 @@
 //   scan      exclusive scan of hist (digit-major => global digit offsets)
 //   scatter   per-tile stable ranking (ballot matching + per-wave counters),
 //             LDS reorder, coalesced write of each digit run.
+#include <mutex>
+
 #include "tgs_common.cuh"
 
 #define SCAN_THREADS 256
@@ -461,6 +463,95 @@ extern "C" int tgs_radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* ke
   sg.tile_base[1] = (uint32_t)sort_tiles(n);
   return radix_passes<uint64_t, uint32_t>(keys, vals, keys_alt, vals_alt, sg, begin_bit, end_bit,
                                           workspace, selector, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of tgs_radix_sort_pairs for callers that cannot
+// allocate device memory (code under HIP graph capture, serving loops that
+// forbid hipMalloc).  Its histograms, their scan and the scan's block sums
+// live in a file-scope device array sized for TGS_NOALLOC_SORT_MAX_KEYS keys
+// (16.0 MiB held by every GPU the library runs on until the process ends).
+// Every pass writes each histogram entry before any is read, so the array
+// needs no clearing between calls; calls that overlap on one GPU share it and
+// race.  Host code reaches the array only through the address that
+// hipGetSymbolAddress returns per device (the symbol's name is a host-side
+// stand-in, not a device address).
+// ---------------------------------------------------------------------------
+#define TGS_NOALLOC_SORT_MAX_KEYS (1ull << 25)
+#define TGS_NOALLOC_SORT_TILES ((TGS_NOALLOC_SORT_MAX_KEYS + SORT_TILE - 1) / SORT_TILE)
+#define TGS_ALIGN256(b) ((((uint64_t)(b)) + 255ull) & ~255ull)
+#define TGS_NOALLOC_SORT_HIST (TGS_NOALLOC_SORT_TILES * SORT_BINS)
+#define TGS_NOALLOC_SORT_BYTES                          \
+  (TGS_ALIGN256(TGS_NOALLOC_SORT_HIST * 4ull) * 2ull + \
+   TGS_ALIGN256((TGS_NOALLOC_SORT_HIST + SCAN_CHUNK - 1) / SCAN_CHUNK * 8ull + 8ull))
+#define TGS_MAX_DEVICES 64
+
+static __device__ __align__(256) uint8_t scratch[TGS_NOALLOC_SORT_BYTES];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[TGS_MAX_DEVICES] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+static int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    tgs_set_error("radix_sort_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  if (dev < 0 || dev >= TGS_MAX_DEVICES) {
+    tgs_set_error("radix_sort_noalloc: device %d out of range", dev);
+    return TGS_ERR_ARG;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      tgs_set_error("radix_sort_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return e != hipSuccess ? (int)e : TGS_ERR_ARG;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TGS_OK;
+}
+
+extern "C" int tgs_radix_sort_pairs_noalloc(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt,
+                                            uint32_t* vals_alt, uint64_t n, int begin_bit,
+                                            int end_bit, int* selector, hipStream_t stream) {
+  TGS_CHECK_ARG(selector != nullptr, "radix_sort_noalloc: null selector");
+  *selector = 0;
+  if (n > TGS_NOALLOC_SORT_MAX_KEYS) {
+    tgs_set_error("radix_sort_noalloc: %llu keys exceed the allocation-free maximum of %llu; "
+                  "use tgs_radix_sort_pairs with a workspace",
+                  (unsigned long long)n, (unsigned long long)TGS_NOALLOC_SORT_MAX_KEYS);
+    return TGS_ERR_ARG;
+  }
+  if (n <= 1 || end_bit <= begin_bit) return TGS_OK;
+  TGS_CHECK_ARG(keys && vals && keys_alt && vals_alt, "radix_sort_noalloc: null pointer");
+  TGS_CHECK_ARG(begin_bit >= 0 && end_bit <= 64, "radix_sort_noalloc: bit range out of [0,64]");
+  static_assert(TGS_NOALLOC_SORT_BYTES >=
+                    TGS_ALIGN256(TGS_NOALLOC_SORT_HIST * 4ull) * 2ull +
+                        TGS_ALIGN256((TGS_NOALLOC_SORT_HIST + SCAN_CHUNK - 1) / SCAN_CHUNK * 8ull +
+                                     8ull),
+                "scratch smaller than the sort workspace");
+  if (radix_workspace(sort_tiles(n)) > TGS_NOALLOC_SORT_BYTES) {
+    tgs_set_error("radix_sort_noalloc: workspace %zu exceeds the scratch array",
+                  radix_workspace(sort_tiles(n)));
+    return TGS_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  RadixSegs sg{};
+  sg.n = 1;
+  sg.key_off[0] = 0;
+  sg.key_off[1] = (uint32_t)n;
+  sg.tile_base[0] = 0;
+  sg.tile_base[1] = (uint32_t)sort_tiles(n);
+  return radix_passes<uint64_t, uint32_t>(keys, vals, keys_alt, vals_alt, sg, begin_bit, end_bit,
+                                          ws, selector, stream);
 }
 
 // Segmented stable sort of uint32 keys with 4- or 8-byte values: each segment
