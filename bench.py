@@ -26,12 +26,20 @@ if str(ROOT) not in sys.path:
 HBM_PEAK_GBS = 8000.0
 METRIC = "ms/train-step (fwd+bwd+Adam) at 4M Gaussians, 16×1080p; bwd HBM GB/s"
 
-# Algorithmic bytes per unit of work (fp32), see DESIGN.md "Measurement".
+# Algorithmic bytes per unit of work (fp32).  The compositing kernels use the
+# per-camera figures of the hot-path scope table: backward 24 B per pixel
+# (alpha, last id, dL/dcolour, dL/dalpha) + 40 B per intersection (flatten id
+# and staged record) + 72 B per visible entry (the 9-float gradient record
+# zero-filled and written); forward 20 B per pixel + 40 B per intersection +
+# 4 B per tile.  The projection/optimizer kernels count what their algorithm
+# moves (each touched row once; the scope table's 760 B per visible entry
+# assumes a read-modify-write of the compact row per camera, which this
+# design does not do).
 BYTES = {
     "visibility": lambda s: 40 * s["N"] + 4 * s["N"],
     "project_fwd": lambda s: s["T"] * (4 + 4 + 4 + 236) + s["V"] * (4 + 48 + 4 + 8),
-    "raster_fwd": lambda s: s["C"] * s["P"] * 20 + s["I"] * 52,
-    "raster_bwd": lambda s: s["C"] * s["P"] * 20 + s["I"] * 52 + s["V"] * 36,
+    "raster_fwd": lambda s: s["C"] * s["P"] * 20 + s["I"] * 40 + s["C"] * s["tiles"] * 4,
+    "raster_bwd": lambda s: s["C"] * s["P"] * 24 + s["I"] * 40 + s["V"] * 72,
     "project_bwd": lambda s: s["T"] * (4 + 4 + 4 + 236 + 236) + s["V"] * (4 + 36),
     "adam": lambda s: s["T"] * 1656,
     # fused: the row read once, p/m/v written, m/v read; no gradient rows
@@ -69,41 +77,119 @@ def profiled_valu(kernel: str):
     return None
 
 
-def cpu_baseline(width, height, frac_a=1 / 16, frac_b=1 / 8, seed=0):
-    """Time the CPU oracle on one camera of the same workload with a random
-    subset of the Gaussians at two subset sizes, fit t = t_pix + f * t_gauss,
-    and extrapolate to 16 cameras x 4M Gaussians (single thread)."""
+def _host_cpu():
+    """(threads to use, nproc, CPU model): the box's CPU share (OMP_NUM_THREADS
+    when set, else the affinity mask) and the lscpu model name."""
+    import subprocess
+
+    nproc = os.cpu_count() or 1
+    try:
+        share = len(os.sched_getaffinity(0))
+    except AttributeError:
+        share = nproc
+    threads = int(os.environ.get("OMP_NUM_THREADS") or share)
+    model = "unknown"
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                model = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return max(1, min(threads, share)), nproc, model
+
+
+def _median_time(fn, repeats=3):
+    """1 warm-up, then the median wall time of ``repeats`` runs (seconds)."""
+    fn()
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def cpu_baseline(width, height, gpu_stats, seed=0):
+    """The CPU oracle (oracle/step_ref.py + oracle/optim_ref.py) timed on the
+    host cores: all threads of the box's CPU share, 1
+    warm-up and the median of 3 repeats per sample.
+
+    * cfg1 (10k Gaussians, one 256x256 camera, L1, Adam) runs in full.
+    * cfg3: one camera at a time on seeded subsets of the 4M rows (4 samples
+      over different cameras and subset sizes); a least-squares fit of the
+      time in the sample's measured visible entries V and intersections I,
+      t = c0 + cV V + cI I, is extrapolated to the GPU step's measured V and I
+      of each of its 16 cameras, plus the Adam update of its touched rows
+      (timed on a row sample, linear in the rows)."""
     import numpy as np
     import torch
+    from scipy.optimize import nnls
 
+    from oracle import optim_ref as O
+    from oracle import raster_ref as R
     from oracle import step_ref as SR
     from tidegs_amd import scenes
 
-    torch.set_num_threads(1)
-    times = []
-    sizes = []
-    for frac in (frac_a, frac_b):
-        n = int(4_000_000 * frac)
-        sc = scenes.cfg3(seed=seed, n=n, n_cams=16, width=width, height=height)
-        vm, K, gt = sc.viewmats[:1], sc.Ks[:1], sc.gt[:1]
-        t0 = time.perf_counter()
-        SR.batch_grads(sc.params, vm, K, gt, width, height, raster_dtype=np.float32,
-                       proj_dtype=torch.float32)
-        times.append(time.perf_counter() - t0)
-        sizes.append(frac)
-    slope = (times[1] - times[0]) / (sizes[1] - sizes[0])
-    t_pix = max(0.0, times[0] - slope * sizes[0])
-    per_cam_full = t_pix + slope * 1.0
-    ms_step = per_cam_full * 16 * 1000.0
+    threads, nproc, model = _host_cpu()
+    torch.set_num_threads(threads)
+    f32 = dict(raster_dtype=np.float32, proj_dtype=torch.float32)
+    # cfg1 in full: forward + backward + one Adam step at lr 1e-3
+    c1 = scenes.cfg1(seed=seed)
+
+    def cfg1_step():
+        touched, grads, *_ = SR.batch_grads(c1.params, c1.viewmats, c1.Ks, c1.gt, c1.width,
+                                            c1.height, lambda_dssim=0.0, **f32)
+        p = c1.params[touched].double().numpy()
+        O.adam_rows(p, grads.numpy(), 0.0, 0.0, 1e-3, 0.9, 0.999, 1e-15, 1.0, 0.1,
+                    np.sqrt(0.001))
+
+    cfg1_s = _median_time(cfg1_step)
+    # cfg3 samples
+    sc = scenes.cfg3(seed=seed, with_gt=False)
+    g = torch.Generator().manual_seed(seed + 1)
+    gt = torch.rand((3, height, width), generator=g) * 255.0
+    rows_all = []
+    samples = []
+    for n_sub, cam in ((31_250, 0), (62_500, 5), (125_000, 10), (62_500, 15)):
+        rows = torch.sort(torch.randperm(sc.n, generator=g)[:n_sub]).values
+        params = sc.params[rows].contiguous()
+        vm, K = sc.viewmats[cam:cam + 1], sc.Ks[cam:cam + 1]
+        t = _median_time(lambda: SR.batch_grads(params, vm, K, gt[None], width, height, **f32))
+        filt = SR.packed_filters(params, vm, K, width, height)[0]
+        radii, m2d, depths, _ = SR.render_projection(params, filt, vm[0], K[0], width, height)
+        tw, th = -(-width // 16), -(-height // 16)
+        n_isect = R.isect_tiles(m2d.float().numpy()[None], radii.numpy()[None],
+                                depths.float().numpy()[None], 16, tw, th)[1].size
+        samples.append((t, filt.numel(), n_isect))
+        rows_all.append(f"{n_sub} rows cam {cam}: V={filt.numel()} I={n_isect} {t:.2f}s")
+    A = np.array([[1.0, v, i] for _, v, i in samples])
+    coef, _ = nnls(A, np.array([s[0] for s in samples]))
+    cams = [coef[0] + coef[1] * v + coef[2] * i
+            for v, i in zip(gpu_stats.visible_per_camera, gpu_stats.isects_per_camera)]
+    # Adam over the touched rows: float64 numpy on a 250k-row sample
+    n_adam = 250_000
+    p = np.random.default_rng(seed).standard_normal((n_adam, 59))
+    gr = p * 1e-3
+    adam_s = _median_time(lambda: O.adam_rows(p, gr, p * 0, p * 0, 1e-3, 0.9, 0.999, 1e-15, 16.0,
+                                              0.1, np.sqrt(0.001)))
+    adam_full = adam_s * gpu_stats.touched_rows / n_adam
+    ms_step = (sum(cams) + adam_full) * 1000.0
     return {
         "value": round(ms_step, 1),
         "unit": "ms/train-step (extrapolated)",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"CPU oracle (oracle/step_ref.py, 1 thread) on 1 camera of the cfg3 workload "
-                   f"with {int(4e6 * frac_a)} and {int(4e6 * frac_b)} random Gaussians: "
-                   f"{times[0]:.1f}s and {times[1]:.1f}s; linear fit in the Gaussian count, "
-                   f"x16 cameras"),
+        "nproc": nproc,
+        "cpu_model": model,
+        "sample": ("CPU oracle (oracle/step_ref.py, float32 projection and compositing; "
+                   f"torch threads {threads}), 1 warm-up + median of 3 per sample, one camera "
+                   f"per sample on seeded subsets of the cfg3 rows: {'; '.join(rows_all)}. "
+                   f"Fit t = {coef[0]:.3g} s + {coef[1]:.3g} s*V + {coef[2]:.3g} s*I, summed over "
+                   f"the 16 cameras' measured V and I ({sum(cams):.1f} s) + Adam over "
+                   f"{gpu_stats.touched_rows} touched rows ({adam_full:.1f} s, from "
+                   f"{n_adam} rows in {adam_s:.2f} s)"),
+        "cfg1_full_ms": round(cfg1_s * 1000.0, 1),
     }
 
 
@@ -121,7 +207,7 @@ WORKLOADS = {
 def _stage_kernels(ts, stats, args, stage_ms, C, P):
     Vvis = int(ts.last_visible_entries)
     shape = {"N": ts.params.shape[0], "C": C, "P": P, "V": stats.entries, "Vvis": Vvis,
-             "I": stats.n_isects, "T": stats.touched_rows}
+             "I": stats.n_isects, "T": stats.touched_rows, "tiles": ts.tw * ts.th}
     kernels = {}
     for name, f in BYTES.items():
         if name in stage_ms and stage_ms[name] > 0:
@@ -246,7 +332,7 @@ def bench_step(args, dev):
         "cpu_baseline": None,
     }
     if args.workload == "cfg3" and not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.width, args.height)
+        line["cpu_baseline"] = cpu_baseline(args.width, args.height, stats)
     return line
 
 

@@ -309,8 +309,11 @@ int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* masks, const u
  * depth_keys [V] (float bits of the depth; 0xffffffff when culled) and
  * entry_rects [V] (tile rectangle x0|x1<<8|y0<<16|y1<<24 in the high word,
  * entry index in the low word; isect_tiles.cu:55-70).  Tile grid at most
- * 255 x 255. */
-int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched, const int32_t* visit_base,
+ * 255 x 255.  n_touched_dev (device, may be null) holds the touched-row
+ * count when the host does not know it yet; n_touched is then the launch's
+ * capacity (rows beyond the device count do nothing). */
+int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touched_dev,
+                         const int32_t* touched, const int32_t* visit_base,
                          const int32_t* visits, const uint32_t* masks, uint32_t C,
                          const float* params, uint32_t row_stride, const float* viewmats,
                          const float* Ks,
@@ -335,6 +338,14 @@ int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched, const int32
  *   tgs_tide_isect_ids       the reference's int64 ids (inspection only). */
 int tgs_tide_isect_count(uint32_t n_entries, const uint64_t* entry_rects, int32_t* tiles,
                          tgs_stream_t stream);
+/* Per-camera intersection counts isect_totals [C] (int64) as the sums of the
+ * entries' tile-rectangle areas (the counts isect_tiles.cu:55-70 produces),
+ * straight from tgs_tide_project_fwd's entry_rects, so the host can size the
+ * intersection buffers while the depth sort runs.  n_entries_dev (device, may
+ * be null) holds the entry count; n_entries is then the launch's capacity. */
+int tgs_tide_isect_totals(uint32_t n_entries, const uint32_t* n_entries_dev,
+                          const uint64_t* entry_rects, const int32_t* cam_offsets, uint32_t C,
+                          int64_t* isect_totals, tgs_stream_t stream);
 int tgs_tide_isect_segments(uint32_t C, const int32_t* cam_offsets, const int64_t* cum_tiles,
                             int64_t* seg, tgs_stream_t stream);
 int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,

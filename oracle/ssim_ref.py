@@ -30,8 +30,15 @@ def gaussian_window(size: int = 11, sigma: float = 1.5, dtype=np.float64) -> np.
 
 
 def _sep_conv(img: np.ndarray, w: np.ndarray) -> np.ndarray:
-    """Zero-padded 'same' separable filter over the last two axes, x then y,
-    accumulating taps in order 0..10."""
+    """Zero-padded 'same' separable filter over the last two axes, x then y.
+    In float32 the taps accumulate in order 0..10 in float32 (the kernel's
+    arithmetic); in float64 the filter is scipy's correlate1d (double
+    accumulation)."""
+    if img.dtype == np.float64:
+        from scipy.ndimage import correlate1d
+
+        hx = correlate1d(img, w, axis=-1, mode="constant", cval=0.0)
+        return correlate1d(hx, w, axis=-2, mode="constant", cval=0.0)
     r = len(w) // 2
     H, W = img.shape[-2:]
     pad = np.zeros(img.shape[:-2] + (H + 2 * r, W + 2 * r), dtype=img.dtype)

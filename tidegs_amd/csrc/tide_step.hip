@@ -332,7 +332,8 @@ __device__ __forceinline__ void project_entry(
 // into every camera it is visible in (its visits, in camera order, are the
 // set bits of its visibility mask); SH coefficients stay in registers.
 __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
-    uint32_t n_touched, const int32_t* __restrict__ touched,
+    uint32_t n_touched, const uint32_t* __restrict__ n_touched_dev,
+    const int32_t* __restrict__ touched,
     const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
     const uint32_t* __restrict__ masks, TideCams tc, const float* __restrict__ params,
     uint32_t row_stride, int W, int H, float eps2d, float near_plane, float far_plane,
@@ -343,7 +344,7 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
   load_cams_lds(tc, s_cam);
   __syncthreads();
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_touched) return;
+  if (t >= (n_touched_dev ? min(*n_touched_dev, n_touched) : n_touched)) return;
   const uint32_t n = (uint32_t)touched[t];
   const float* row = params + (uint64_t)n * row_stride;
   const float p[3] = {row[0], row[1], row[2]};
@@ -383,6 +384,56 @@ __global__ void __launch_bounds__(256) tide_isect_count_kernel(
   const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= n_entries) return;
   tiles[j] = (int32_t)rect_tiles((uint32_t)(rects[j] >> 32));
+}
+
+// Per-camera intersection counts from the (unsorted) tile rectangles: the
+// sum of the rectangles' areas over each camera's entries.  Each workgroup
+// sums ISECT_TOTAL_PER_BLOCK consecutive entries into LDS counters and adds
+// them to the camera totals with one 64-bit atomic per camera it met.
+#define ISECT_TOTAL_ITEMS 32
+#define ISECT_TOTAL_PER_BLOCK (256 * ISECT_TOTAL_ITEMS)
+
+__global__ void tide_zero_i64_kernel(int64_t* __restrict__ p, uint32_t n) {
+  if (threadIdx.x < n) p[threadIdx.x] = 0;
+}
+
+__global__ void __launch_bounds__(256) tide_isect_totals_kernel(
+    uint32_t n_cap, const uint32_t* __restrict__ n_dev, const uint64_t* __restrict__ rects,
+    const int32_t* __restrict__ cam_offsets, uint32_t C, int64_t* __restrict__ totals) {
+  __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
+  __shared__ uint32_t s_sum[TIDE_MAX_CAMS];
+  if (threadIdx.x <= C) s_off[threadIdx.x] = cam_offsets[threadIdx.x];
+  if (threadIdx.x < TIDE_MAX_CAMS) s_sum[threadIdx.x] = 0u;
+  __syncthreads();
+  const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
+  const uint32_t base = blockIdx.x * ISECT_TOTAL_PER_BLOCK;
+  if (base >= n) return;
+  // entries are grouped by camera: a thread's entries ascend, so its camera
+  // only moves forward; the running sum goes to LDS when it does
+  // all of the thread's rectangles (high words) are loaded before any is used
+  const uint32_t* hi = reinterpret_cast<const uint32_t*>(rects) + 1;
+  uint32_t rc[ISECT_TOTAL_ITEMS];
+#pragma unroll
+  for (int k = 0; k < ISECT_TOTAL_ITEMS; ++k) {
+    const uint32_t e = base + (uint32_t)k * 256u + threadIdx.x;
+    rc[k] = e < n ? hi[2ull * e] : 0u;
+  }
+  uint32_t e = base + threadIdx.x;
+  uint32_t c = entry_camera(s_off, C, min(e, n - 1));
+  uint32_t acc = 0u;
+#pragma unroll
+  for (int k = 0; k < ISECT_TOTAL_ITEMS; ++k, e += 256u) {
+    while (c + 1 < C && e >= (uint32_t)s_off[c + 1]) {
+      if (acc) atomicAdd(&s_sum[c], acc);
+      acc = 0u;
+      ++c;
+    }
+    acc += rect_tiles(rc[k]);
+  }
+  if (acc) atomicAdd(&s_sum[c], acc);
+  __syncthreads();
+  if (threadIdx.x < C && s_sum[threadIdx.x])
+    atomicAdd((unsigned long long*)&totals[threadIdx.x], (unsigned long long)s_sum[threadIdx.x]);
 }
 
 __global__ void tide_isect_segments_kernel(uint32_t C, const int32_t* __restrict__ cam_offsets,
@@ -797,7 +848,8 @@ extern "C" int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* mas
   TGS_RETURN_LAUNCH("tgs_tide_compact");
 }
 
-extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched,
+extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touched_dev,
+                                    const int32_t* touched,
                                     const int32_t* visit_base, const int32_t* visits,
                                     const uint32_t* masks, uint32_t C, const float* params,
                                     uint32_t row_stride, const float* viewmats, const float* Ks,
@@ -821,7 +873,8 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const int32_t* touched,
   TGS_CHECK_ARG(row_stride >= TIDE_ROW, "tide step: row_stride must be >= %d", TIDE_ROW);
   TideCams tc{viewmats, Ks, campos, C};
   hipLaunchKernelGGL(tide_project_fwd_kernel, dim3(tgs_blocks(n_touched, 256)), dim3(256), 0,
-                     stream, n_touched, touched, visit_base, visits, masks, tc, params, row_stride,
+                     stream, n_touched, n_touched_dev, touched, visit_base, visits, masks, tc,
+                     params, row_stride,
                      W, H,
                      eps2d, near_plane, far_plane, radius_clip, sh_degree, tile_size, tile_width,
                      tile_height, (float4*)splats, depth_keys, entry_rects);
@@ -836,6 +889,21 @@ extern "C" int tgs_tide_isect_count(uint32_t n_entries, const uint64_t* entry_re
   hipLaunchKernelGGL(tide_isect_count_kernel, dim3(tgs_blocks(n_entries, 256)), dim3(256), 0,
                      stream, n_entries, entry_rects, tiles);
   TGS_RETURN_LAUNCH("tgs_tide_isect_count");
+}
+
+extern "C" int tgs_tide_isect_totals(uint32_t n_entries, const uint32_t* n_entries_dev,
+                                     const uint64_t* entry_rects, const int32_t* cam_offsets,
+                                     uint32_t C, int64_t* isect_totals, hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  TGS_CHECK_ARG(isect_totals && cam_offsets, "tide_isect_totals: null");
+  hipLaunchKernelGGL(tide_zero_i64_kernel, dim3(1), dim3(64), 0, stream, isect_totals, C);
+  if (n_entries == 0) TGS_RETURN_LAUNCH("tgs_tide_isect_totals");
+  TGS_CHECK_ARG(entry_rects != nullptr, "tide_isect_totals: null rects");
+  const uint64_t blocks = ((uint64_t)n_entries + ISECT_TOTAL_PER_BLOCK - 1) / ISECT_TOTAL_PER_BLOCK;
+  hipLaunchKernelGGL(tide_isect_totals_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     n_entries, n_entries_dev, entry_rects, cam_offsets, C, isect_totals);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_totals");
 }
 
 extern "C" int tgs_tide_isect_segments(uint32_t C, const int32_t* cam_offsets,

@@ -14,10 +14,14 @@ whole batch: parameters do not change between the cameras of a batch, so the
 gradients are the same, and each touched row accumulates its cameras in the
 reference's camera order.
 
-Host synchronisations per step: the visibility totals and the intersection
-count; the optimizer's per-block touch counts are launched after the first and
-read after the second (the reference syncs for all three,
-``isect_tiles.cu:166``, ``base_engine.py:407``, ``gpu_resident_optimizer.py:296``).
+The host reads three small results per step (the reference syncs for all
+three, ``isect_tiles.cu:166``, ``base_engine.py:407``,
+``gpu_resident_optimizer.py:296``), each while the GPU has queued work behind
+it, so the GPU never waits for the host: the visibility totals while the
+projection runs (its launch covers every row and reads the touched-row count
+on the device), the per-camera intersection counts (sums of the tile
+rectangles' areas, known right after the projection) while the depth sort
+runs, and the optimizer's per-block touch counts while the rasterizers run.
 By default the optimizer update runs inside the projection-backward launch
 (``tgs_tide_project_bwd_update``), so the compact gradient rows never reach
 memory; ``fuse_update=False`` keeps the two-launch form (gradient rows, then
@@ -83,6 +87,7 @@ class StepStats:
     n_isects: int
     loss_sums: torch.Tensor = field(repr=False)  # [C, 2] double on device
     optimizer: dict = field(default_factory=dict)
+    isects_per_camera: list = field(default_factory=list)
 
     def losses(self, width: int, height: int, lambda_dssim: float = 0.2):
         s = self.loss_sums.double().cpu()
@@ -212,6 +217,20 @@ class TideStep:
             self._bufs[name] = b
         return b[:numel]
 
+    def _pinned(self, name: str, numel: int, dtype) -> torch.Tensor:
+        """Pinned host buffer for an asynchronous device-to-host copy."""
+        key = "host_" + name
+        b = self._bufs.get(key)
+        if b is None or b.numel() < numel or b.dtype != dtype:
+            b = torch.empty(numel, dtype=dtype, pin_memory=True)
+            self._bufs[key] = b
+        return b[:numel]
+
+    def _record(self) -> torch.cuda.Event:
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        return ev
+
     # ---- stages -----------------------------------------------------------
     def forward_backward(self, viewmats: torch.Tensor, Ks: torch.Tensor, gt: torch.Tensor):
         """Everything up to the compact gradients; returns (touched, grads, stats)."""
@@ -259,38 +278,53 @@ class TideStep:
                N.ptr(touched), N.ptr(visit_base), N.ptr(visits), N.ptr(totals),
                N.ptr(cam_offsets), s)
         self._end()
-        tot = totals.cpu().tolist()  # sync 1
-        V = tot[C + 1]
-        T = tot[C]
+        # the totals (V per camera, T, V) go to the host while the projection
+        # runs: its launch covers every row and reads T on the device
+        tot_host = self._pinned("totals", C + 3, torch.int32)
+        tot_host.copy_(totals, non_blocking=True)
+        totals_ready = self._record()
 
         # 2. projection + SH colours for every (camera, visible row), one pass over
-        #    the touched rows; depth keys and tile rectangles for the sort
+        #    the touched rows; depth keys and tile rectangles for the sort.
+        #    Entry buffers hold the C * N entries a batch can have at most.
         n_buckets = C * th * tw
-        splats = self._buf("splats", max(V, 1) * 12, torch.float32)
-        dkeys = self._buf("depth_keys", max(V, 1), torch.int32)
-        rects = self._buf("entry_rects", max(V, 1), torch.int64)
+        cap_v = C * n
+        splats = self._buf("splats", cap_v * 12, torch.float32)
+        dkeys = self._buf("depth_keys", cap_v, torch.int32)
+        rects = self._buf("entry_rects", cap_v, torch.int64)
         self._begin("project_fwd")
-        N.call("tgs_tide_project_fwd", T, N.ptr(touched), N.ptr(visit_base), N.ptr(visits),
-               N.ptr(masks), C, N.ptr(P), self.row_stride, N.ptr(viewmats), N.ptr(Ks),
-               N.ptr(campos), W, H,
-               self.eps2d, self.near, self.far, 0.0, self.sh_degree, self.TILE, tw, th,
-               N.ptr(splats), N.ptr(dkeys), N.ptr(rects), s)
+        N.call("tgs_tide_project_fwd", n, N.ptr(totals) + 4 * C, N.ptr(touched),
+               N.ptr(visit_base), N.ptr(visits), N.ptr(masks), C, N.ptr(P), self.row_stride,
+               N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H, self.eps2d, self.near, self.far,
+               0.0, self.sh_degree, self.TILE, tw, th, N.ptr(splats), N.ptr(dkeys), N.ptr(rects),
+               s)
         self._end()
+        # per-camera intersection counts (sums of the rectangles' areas) go to
+        # the host while the depth sort runs
+        isect_tot = self._buf("isect_totals", C, torch.int64)
+        N.call("tgs_tide_isect_totals", cap_v, N.ptr(totals) + 4 * (C + 1), N.ptr(rects),
+               N.ptr(cam_offsets), C, N.ptr(isect_tot), s)
+        isect_host = self._pinned("isect_totals", C, torch.int64)
+        isect_host.copy_(isect_tot, non_blocking=True)
+        isects_ready = self._record()
+
+        totals_ready.synchronize()  # host read 1: the projection keeps the GPU busy
+        tot = tot_host.tolist()
+        V = tot[C + 1]
+        T = tot[C]
         if update and T:
-            # per-block touch counts for the optimizer's slot bookkeeping, on
-            # the host by sync 2 (launched after the projection, which needs
-            # the GPU first after sync 1)
+            # per-block touch counts for the optimizer's slot bookkeeping
             counts_host = self.optimizer.launch_touch_counts(self.gaussians, touched[:T])
+            counts_ready = self._record()
 
         # 3. intersections in the reference's (camera, tile, depth, entry) order:
         #    depth sort of the entries per camera, count + scan, emission in depth
         #    order, stable sort of the tile bits per camera, bucket offsets
         cam_segs = _segments([sum(tot[:c]) for c in range(C + 1)])
-        dkeys2 = self._buf("depth_keys2", max(V, 1), torch.int32)
-        rects2 = self._buf("entry_rects2", max(V, 1), torch.int64)
-        tiles = self._buf("tiles", max(V, 1), torch.int32)
-        cum = self._buf("cum_tiles", max(V, 1), torch.int64)
-        seg = self._buf("isect_segs", C + 1, torch.int64)
+        dkeys2 = self._buf("depth_keys2", cap_v, torch.int32)
+        rects2 = self._buf("entry_rects2", cap_v, torch.int64)
+        tiles = self._buf("tiles", cap_v, torch.int32)
+        cum = self._buf("cum_tiles", cap_v, torch.int64)
         ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(max(V, 1)), torch.uint8)
         self._begin("isect_scan")
         if V:
@@ -304,11 +338,12 @@ class TideStep:
             N.call("tgs_tide_isect_count", V, N.ptr(rects), N.ptr(tiles), s)
             N.call("tgs_inclusive_scan_i32_i64", N.ptr(tiles), N.ptr(cum), V, N.ptr(ws),
                    ws.numel(), s)
-            N.call("tgs_tide_isect_segments", C, N.ptr(cam_offsets), N.ptr(cum), N.ptr(seg), s)
-        else:
-            seg.zero_()
         self._end()
-        isect_segs = seg.cpu().tolist()  # sync 2
+        isects_ready.synchronize()  # host read 2: the depth sort keeps the GPU busy
+        per_cam = isect_host.tolist()
+        isect_segs = [0]
+        for k in per_cam:
+            isect_segs.append(isect_segs[-1] + int(k))
         n_isects = isect_segs[C]
         check_isect_count(n_isects)
         tile_bits = (tw * th).bit_length()
@@ -372,6 +407,7 @@ class TideStep:
         if update:
             if T:
                 self._iteration += 1
+                counts_ready.synchronize()
                 opt_args, opt_stats = self.optimizer.fused_update_args(
                     self._iteration, self.gaussians, T, counts_host)
                 self._begin("project_bwd_update")
@@ -400,7 +436,8 @@ class TideStep:
                          last_ids=last_ids.view(C, H, W), v_images=v_images.view(C, H, W, 3),
                          splat_grads=sgrads[: V * 9].view(-1, 9), grads=grads, campos=campos)
         stats = StepStats(n_cameras=C, visible_per_camera=tot[:C], touched_rows=T, entries=V,
-                          n_isects=n_isects, loss_sums=sums.view(C, 2), optimizer=opt_stats)
+                          n_isects=n_isects, loss_sums=sums.view(C, 2), optimizer=opt_stats,
+                          isects_per_camera=[isect_segs[c + 1] - isect_segs[c] for c in range(C)])
         return touched[:T], grads, stats
 
     def optimizer_step(self, touched: torch.Tensor, grads: torch.Tensor) -> dict:
