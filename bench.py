@@ -195,6 +195,8 @@ def cpu_baseline(width, height, gpu_stats, seed=0):
 
 WORKLOADS = {
     "cfg3": "cfg3: 4M Gaussians, 16 cams x 1920x1080, L1+SSIM, fwd+bwd+Adam",
+    "cfg3-dropin": "cfg3 through the drop-in gsplat/clm ops and GPUResidentAdam at TideGS's "
+                   "per-camera call sites (engine.py:2255-2469, runtime.py:1762)",
     "cfg2": "cfg2: 1M Gaussians, 1 cam 1920x1080, rasterizer fwd+bwd",
     "cfg4": "cfg4: 16M-Gaussian aerial city, 4 oblique cams x 1920x1080, fwd+bwd+Adam",
     "cfg5": "cfg5: resident [32M,59] optimizer step, 30% rows visible",
@@ -334,6 +336,134 @@ def bench_step(args, dev):
     if args.workload == "cfg3" and not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.width, args.height, stats)
     return line
+
+
+def bench_dropin(args, dev):
+    """cfg3 through the drop-in ops at TideGS's own call sites, camera by
+    camera, as the reference's batch loop runs them
+    (``strategies/base_engine.py:329-425`` filters,
+    ``strategies/tide_engine/engine.py:2255-2469`` per camera,
+    ``runtime.py:1762`` optimizer): the packed projection of all cameras for the
+    filters and the touched rows, then per camera the gather + clone of the
+    filter's rows, activations, ``fully_fused_projection``,
+    ``spherical_harmonics``, ``isect_tiles``, ``isect_offset_encode``,
+    ``rasterize_to_pixels``, L1 + ``fused_ssim`` loss, autograd backward and
+    ``scatter_add_`` into the compact gradients, and finally
+    ``GPUResidentAdam.step`` over the touched rows."""
+    import math
+    import types
+
+    import torch
+
+    from tidegs_amd import gsplat_ops as ops
+    from tidegs_amd import scenes
+    from tidegs_amd.clm_ops import fused_ssim
+    from tidegs_amd.resident_optim import GPUResidentAdam
+    from tidegs_amd.tide_step import _Manager
+
+    sc = scenes.cfg3(seed=0, n=args.n, n_cams=args.cams, width=args.width, height=args.height,
+                     with_gt=True).to(dev)
+    C, W, H = sc.n_cams, sc.width, sc.height
+    n = sc.params.shape[0]
+    # TideGS's GPU-resident component tensors
+    comp = {"xyz": (0, 3), "scaling": (3, 6), "rotation": (6, 10), "opacity": (10, 11),
+            "features_dc": (11, 14), "features_rest": (14, 59)}
+    g = types.SimpleNamespace()
+    for name, (a, b) in comp.items():
+        setattr(g, "_" + name, sc.params[:, a:b].contiguous())
+    del sc.params
+    bsz = C
+    lrs = torch.tensor([1.6e-4, 0.05, 5e-3, 1e-3, 2.5e-3, 2.5e-3 / 20.0]) * math.sqrt(bsz)
+    g.optimizer = types.SimpleNamespace(
+        columns_lr=lrs, param_groups=[{"betas": (0.9 ** bsz, 0.999 ** bsz),
+                                       "eps": 1e-15 / math.sqrt(bsz)}])
+    g.gpu_working_set_manager = _Manager(n, 4096, dev)
+    opt = GPUResidentAdam(batch_size=bsz, block_size=4096,
+                          capacity_blocks=len(g.gpu_working_set_manager.loaded_blocks),
+                          device=str(dev))
+    opt.set_resident_blocks(g.gpu_working_set_manager.loaded_blocks)
+    vms, Ks = sc.viewmats.contiguous(), sc.Ks.contiguous()
+    camtoworlds = torch.linalg.inv(vms)
+    gts = [torch.clamp(sc.gt[c] / 255.0, 0.0, 1.0) for c in range(C)]
+    tw, th = -(-W // 16), -(-H // 16)
+    state = {"it": 0, "visible": 0, "isects": 0}
+
+    def step():
+        with torch.no_grad():
+            quats = torch.nn.functional.normalize(g._rotation, dim=-1)
+            out = ops.fully_fused_projection(g._xyz, None, quats, torch.exp(g._scaling), vms, Ks,
+                                             W, H, packed=True)
+            cam_ids, gauss_ids = out[0], out[1]
+            counts = torch.bincount(cam_ids, minlength=C).tolist()
+            filters = torch.split(gauss_ids, counts)
+            touched = torch.unique(gauss_ids)
+        grads = {name: torch.zeros((touched.numel(), b - a), device=dev)
+                 for name, (a, b) in comp.items()}
+        n_isect = 0
+        for c in range(C):
+            rows = filters[c]
+            xyz = g._xyz[rows].clone().requires_grad_(True)
+            op_raw = g._opacity[rows].clone().requires_grad_(True)
+            sc_raw = g._scaling[rows].clone().requires_grad_(True)
+            rot_raw = g._rotation[rows].clone().requires_grad_(True)
+            shs = torch.cat([g._features_dc[rows], g._features_rest[rows]], 1)
+            shs = shs.reshape(-1, 16, 3).requires_grad_(True)
+            opac = torch.sigmoid(op_raw)
+            scales = torch.exp(sc_raw)
+            rots = torch.nn.functional.normalize(rot_raw, dim=-1)
+            radii, m2d, depths, conics, _ = ops.fully_fused_projection(
+                xyz, None, rots, scales, vms[c:c + 1], Ks[c:c + 1], W, H, packed=False)
+            m2d.retain_grad()
+            dirs = xyz[None] - camtoworlds[c:c + 1, None, :3, 3]
+            colors = torch.clamp_min(ops.spherical_harmonics(3, dirs, shs[None]) + 0.5, 0.0)
+            _, isect_ids, flat = ops.isect_tiles(m2d, radii, depths, 16, tw, th)
+            offs = ops.isect_offset_encode(isect_ids, 1, tw, th)
+            img, _ = ops.rasterize_to_pixels(m2d, conics, colors, opac.squeeze(1)[None], W, H,
+                                             16, offs, flat)
+            img = img[0].permute(2, 0, 1).contiguous()
+            loss = 0.8 * (img - gts[c]).abs().mean() + \
+                0.2 * (1.0 - fused_ssim(img[None], gts[c][None]))
+            loss.backward()
+            idx = torch.searchsorted(touched, rows)
+            for name, t in (("xyz", xyz), ("opacity", op_raw), ("scaling", sc_raw),
+                            ("rotation", rot_raw)):
+                grads[name].index_add_(0, idx, t.grad)
+            sg = shs.grad.reshape(-1, 48)
+            grads["features_dc"].index_add_(0, idx, sg[:, :3])
+            grads["features_rest"].index_add_(0, idx, sg[:, 3:])
+            n_isect += isect_ids.numel()
+        state["it"] += 1
+        opt.step(state["it"], g, touched, grads)
+        state["visible"], state["isects"], state["touched"] = sum(counts), n_isect, touched.numel()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    return {
+        "metric": "ms/train-step (fwd+bwd+Adam) at 4M Gaussians, 16×1080p, drop-in ops at "
+                  "TideGS's per-camera call sites",
+        "value": round(ms, 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded cfg3 scene, random-init Gaussians, random targets)",
+        "config": {"workload": WORKLOADS["cfg3-dropin"], "gaussians": n, "cameras": C,
+                   "width": W, "height": H, "visible_entries": state["visible"],
+                   "touched_rows": state["touched"], "isects": state["isects"]},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
 
 
 def bench_optimizer(args, dev):
@@ -743,6 +873,8 @@ def main():
         line = bench_resident(args, dev)
     elif args.workload == "init":
         line = bench_init(args, dev)
+    elif args.workload == "cfg3-dropin":
+        line = bench_dropin(args, dev)
     else:
         line = bench_step(args, dev)
     print(json.dumps(line), flush=True)

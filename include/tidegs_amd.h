@@ -359,7 +359,8 @@ int tgs_tide_isect_ids(uint32_t n_isects, const uint32_t* keys, const int32_t* f
                        const float* splats, int64_t* isect_ids, tgs_stream_t stream);
 /* Rasterize forward/backward over packed splats (tile 16, 3 channels);
  * images / v_images [C,H,W,3], alphas [C,H,W], last_ids [C,H,W];
- * splat_grads [V,9] accumulated (zero first): {mean2d 2, conic 3, color 3, opacity}.
+ * splat_grads [V,9] accumulated (zero first): {mean2d 2, conic 3, color 3, opacity};
+ * v_alphas [C,H,W] (dL/dalpha, nullable: zero).
  * The forward also zeroes clear[0..clear_words) (nullable; 16-byte aligned,
  * clear_words a multiple of 4), normally the backward's splat_grads: the
  * stores overlap the compositing instead of taking a pass of their own. */
@@ -372,7 +373,18 @@ int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const float* backgro
                            uint32_t H, uint32_t tile_width, uint32_t tile_height,
                            const int32_t* tile_offsets, const int32_t* flatten_ids,
                            uint32_t n_isects, const float* alphas, const int32_t* last_ids,
-                           const float* v_images, float* splat_grads, tgs_stream_t stream);
+                           const float* v_images, const float* v_alphas, float* splat_grads,
+                           tgs_stream_t stream);
+/* The drop-in rasterizer's 3-channel path (rasterize_to_pixels_fwd.cu:162-284,
+ * rasterize_to_pixels_bwd.cu:251-402 with 3 channels): gsplat's SoA tensors
+ * means2d [n,2], conics [n,3], colors [n,3], opacities [n] packed into the
+ * splat records above (16-byte aligned [n,12]; radius and depth slots 0), and
+ * the [n,9] gradient records unpacked into the SoA gradient tensors. */
+int tgs_pack_splats(uint64_t n, const float* means2d, const float* conics, const float* colors,
+                    const float* opacities, float* splats, tgs_stream_t stream);
+int tgs_unpack_splat_grads(uint64_t n, const float* splat_grads, float* v_means2d,
+                           float* v_conics, float* v_colors, float* v_opacities,
+                           tgs_stream_t stream);
 /* Per touched row: projection + SH + activation backward over its visits in
  * camera order (the set bits of masks[row]); the render projection (near, far,
  * radius_clip as in tgs_tide_project_fwd) is recomputed per visit.  Writes the

@@ -195,7 +195,7 @@ def test_cfg4_city_hot_tiles(gpu):
     d_v = v.to(gpu)
     sg = torch.zeros((sp.shape[0], 9), device=gpu)
     N.call("tgs_tide_rasterize_bwd", 1, N.ptr(L["splats"]), None, W, H, tw, th, N.ptr(d_offs),
-           N.ptr(d_flat), r_flat.size, N.ptr(alp), N.ptr(last), N.ptr(d_v), N.ptr(sg), s)
+           N.ptr(d_flat), r_flat.size, N.ptr(alp), N.ptr(last), N.ptr(d_v), None, N.ptr(sg), s)
     vm2, vc, vcol, vo, _ = R.rasterize_bwd(m2d, con, col, op, W, H, 16, r_offs[None], r_flat,
                                            ref_a, ref_last, v.numpy())
     used = np.unique(r_flat)

@@ -157,7 +157,8 @@ def test_projection_covars(gpu):
     assert rel_l2(to_np(dc.grad), v_cov) < 1e-4
 
 
-@pytest.mark.parametrize("degree,K", [(0, 16), (1, 16), (2, 9), (3, 16), (4, 25)])
+@pytest.mark.parametrize("degree,K", [(0, 16), (1, 16), (2, 9), (3, 16), (4, 25), (1, 4),
+                                      (2, 12)])
 def test_spherical_harmonics(gpu, degree, K):
     announce(f"sh degree={degree} K={K}")
     g = torch.Generator().manual_seed(degree)

@@ -109,7 +109,9 @@ SIGNATURES = {
     "tgs_tide_rasterize_fwd": (
         ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, U64, P]),
     "tgs_tide_rasterize_bwd": (
-        ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, P]),
+        ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, P, P]),
+    "tgs_pack_splats": (ctypes.c_int, [U64, P, P, P, P, P, P]),
+    "tgs_unpack_splat_grads": (ctypes.c_int, [U64, P, P, P, P, P, P]),
     "tgs_tide_project_bwd": (
         ctypes.c_int,
         [U32, P, P, P, P, U32, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, I32, P, P, U32, P]),

@@ -132,3 +132,62 @@ extern "C" int tgs_rasterize_to_pixels_bwd(
   }
 #undef TGS_BWD_CASE
 }
+
+// ---------------------------------------------------------------------------
+// Packed records for the 3-channel case: the drop-in op packs gsplat's SoA
+// tensors into the fused step's 48-byte splat records (one gather per
+// staged Gaussian instead of four) and runs tgs_tide_rasterize_fwd/bwd on
+// them; the backward's 9-float gradient records are unpacked into the SoA
+// gradient tensors.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) pack_splats_kernel(uint64_t n, const float* __restrict__ m2d,
+                                                          const float* __restrict__ con,
+                                                          const float* __restrict__ col,
+                                                          const float* __restrict__ op,
+                                                          float4* __restrict__ rec) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= n) return;
+  rec[3 * i + 0] = make_float4(m2d[2 * i], m2d[2 * i + 1], op[i], 0.f);
+  rec[3 * i + 1] = make_float4(con[3 * i], con[3 * i + 1], con[3 * i + 2], 0.f);
+  rec[3 * i + 2] = make_float4(col[3 * i], col[3 * i + 1], col[3 * i + 2], 0.f);
+}
+
+__global__ void __launch_bounds__(256) unpack_splat_grads_kernel(
+    uint64_t n, const float* __restrict__ g, float* __restrict__ v_m2d,
+    float* __restrict__ v_con, float* __restrict__ v_col, float* __restrict__ v_op) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= n) return;
+  const float* r = g + 9 * i;
+  v_m2d[2 * i] = r[0];
+  v_m2d[2 * i + 1] = r[1];
+  v_con[3 * i] = r[2];
+  v_con[3 * i + 1] = r[3];
+  v_con[3 * i + 2] = r[4];
+  v_col[3 * i] = r[5];
+  v_col[3 * i + 1] = r[6];
+  v_col[3 * i + 2] = r[7];
+  v_op[i] = r[8];
+}
+
+extern "C" int tgs_pack_splats(uint64_t n, const float* means2d, const float* conics,
+                               const float* colors, const float* opacities, float* splats,
+                               hipStream_t stream) {
+  if (n == 0) return TGS_OK;
+  TGS_CHECK_ARG(means2d && conics && colors && opacities && splats, "pack_splats: null pointer");
+  TGS_CHECK_ARG(((uintptr_t)splats & 15u) == 0, "pack_splats: splats must be 16-byte aligned");
+  hipLaunchKernelGGL(pack_splats_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     n, means2d, conics, colors, opacities, (float4*)splats);
+  TGS_RETURN_LAUNCH("tgs_pack_splats");
+}
+
+extern "C" int tgs_unpack_splat_grads(uint64_t n, const float* splat_grads, float* v_means2d,
+                                      float* v_conics, float* v_colors, float* v_opacities,
+                                      hipStream_t stream) {
+  if (n == 0) return TGS_OK;
+  TGS_CHECK_ARG(splat_grads && v_means2d && v_conics && v_colors && v_opacities,
+                "unpack_splat_grads: null pointer");
+  hipLaunchKernelGGL(unpack_splat_grads_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     stream, n, splat_grads, v_means2d, v_conics, v_colors, v_opacities);
+  TGS_RETURN_LAUNCH("tgs_unpack_splat_grads");
+}
+

@@ -986,8 +986,8 @@ extern "C" int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const flo
                                       uint32_t tile_height, const int32_t* tile_offsets,
                                       const int32_t* flatten_ids, uint32_t n_isects,
                                       const float* alphas, const int32_t* last_ids,
-                                      const float* v_images, float* splat_grads,
-                                      hipStream_t stream) {
+                                      const float* v_images, const float* v_alphas,
+                                      float* splat_grads, hipStream_t stream) {
   if (C == 0 || W == 0 || H == 0 || n_isects == 0) return TGS_OK;
   TGS_CHECK_ARG(splats && tile_offsets && flatten_ids && alphas && last_ids && v_images &&
                     splat_grads,
@@ -997,7 +997,7 @@ extern "C" int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const flo
   hipLaunchKernelGGL((raster_bwd_kernel<3, 16, PackedSplats, PackedGrads>),
                      dim3(C, tile_height, tile_width), dim3(256), 0, stream, G,
                      PackedSplats{(const float4*)splats}, PackedGrads{splat_grads}, backgrounds,
-                     tile_offsets, flatten_ids, alphas, last_ids, v_images, (const float*)nullptr);
+                     tile_offsets, flatten_ids, alphas, last_ids, v_images, v_alphas);
   TGS_RETURN_LAUNCH("tgs_tide_rasterize_bwd");
 }
 

@@ -385,7 +385,20 @@ def isect_offset_encode(isect_ids: Tensor, n_cameras: int, tile_width: int,
 # ---------------------------------------------------------------------------
 
 
+def _packed_splats(means2d, conics, colors, opacities) -> Tensor:
+    """gsplat's SoA splat tensors as the 48-byte records [n, 12] of the packed
+    rasterizer kernels (one gather per staged Gaussian instead of four)."""
+    n = opacities.numel()
+    rec = torch.empty((max(n, 1), 12), dtype=torch.float32, device=means2d.device)
+    N.call("tgs_pack_splats", n, N.ptr(means2d), N.ptr(conics), N.ptr(colors), N.ptr(opacities),
+           N.ptr(rec), _stream())
+    return rec
+
+
 class _RasterizeToPixels(torch.autograd.Function):
+    """3 channels at tile 16 without absgrad (TideGS's case) run the packed
+    record kernels; every other shape runs the SoA kernels."""
+
     @staticmethod
     def forward(ctx, means2d, conics, colors, opacities, backgrounds, width, height, tile_size,
                 isect_offsets, flatten_ids, absgrad):
@@ -396,19 +409,27 @@ class _RasterizeToPixels(torch.autograd.Function):
         render_colors = torch.empty((C, height, width, ch), dtype=torch.float32, device=dev)
         render_alphas = torch.empty((C, height, width, 1), dtype=torch.float32, device=dev)
         last_ids = torch.empty((C, height, width), dtype=torch.int32, device=dev)
-        N.call("tgs_rasterize_to_pixels_fwd", C, ch, N.ptr(means2d), N.ptr(conics), N.ptr(colors),
-               N.ptr(opacities), N.ptr(backgrounds), width, height, tile_size, tw, th,
-               N.ptr(isect_offsets), N.ptr(flatten_ids), flatten_ids.numel(), N.ptr(render_colors),
-               N.ptr(render_alphas), N.ptr(last_ids), _stream())
+        records = None
+        if ch == 3 and tile_size == 16 and not absgrad:
+            records = _packed_splats(means2d, conics, colors, opacities)
+            N.call("tgs_tide_rasterize_fwd", C, N.ptr(records), N.ptr(backgrounds), width, height,
+                   tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids), flatten_ids.numel(),
+                   N.ptr(render_colors), N.ptr(render_alphas), N.ptr(last_ids), None, 0,
+                   _stream())
+        else:
+            N.call("tgs_rasterize_to_pixels_fwd", C, ch, N.ptr(means2d), N.ptr(conics),
+                   N.ptr(colors), N.ptr(opacities), N.ptr(backgrounds), width, height, tile_size,
+                   tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids), flatten_ids.numel(),
+                   N.ptr(render_colors), N.ptr(render_alphas), N.ptr(last_ids), _stream())
         ctx.save_for_backward(means2d, conics, colors, opacities, backgrounds, isect_offsets,
-                              flatten_ids, render_alphas, last_ids)
+                              flatten_ids, render_alphas, last_ids, records)
         ctx.width, ctx.height, ctx.tile_size, ctx.absgrad = width, height, tile_size, absgrad
         return render_colors, render_alphas
 
     @staticmethod
     def backward(ctx, v_render_colors, v_render_alphas):
         (means2d, conics, colors, opacities, backgrounds, isect_offsets, flatten_ids,
-         render_alphas, last_ids) = ctx.saved_tensors
+         render_alphas, last_ids, records) = ctx.saved_tensors
         C = isect_offsets.shape[0]
         th, tw = isect_offsets.shape[1], isect_offsets.shape[2]
         ch = colors.shape[-1]
@@ -420,12 +441,23 @@ class _RasterizeToPixels(torch.autograd.Function):
         v_colors = torch.zeros_like(colors)
         v_opacities = torch.zeros_like(opacities)
         v_abs = torch.zeros_like(means2d) if ctx.absgrad else None
-        N.call("tgs_rasterize_to_pixels_bwd", C, ch, N.ptr(means2d), N.ptr(conics), N.ptr(colors),
-               N.ptr(opacities), N.ptr(backgrounds), ctx.width, ctx.height, ctx.tile_size, tw, th,
-               N.ptr(isect_offsets), N.ptr(flatten_ids), flatten_ids.numel(),
-               N.ptr(render_alphas), N.ptr(last_ids), N.ptr(v_render_colors),
-               N.ptr(v_render_alphas), N.ptr(v_abs), N.ptr(v_means2d), N.ptr(v_conics),
-               N.ptr(v_colors), N.ptr(v_opacities), _stream())
+        if records is not None:
+            n = opacities.numel()
+            grads = torch.zeros((max(n, 1), 9), dtype=torch.float32, device=means2d.device)
+            N.call("tgs_tide_rasterize_bwd", C, N.ptr(records), N.ptr(backgrounds), ctx.width,
+                   ctx.height, tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids),
+                   flatten_ids.numel(), N.ptr(render_alphas), N.ptr(last_ids),
+                   N.ptr(v_render_colors), N.ptr(v_render_alphas), N.ptr(grads), _stream())
+            N.call("tgs_unpack_splat_grads", n, N.ptr(grads), N.ptr(v_means2d), N.ptr(v_conics),
+                   N.ptr(v_colors), N.ptr(v_opacities), _stream())
+        else:
+            N.call("tgs_rasterize_to_pixels_bwd", C, ch, N.ptr(means2d), N.ptr(conics),
+                   N.ptr(colors), N.ptr(opacities), N.ptr(backgrounds), ctx.width, ctx.height,
+                   ctx.tile_size, tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids),
+                   flatten_ids.numel(), N.ptr(render_alphas), N.ptr(last_ids),
+                   N.ptr(v_render_colors), N.ptr(v_render_alphas), N.ptr(v_abs),
+                   N.ptr(v_means2d), N.ptr(v_conics), N.ptr(v_colors), N.ptr(v_opacities),
+                   _stream())
         if ctx.absgrad:
             ctx.saved_tensors[0].absgrad = v_abs
         v_backgrounds = None

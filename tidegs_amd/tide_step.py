@@ -397,7 +397,7 @@ class TideStep:
         self._begin("raster_bwd")
         N.call("tgs_tide_rasterize_bwd", C, N.ptr(splats), N.ptr(bg), W, H, tw, th,
                N.ptr(offsets), N.ptr(fids), n_isects, N.ptr(alphas), N.ptr(last_ids),
-               N.ptr(v_images), N.ptr(sgrads), s)
+               N.ptr(v_images), None, N.ptr(sgrads), s)
         self._end()
 
         # 5. per touched row: projection + SH + activation backward (and, with
