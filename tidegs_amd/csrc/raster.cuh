@@ -80,6 +80,7 @@ struct SoAGrads {
   float* v_opacities;
   float* v_means2d_abs;  // may be null
   static constexpr int NV = 6 + CDIM;
+  static constexpr bool MAY_ABS = true;  // |mean2d| gradients when v_means2d_abs is set
   __device__ __forceinline__ bool absgrad() const { return v_means2d_abs != nullptr; }
   __device__ __forceinline__ float* ptr(int32_t g, int k) const {
     const int64_t gg = g;
@@ -115,6 +116,7 @@ struct PackedSplats {
 struct PackedGrads {
   float* grads;  // [V, 9]
   static constexpr int NV = 9;
+  static constexpr bool MAY_ABS = false;
   __device__ __forceinline__ bool absgrad() const { return false; }
   __device__ __forceinline__ float* ptr(int32_t g, int k) const { return grads + (int64_t)g * 9 + k; }
 };
@@ -192,24 +194,27 @@ __device__ __forceinline__ float raster_power(const float4& g0, const float2& g1
 }
 
 // Compact batch entries [j_lo, batch_size) whose box meets the wave's pixel
-// strip into s_list (ascending j).  Returns the count (wave-uniform).
+// strip into s_list (ascending j).  Returns the count (wave-uniform); `hits`
+// receives the membership bits of entries 0..63 (bit j set iff j is listed).
 template <int BLOCK>
 __device__ __forceinline__ int build_wave_list(const float4* s_box, uint8_t* s_list, int j_lo,
                                                int batch_size, float x0, float x1, float y0,
-                                               float y1) {
-  const int lane = threadIdx.x & 63;
-  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+                                               float y1, uint64_t& hits) {
   int count = 0;
 #pragma unroll
   for (int k = 0; k < BLOCK; k += 64) {
-    const int j = k + lane;
+    const int j = k + (int)(threadIdx.x & 63);
     bool hit = false;
     if (j >= j_lo && j < batch_size) {
       const float4 b = s_box[j];
       hit = !(b.y < x0 || b.x > x1 || b.w < y0 || b.z > y1);
     }
     const uint64_t m = tgs_ballot(hit);
-    if (hit) s_list[count + __popcll(m & lt)] = (uint8_t)j;
+    if (k == 0) hits = m;
+    // rank among the hits below this lane: mbcnt counts the mask bits of lower lanes
+    const int rank = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (hit) s_list[count + rank] = (uint8_t)j;
     count += __popcll(m);
   }
   __builtin_amdgcn_wave_barrier();
@@ -256,14 +261,15 @@ __device__ __forceinline__ uint32_t cover_row(const float4& g0, const float2& g1
 }
 
 // Pixel-row masks of the first n_list entries of a wavefront's list: lane
-// (e, r) computes entry li0 + e, row r; the ROWS masks of an entry form its
-// 64-bit pixel mask (bit r * TILE + j = pixel (r, j) of the strip), which is
-// stored to s_em and also returned to lane e * ROWS.
+// (e, r) computes entry li0 + e, row r.  The ROWS masks of an entry form its
+// 64-bit pixel mask (bit r * TILE + j = pixel (r, j) of the strip = lane
+// r * TILE + j), stored as two 32-bit halves: s_emh[0][li] holds lanes 0..31,
+// s_emh[1][li] lanes 32..63, so that a lane reads only its own half.
 template <int TILE, int BATCH>
 __device__ __forceinline__ void strip_masks(const uint8_t* s_list, int n_list, const float4* s_g0,
                                             const float2* s_g1, const float4* s_box,
-                                            const float4* s_cov, uint64_t* s_em, float px0,
-                                            float py0, uint64_t alive) {
+                                            const float4* s_cov, uint32_t (*s_emh)[BATCH],
+                                            float px0, float py0, uint64_t alive) {
   using RM = typename std::conditional<TILE == 16, uint16_t, uint8_t>::type;
   constexpr int ROWS = 64 / TILE;
   constexpr int PER = 64 / ROWS;  // entries per pass
@@ -276,7 +282,8 @@ __device__ __forceinline__ void strip_masks(const uint8_t* s_list, int n_list, c
       const int t = s_list[li];
       const uint32_t m =
           cover_row<TILE>(s_g0[t], s_g1[t], s_box[t], s_cov[t], px0, py0 + (float)r);
-      reinterpret_cast<RM*>(&s_em[li])[r] = (RM)(m & alive_row);
+      reinterpret_cast<RM*>(&s_emh[(r * TILE) >> 5][li])[((r * TILE) & 31) / TILE] =
+          (RM)(m & alive_row);
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -284,29 +291,49 @@ __device__ __forceinline__ void strip_masks(const uint8_t* s_list, int n_list, c
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// This lane's bits of the list masks: bit li of word li / 32 is bit `lane` of
-// s_em[li], for li in [li_min, n_list).
-template <int WORDS>
-__device__ __forceinline__ void lane_bits(const uint64_t* s_em, int n_list, int li_min,
+// This lane's bits of the list masks: bit li of word li / 32 is this lane's
+// bit of entry li's mask, for li in [li_min, n_list).  `half` is the lane's
+// half row s_emh[lane / 32] (16-byte aligned): one LDS read serves four
+// entries.  UNROLL picks a fully unrolled read sequence (faster where the
+// kernel has registers to spare) over a compact loop per word.
+template <int WORDS, bool UNROLL>
+__device__ __forceinline__ void lane_bits(const uint32_t* half, int n_list, int li_min,
                                           uint32_t (&mw)[WORDS]) {
-  const int lane = threadIdx.x & 63;
-  const uint32_t* em32 = reinterpret_cast<const uint32_t*>(s_em) + (lane >> 5);
-  const int sh = lane & 31;
+  const uint32_t sh = threadIdx.x & 31;
+  const uint4* q4 = reinterpret_cast<const uint4*>(half);
+  if (UNROLL) {
+#pragma unroll
+    for (int W = 0; W < WORDS; ++W) mw[W] = 0u;
+#pragma unroll
+    for (int q = 0; q < WORDS * 8; ++q) {
+      if (4 * q >= n_list) break;
+      const uint4 x = q4[q];
+      const uint32_t b = ((x.x >> sh) & 1u) | (((x.y >> sh) & 1u) << 1) |
+                         (((x.z >> sh) & 1u) << 2) | (((x.w >> sh) & 1u) << 3);
+      mw[q >> 3] |= b << (4 * (q & 7));
+    }
+  } else {
+#pragma unroll
+    for (int W = 0; W < WORDS; ++W) {
+      uint32_t w = 0u;
+      const int qn = min(8, (n_list - 32 * W + 3) >> 2);  // wave-uniform
+#pragma unroll 1
+      for (int q = 0; q < qn; ++q) {
+        const uint4 x = q4[8 * W + q];
+        const uint32_t b = ((x.x >> sh) & 1u) | (((x.y >> sh) & 1u) << 1) |
+                           (((x.z >> sh) & 1u) << 2) | (((x.w >> sh) & 1u) << 3);
+        w |= b << (4 * q);
+      }
+      mw[W] = w;
+    }
+  }
+  // keep positions [li_min, n_list): the words past n_list hold stale masks
 #pragma unroll
   for (int W = 0; W < WORDS; ++W) {
-    uint32_t w = 0;
-    const int lim = min(32, n_list - W * 32);
-    const uint32_t* e = em32 + 2 * W * 32;
-    int bb = 0;
-    for (; bb + 2 <= lim; bb += 2) {
-      const uint32_t d0 = e[2 * bb], d1 = e[2 * bb + 2];
-      w |= (((d0 >> sh) & 1u) | (((d1 >> sh) & 1u) << 1)) << bb;
-    }
-    if (bb < lim) w |= ((e[2 * bb] >> sh) & 1u) << bb;
-    const int lo = li_min - W * 32;  // clear positions below li_min
-    if (lo >= 32) w = 0u;
-    else if (lo > 0) w &= ~((1u << lo) - 1u);
-    mw[W] = w;
+    const int lo = min(max(li_min - 32 * W, 0), 32), hi = min(max(n_list - 32 * W, 0), 32);
+    const uint32_t below_hi = hi >= 32 ? 0xffffffffu : ((1u << hi) - 1u);
+    const uint32_t below_lo = lo >= 32 ? 0xffffffffu : ((1u << lo) - 1u);
+    mw[W] &= below_hi & ~below_lo;
   }
 }
 
@@ -344,13 +371,13 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
   __shared__ float4 s_cov[BATCH];
   __shared__ float s_col[BATCH][CDIM];
   __shared__ uint8_t s_list[WAVES][BATCH];
-  __shared__ uint64_t s_em[WAVES][BATCH];
+  __shared__ __align__(16) uint32_t s_emh[WAVES][2][BATCH];
 
   const uint32_t cam = blockIdx.x;
   const uint32_t ty = blockIdx.y, tx = blockIdx.z;
   const uint32_t tile_id = ty * G.tile_w + tx;
   const uint32_t tr = threadIdx.x;
-  const int wave = tr >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(tr >> 6));  // wave-uniform
   const uint32_t i = ty * TILE + tr / TILE;
   const uint32_t j = tx * TILE + tr % TILE;
   const uint64_t img = (uint64_t)cam * G.H * G.W;
@@ -378,9 +405,10 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     if (__syncthreads_count(done) >= BLOCK) break;
     const int32_t batch_start = range_start + BATCH * b;
     const int32_t idx = batch_start + (int32_t)tr;
-    if ((int)tr < BATCH && idx < range_end) {
-      SplatData<CDIM> s;
-      src.load(flatten_ids[idx], s);
+    const bool have = (int)tr < BATCH && idx < range_end;
+    SplatData<CDIM> s;
+    if (have) src.load(flatten_ids[idx], s);
+    if (have) {
       const StagedGeo sg = stage_geo<CDIM>(s);
       s_g0[tr] = sg.g0;
       s_g1[tr] = sg.g1;
@@ -393,12 +421,13 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     const int32_t batch_size = min(BATCH, range_end - batch_start);
     const uint64_t alive = tgs_ballot(!done);
     if (!alive) continue;
+    uint64_t hits;
     const int n_list =
-        build_wave_list<BATCH>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1);
-    strip_masks<TILE, BATCH>(s_list[wave], n_list, s_g0, s_g1, s_box, s_cov, s_em[wave], wx0, wy0,
-                             alive);
+        build_wave_list<BATCH>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1, hits);
+    strip_masks<TILE, BATCH>(s_list[wave], n_list, s_g0, s_g1, s_box, s_cov, s_emh[wave], wx0,
+                             wy0, alive);
     uint32_t mw[WORDS];
-    lane_bits<WORDS>(s_em[wave], n_list, 0, mw);
+    lane_bits<WORDS, false>(s_emh[wave][(tr & 63) >> 5], n_list, 0, mw);
 #pragma unroll
     for (int W = 0; W < WORDS; ++W) {
       if (W * 32 >= n_list) break;
@@ -475,11 +504,11 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
 // wave reduction.  When a batch has more pairs than the buffer holds, the list
 // is processed in consecutive segments (each Gaussian's pairs fit: <= 64).
 // ---------------------------------------------------------------------------
-#define RB_PAIRS 384  // pair-buffer slots per wavefront
+#define RB_PAIRS 320  // pair-buffer slots per wavefront
 #define RB_BATCH 64  // Gaussians staged per batch
 
 template <int CDIM, int TILE, class Src, class Sink>
-__global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
+__global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kernel(
     RasterGeom G, Src src, Sink sink, const float* __restrict__ backgrounds,
     const int32_t* __restrict__ tile_offsets, const int32_t* __restrict__ flatten_ids,
     const float* __restrict__ render_alphas, const int32_t* __restrict__ last_ids,
@@ -501,18 +530,22 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
   __shared__ float4 s_box[BATCH];
   __shared__ float4 s_cov[BATCH];
   __shared__ float2 s_pair[WAVES][RB_PAIRS];  // (alpha T, v_sigma)
-  __shared__ uint64_t s_em[WAVES][BATCH];         // pixel mask of each list entry
-  __shared__ uint16_t s_po[WAVES][BATCH + 1];     // first pair slot of each list entry
-  __shared__ float s_stage[WAVES][32 * NA];       // one owner group's gradient values
+  __shared__ __align__(16) uint32_t s_emh[WAVES][2][BATCH];  // pixel mask halves of each list entry
+  // first pair slot of each list entry's half: [0][li] that of lanes 0..31
+  // (and [0][n_list] the list's total), [1][li] that of lanes 32..63
+  __shared__ uint16_t s_poh[WAVES][2][BATCH + 1];
+  __shared__ float s_stage[WAVES][32 * (Sink::MAY_ABS ? NA : NV)];  // one owner group's values
   __shared__ int32_t s_gid[WAVES][32];            // and their Gaussian ids
 
   const uint32_t cam = blockIdx.x;
   const uint32_t ty = blockIdx.y, tx = blockIdx.z;
   const uint32_t tile_id = ty * G.tile_w + tx;
   const uint32_t tr = threadIdx.x;
+  static_assert(BATCH == 64, "one list entry per lane");
   const int lane = tr & 63;
-  const int wave = tr >> 6;
-  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(tr >> 6));  // wave-uniform
+  const int half = lane >> 5;
+  const uint32_t lt_half = (1u << (lane & 31)) - 1u;  // lanes below this one in its half
   const uint32_t i = ty * TILE + tr / TILE;
   const uint32_t j = tx * TILE + tr % TILE;
   const bool inside = i < G.H && j < G.W;
@@ -531,11 +564,12 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
 
   const float T_final = 1.f - render_alphas[pid];
   float T = T_final;
-  float buffer[CDIM];
+  // the colour sum behind the current Gaussian enters v_alpha only through its
+  // dot product with dL/dcolor: buffer_dot = sum_k buffer_k v_rc_k
+  float buffer_dot = 0.f;
   float v_rc[CDIM];
 #pragma unroll
   for (int k = 0; k < CDIM; ++k) {
-    buffer[k] = 0.f;
     v_rc[k] = v_render_colors[pid * CDIM + k];
     s_vrc[tr][k] = v_rc[k];
   }
@@ -559,10 +593,11 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
     const int32_t batch_end = range_end - 1 - BATCH * b;
     const int32_t batch_size = min(BATCH, batch_end + 1 - range_start);
     const int32_t idx = batch_end - (int32_t)tr;
-    if ((int)tr < BATCH && idx >= range_start) {
-      const int32_t g = flatten_ids[idx];
-      SplatData<CDIM> s;
-      src.load(g, s);
+    const bool have = (int)tr < BATCH && idx >= range_start;
+    const int32_t g = have ? flatten_ids[idx] : 0;
+    SplatData<CDIM> s;
+    if (have) src.load(g, s);
+    if (have) {
       const StagedGeo sg = stage_geo<CDIM>(s);
       s_g0[tr] = sg.g0;
       s_g1[tr] = sg.g1;
@@ -580,35 +615,37 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
     // entries with global index > wave_bin_final contribute to no pixel of this wave
     const int j_lo = max(0, batch_end - wave_bin_final);
     int n_list = 0;
+    uint64_t hits = 0;
     if (alive)
-      n_list =
-          build_wave_list<BATCH>(s_box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1);
+      n_list = build_wave_list<BATCH>(s_box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1,
+                                      hits);
     // 1. pixel masks, slot ranges and this lane's bits over the list
     uint32_t m[WORDS];
 #pragma unroll
     for (int W = 0; W < WORDS; ++W) m[W] = 0u;
     uint32_t n_pairs = 0;  // wave-uniform
     if (n_list) {
-      strip_masks<TILE, BATCH>(s_list[wave], n_list, s_g0, s_g1, s_box, s_cov, s_em[wave], wx0, wy0,
-                               alive);
-      const uint32_t cnt = lane < n_list ? (uint32_t)__popcll(s_em[wave][lane]) : 0u;
-      const uint32_t inc = wave_incl_scan(cnt);
-      if (lane < n_list) s_po[wave][lane] = (uint16_t)(inc - cnt);
-      n_pairs = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
-      if (lane == 63) s_po[wave][n_list] = (uint16_t)inc;
-      // list positions before li_min hold entries behind this lane's last
-      // contributor (the list is ascending in t)
-      int li_min = 0;
-      if (t_min > 0) {
-        int lo = 0, hi = n_list;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if ((int)s_list[wave][mid] < t_min) lo = mid + 1;
-          else hi = mid;
-        }
-        li_min = lo;
+      strip_masks<TILE, BATCH>(s_list[wave], n_list, s_g0, s_g1, s_box, s_cov, s_emh[wave], wx0,
+                               wy0, alive);
+      uint32_t c_lo = 0u, c_hi = 0u;
+      if (lane < n_list) {
+        c_lo = (uint32_t)__popc(s_emh[wave][0][lane]);
+        c_hi = (uint32_t)__popc(s_emh[wave][1][lane]);
       }
-      lane_bits<WORDS>(s_em[wave], n_list, li_min, m);
+      const uint32_t cnt = c_lo + c_hi;
+      const uint32_t inc = wave_incl_scan(cnt);
+      if (lane < n_list) {
+        s_poh[wave][0][lane] = (uint16_t)(inc - cnt);
+        s_poh[wave][1][lane] = (uint16_t)(inc - cnt + c_lo);
+      }
+      n_pairs = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+      if (lane == 63) s_poh[wave][0][n_list] = (uint16_t)inc;
+      // list positions before li_min hold entries behind this lane's last
+      // contributor: the listed entries t < t_min (the list is ascending in t)
+      const int li_min =
+          t_min <= 0 ? 0
+                     : __popcll(hits & (t_min >= 64 ? ~0ull : ((1ull << t_min) - 1ull)));
+      lane_bits<WORDS, true>(s_emh[wave][half], n_list, li_min, m);
       if (!((alive >> lane) & 1ull)) {
 #pragma unroll
         for (int W = 0; W < WORDS; ++W) m[W] = 0u;
@@ -616,21 +653,21 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
     }
     int a = 0;        // first list entry of the current segment
     while (a < n_list) {
-      const uint32_t base = s_po[wave][a];
+      const uint32_t base = s_poh[wave][0][a];
       // largest end with at most RB_PAIRS pairs (an entry has <= 64)
       int e_end = n_list;
       if (n_pairs - base > RB_PAIRS) {
-        int lo = a + 1, hi = n_list;  // s_po[lo] - base <= RB_PAIRS < s_po[hi] - base
+        int lo = a + 1, hi = n_list;  // s_poh[0][lo] - base <= RB_PAIRS < s_poh[0][hi] - base
         while (hi - lo > 1) {
           const int mid = (lo + hi) >> 1;
-          if ((uint32_t)s_po[wave][mid] - base <= RB_PAIRS) lo = mid;
+          if ((uint32_t)s_poh[wave][0][mid] - base <= RB_PAIRS) lo = mid;
           else hi = mid;
         }
         e_end = lo;
       }
       // zero the segment's slots: pixels that fail the exact test or do not
       // composite an entry leave theirs untouched
-      const uint32_t seg_pairs = (uint32_t)s_po[wave][e_end] - base;
+      const uint32_t seg_pairs = (uint32_t)s_poh[wave][0][e_end] - base;
       for (uint32_t s = lane; s < seg_pairs; s += 64) s_pair[wave][s] = make_float2(0.f, 0.f);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -657,17 +694,16 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
               const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
               T *= ra;
               const float fac = alpha * T;
-              float v_alpha = ra * tf_term;
+              // v_alpha = sum_k (c_k T - buffer_k ra) v_rc_k + ra tf_term
+              float cv = 0.f;
 #pragma unroll
-              for (int k = 0; k < CDIM; ++k) {
-                const float ck = s_col[t][k];
-                v_alpha += (ck * T - buffer[k] * ra) * v_rc[k];
-                buffer[k] += ck * fac;
-              }
+              for (int k = 0; k < CDIM; ++k) cv = fmaf(s_col[t][k], v_rc[k], cv);
+              const float v_alpha = fmaf(T, cv, ra * (tf_term - buffer_dot));
+              buffer_dot = fmaf(fac, cv, buffer_dot);
               // reference: the sigma terms only where alpha was not clamped
               const float v_sigma = raw <= 0.999f ? -raw * v_alpha : 0.f;
-              const uint32_t slot = (uint32_t)s_po[wave][li] - base +
-                                    (uint32_t)__popcll(s_em[wave][li] & lt_mask);
+              const uint32_t slot = (uint32_t)s_poh[wave][half][li] - base +
+                                    (uint32_t)__popc(s_emh[wave][half][li] & lt_half);
               s_pair[wave][slot] = make_float2(fac, v_sigma);
             }
           }
@@ -692,10 +728,8 @@ __global__ void __launch_bounds__(TILE* TILE) raster_bwd_kernel(
           t = s_list[wave][li];
           const float4 g0 = s_g0[t];
           q = staged_conic_rop(g0, s_g1[t]);
-          const uint64_t em = s_em[wave][li];
-          uint32_t slot = (uint32_t)s_po[wave][li] - base +
-                          (oh == 0 ? 0u : (uint32_t)__popc((uint32_t)em));
-          const uint32_t hb = (uint32_t)(em >> (32 * oh));
+          uint32_t slot = (uint32_t)s_poh[wave][oh][li] - base;
+          const uint32_t hb = s_emh[wave][oh][li];
           if (TILE == 16) {
             // the half is two pixel rows; within a row dy is constant, so
             // each row's dy moments follow from its sum(v_sigma) and

@@ -53,12 +53,13 @@ class PlyHeader:
 
     @property
     def vertex_dtype(self) -> np.dtype:
-        fields = []
-        for name, ply_type in self.vertex_properties:
-            if ply_type not in PLY_DTYPE_MAP:
-                raise ValueError(f"Unsupported PLY property type {ply_type!r} for {name!r}")
-            fields.append((name, PLY_DTYPE_MAP[ply_type]))
-        return np.dtype(fields)
+        """Packed little-endian record of one vertex, in header order."""
+        bad = [f"{name} ({kind})" for name, kind in self.vertex_properties
+               if kind not in PLY_DTYPE_MAP]
+        if bad:
+            raise ValueError("PLY vertex properties of unsupported type: " + ", ".join(bad))
+        return np.dtype({"names": [name for name, _ in self.vertex_properties],
+                         "formats": [PLY_DTYPE_MAP[kind] for _, kind in self.vertex_properties]})
 
 
 def read_binary_ply_header(path) -> PlyHeader:
