@@ -470,13 +470,17 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
   }
 }
 
-// Inclusive prefix sum over the 64 lanes.
+// Inclusive prefix sum over the 64 lanes, in DPP: shifts by 1, 2, 4, 8 within
+// each 16-lane row (lanes shifted in from outside the row add 0), then row 0's
+// total into row 1 and row 2's into row 3 (row_bcast:15), then the total of
+// rows 0-1 into rows 2 and 3 (row_bcast:31).  No lane-address registers.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t o = __shfl_up(v, off, 64);
-    if ((int)(threadIdx.x & 63) >= off) v += o;
-  }
+  v += tgs_dpp_u32<0x111, 0xf, 0xf, true>(v);  // row_shr:1
+  v += tgs_dpp_u32<0x112, 0xf, 0xf, true>(v);  // row_shr:2
+  v += tgs_dpp_u32<0x114, 0xf, 0xf, true>(v);  // row_shr:4
+  v += tgs_dpp_u32<0x118, 0xf, 0xf, true>(v);  // row_shr:8
+  v += tgs_dpp_u32<0x142, 0xa>(v);             // row_bcast:15 into rows 1 and 3
+  v += tgs_dpp_u32<0x143, 0xc>(v);             // row_bcast:31 into rows 2 and 3
   return v;
 }
 
