@@ -14,6 +14,14 @@ def to_np(t):
     return t.detach().cpu().numpy() if isinstance(t, torch.Tensor) else np.asarray(t)
 
 
+def clamp_marks(colors) -> np.ndarray:
+    """Channels of fused-step splat records whose colour the projection
+    clamped (clamp_min(SH + 0.5, 0)): stored as -0.0, given no colour
+    gradient by the rasterizer backward."""
+    c = np.asarray(colors)
+    return np.signbit(c) & (c == 0)
+
+
 def announce(msg: str) -> None:
     print(f"[gpu-case] {msg}", flush=True)
 

@@ -40,7 +40,7 @@ import torch
 from oracle import raster_ref as R
 from oracle import ssim_ref as S
 from oracle import step_ref as SR
-from tests.gpu_util import announce, check_isect_properties, rel_l2, to_np
+from tests.gpu_util import announce, check_isect_properties, clamp_marks, rel_l2, to_np
 from tidegs_amd import _native as N
 from tidegs_amd import scenes
 from tidegs_amd.tide_step import TideStep
@@ -132,6 +132,8 @@ def _check_downstream(ts, stats, params, g_filters, vm, K, gt, W, H, grads):
         assert rel_l2(vimg[c].transpose(2, 0, 1), v_ref) < 1e-5
         vm2, vcon, vcol, vop, _ = R.rasterize_bwd(*splat, W, H, 16, toffs, flat, alphas, last,
                                                   vimg[c][None])
+        # channels the projection clamped (stored as -0.0) get no colour gradient
+        vcol = np.where(clamp_marks(rec[:, 8:11]), 0.0, vcol)
         mine = sgr[offs[c]:offs[c + 1]]
         for name, got, ref in (("means2d", mine[:, 0:2], vm2), ("conics", mine[:, 2:5], vcon),
                                ("colors", mine[:, 5:8], vcol), ("opacities", mine[:, 8], vop)):

@@ -27,7 +27,7 @@ import torch
 from oracle import optim_ref as O
 from oracle import raster_ref as R
 from oracle import step_ref as SR
-from tests.gpu_util import announce, check_isect_properties as _check_isect_properties, rel_l2, to_np
+from tests.gpu_util import announce, check_isect_properties as _check_isect_properties, clamp_marks, rel_l2, to_np
 from tidegs_amd import _native as N
 from tidegs_amd import gsplat_ops as ops
 from tidegs_amd import scenes
@@ -198,6 +198,7 @@ def test_cfg4_city_hot_tiles(gpu):
            N.ptr(d_flat), r_flat.size, N.ptr(alp), N.ptr(last), N.ptr(d_v), None, N.ptr(sg), s)
     vm2, vc, vcol, vo, _ = R.rasterize_bwd(m2d, con, col, op, W, H, 16, r_offs[None], r_flat,
                                            ref_a, ref_last, v.numpy())
+    vcol = np.where(clamp_marks(col), 0.0, vcol)  # channels the projection clamped
     used = np.unique(r_flat)
     got = to_np(sg)[used]
     print(f"  hot-tile parity on {tiles.size} tiles, {r_flat.size} isects, "

@@ -54,6 +54,7 @@ struct SplatData {
 // gsplat tensor layout: means2d [*,2], conics [*,3], colors [*,CDIM], opacities [*].
 template <int CDIM>
 struct SoASplats {
+  static constexpr bool CLAMP_MARKS = false;
   const float* means2d;
   const float* conics;
   const float* colors;
@@ -95,7 +96,11 @@ struct SoAGrads {
 // Packed per-splat records of the fused step (CDIM = 3):
 //   rec[3g+0] = {x, y, opacity, depth}, rec[3g+1] = {a, b, c, radius},
 //   rec[3g+2] = {r, g, b, 0};  gradients grads[9g + k] in SoAGrads' k order.
+// A colour channel stored as -0.0 was clamped by the projection
+// (clamp_min(SH + 0.5, 0), whose gradient is zero there): the backward
+// writes a zero colour gradient for it.
 struct PackedSplats {
+  static constexpr bool CLAMP_MARKS = true;
   const float4* rec;
   __device__ __forceinline__ void load(int32_t g, SplatData<3>& s) const {
     const float4 r0 = rec[(int64_t)g * 3 + 0];
@@ -820,7 +825,10 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
           st[3] = acc[3];
           st[4] = 0.5f * acc[4];
 #pragma unroll
-          for (int k = 0; k < CDIM; ++k) st[5 + k] = acc[5 + k];
+          for (int k = 0; k < CDIM; ++k)
+            st[5 + k] = Src::CLAMP_MARKS && __float_as_uint(s_col[t][k]) == 0x80000000u
+                            ? 0.f
+                            : acc[5 + k];
           st[5 + CDIM] = -acc[5 + CDIM] * q.w;
           if (absg) {
             st[NV] = acc[NV];

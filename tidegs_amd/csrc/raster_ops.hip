@@ -149,7 +149,11 @@ __global__ void __launch_bounds__(256) pack_splats_kernel(uint64_t n, const floa
   if (i >= n) return;
   rec[3 * i + 0] = make_float4(m2d[2 * i], m2d[2 * i + 1], op[i], 0.f);
   rec[3 * i + 1] = make_float4(con[3 * i], con[3 * i + 1], con[3 * i + 2], 0.f);
-  rec[3 * i + 2] = make_float4(col[3 * i], col[3 * i + 1], col[3 * i + 2], 0.f);
+  // a colour of -0.0 marks a channel clamped by the projection (the packed
+  // rasterizer then drops its gradient); caller colours carry no such mark
+  auto unmark = [](float c) { return __float_as_uint(c) == 0x80000000u ? 0.f : c; };
+  rec[3 * i + 2] =
+      make_float4(unmark(col[3 * i]), unmark(col[3 * i + 1]), unmark(col[3 * i + 2]), 0.f);
 }
 
 __global__ void __launch_bounds__(256) unpack_splat_grads_kernel(

@@ -117,15 +117,17 @@ __device__ __forceinline__ void sh_eval3(int degree, float dx, float dy, float d
 // VJP of sh_eval3.  Writes (ACCUM: adds to) v_coeffs[k*3+c] for
 // k < (degree+1)^2 (entries above the degree are left to the caller) and
 // returns v_dir (the gradient w.r.t. the un-normalised direction) when
-// want_dir is set.
-template <bool ACCUM = false>
+// want_dir is set.  FAST_NORM normalises with the hardware reciprocal square
+// root (1 ulp) instead of an IEEE square root and division.
+template <bool ACCUM = false, bool FAST_NORM = false>
 __device__ __forceinline__ void sh_vjp3(int degree, float dx, float dy, float dz,
                                         const float* __restrict__ coeffs, const float v_col[3],
                                         float* __restrict__ v_coeffs, bool want_dir,
                                         float v_dir[3]) {
   float x = 0.f, y = 0.f, z = 0.f, inorm = 0.f;
   if (degree >= 1) {
-    inorm = 1.0f / sqrtf(dx * dx + dy * dy + dz * dz);
+    const float n2 = dx * dx + dy * dy + dz * dz;
+    inorm = FAST_NORM ? __builtin_amdgcn_rsqf(n2) : 1.0f / sqrtf(n2);
     x = dx * inorm;
     y = dy * inorm;
     z = dz * inorm;

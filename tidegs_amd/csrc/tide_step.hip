@@ -48,14 +48,18 @@ struct TideCams {
 struct CamLDS {
   Cam cam[TIDE_MAX_CAMS];
   float campos[TIDE_MAX_CAMS][3];
+  float lim[TIDE_MAX_CAMS][2];  // projection clamp 1.3 * (0.5 W / fx), 1.3 * (0.5 H / fy)
 };
 
-__device__ __forceinline__ void load_cams_lds(const TideCams& tc, CamLDS& s) {
+__device__ __forceinline__ void load_cams_lds(const TideCams& tc, CamLDS& s, int W = 0,
+                                              int H = 0) {
   for (uint32_t c = threadIdx.x; c < tc.C; c += blockDim.x) {
     s.cam[c] = load_cam(tc.viewmats + c * 16, tc.Ks + c * 9);
     s.campos[c][0] = tc.campos[c * 3 + 0];
     s.campos[c][1] = tc.campos[c * 3 + 1];
     s.campos[c][2] = tc.campos[c * 3 + 2];
+    s.lim[c][0] = 1.3f * (0.5f * (float)W / s.cam[c].fx);
+    s.lim[c][1] = 1.3f * (0.5f * (float)H / s.cam[c].fy);
   }
   __syncthreads();
 }
@@ -310,8 +314,11 @@ __device__ __forceinline__ void project_entry(
   sh_eval3(sh_degree, p[0] - campos[0], p[1] - campos[1], p[2] - campos[2], sh, col);
   out[0] = make_float4(r.mean2d[0], r.mean2d[1], opac, r.depth);
   out[1] = make_float4(r.conic[0], r.conic[1], r.conic[2], (float)r.radius);
-  out[2] = make_float4(fmaxf(col[0] + 0.5f, 0.f), fmaxf(col[1] + 0.5f, 0.f),
-                       fmaxf(col[2] + 0.5f, 0.f), 0.f);
+  // colour = clamp_min(SH + 0.5, 0); a clamped channel is stored as -0.0, so
+  // that the rasterizer backward gives it a zero gradient (the clamp's VJP)
+  auto clamp_mark = [](float v) { return v >= 0.f ? v : -0.f; };
+  out[2] = make_float4(clamp_mark(col[0] + 0.5f), clamp_mark(col[1] + 0.5f),
+                       clamp_mark(col[2] + 0.5f), 0.f);
   // tile count (isect_tiles.cu:55-70)
   const float ts = (float)tile_size;
   const float trd = (float)r.radius / ts;
@@ -526,6 +533,108 @@ __global__ void __launch_bounds__(256) tide_isect_ids_kernel(
 // ---------------------------------------------------------------------------
 // Backward: one thread per touched row.
 // ---------------------------------------------------------------------------
+// VJP of the render projection of one (row, camera) visit
+// (fully_fused_projection_bwd.cu:199-366 composed with the forward of
+// fully_fused_projection_fwd.cu:18-129), restated for the resident step.
+// Entries the forward culled carry zero splat gradients, so the backward
+// skips only the visits where its own arithmetic would not be finite: depth
+// outside [near, far] or a non-positive 2D determinant.  Reciprocals use the
+// hardware rcp (1 ulp); the camera-space covariance, its gradient and the
+// world-space covariance gradient are symmetric and formed from their six
+// unique entries (order 00, 01, 02, 11, 12, 22).  Adds d/dmean to v_p and
+// d/dSigma to vS; returns false for a skipped visit.
+__device__ __forceinline__ bool tide_visit_backward(const float p[3], const float S[6],
+                                                    const Cam& cam, float lim_x, float lim_y,
+                                                    float eps2d, float near_plane,
+                                                    float far_plane, const float vm[2],
+                                                    const float vc[3], float v_p[3],
+                                                    float vS[6]) {
+  const auto& R = cam.R;
+  float pc[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    pc[i] = cam.R[i][0] * p[0] + cam.R[i][1] * p[1] + cam.R[i][2] * p[2] + cam.t[i];
+  const float x = pc[0], y = pc[1], z = pc[2];
+  if (!(z >= near_plane && z <= far_plane)) return false;
+  // Sc = R Sigma R^T
+  float RS[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    RS[i][0] = R[i][0] * S[0] + R[i][1] * S[1] + R[i][2] * S[2];
+    RS[i][1] = R[i][0] * S[1] + R[i][1] * S[3] + R[i][2] * S[4];
+    RS[i][2] = R[i][0] * S[2] + R[i][1] * S[4] + R[i][2] * S[5];
+  }
+  auto dot3 = [](const float* a, const float* b) { return a[0] * b[0] + a[1] * b[1] + a[2] * b[2]; };
+  const float c00 = dot3(RS[0], R[0]), c01 = dot3(RS[0], R[1]), c02 = dot3(RS[0], R[2]);
+  const float c11 = dot3(RS[1], R[1]), c12 = dot3(RS[1], R[2]), c22 = dot3(RS[2], R[2]);
+  const float fx = cam.fx, fy = cam.fy;
+  const float rz = __builtin_amdgcn_rcpf(z);
+  const float rz2 = rz * rz, rz3 = rz2 * rz;
+  const float xr = x * rz, yr = y * rz;
+  const float tx = z * fminf(lim_x, fmaxf(-lim_x, xr));
+  const float ty = z * fminf(lim_y, fmaxf(-lim_y, yr));
+  const float J00 = fx * rz, J02 = -fx * tx * rz2;
+  const float J11 = fy * rz, J12 = -fy * ty * rz2;
+  // J Sc (2x3) and cov2d = J Sc J^T + eps2d I
+  const float JS0[3] = {J00 * c00 + J02 * c02, J00 * c01 + J02 * c12, J00 * c02 + J02 * c22};
+  const float JS1[3] = {J11 * c01 + J12 * c02, J11 * c11 + J12 * c12, J11 * c12 + J12 * c22};
+  const float a = JS0[0] * J00 + JS0[2] * J02 + eps2d;
+  const float b = JS0[1] * J11 + JS0[2] * J12;
+  const float d = JS1[1] * J11 + JS1[2] * J12 + eps2d;
+  const float det = a * d - b * b;
+  if (!(det > 0.f)) return false;
+  const float inv = __builtin_amdgcn_rcpf(det);
+  const float P00 = d * inv, P01 = -b * inv, P11 = a * inv;
+  // conic = cov2d^-1: dL/dcov2d = -P G P (symmetric; G's off-diagonal split
+  // evenly over the two entries)
+  const float G00 = vc[0], G01 = 0.5f * vc[1], G11 = vc[2];
+  const float T00 = G00 * P00 + G01 * P01, T01 = G00 * P01 + G01 * P11;
+  const float T10 = G01 * P00 + G11 * P01, T11 = G01 * P01 + G11 * P11;
+  const float C00 = -(P00 * T00 + P01 * T10);
+  const float C01 = -(P00 * T01 + P01 * T11);
+  const float C11 = -(P01 * T01 + P11 * T11);
+  // dL/dSc = J^T C J
+  const float GJ0[3] = {C00 * J00, C01 * J11, C00 * J02 + C01 * J12};
+  const float GJ1[3] = {C01 * J00, C11 * J11, C01 * J02 + C11 * J12};
+  const float g[6] = {J00 * GJ0[0], J00 * GJ0[1], J00 * GJ0[2],
+                      J11 * GJ1[1], J11 * GJ1[2], J02 * GJ0[2] + J12 * GJ1[2]};
+  // dL/dJ = 2 C J Sc (entries 00, 02, 11, 12 are the ones J depends on)
+  const float GJm00 = 2.f * (C00 * JS0[0] + C01 * JS1[0]);
+  const float GJm02 = 2.f * (C00 * JS0[2] + C01 * JS1[2]);
+  const float GJm11 = 2.f * (C01 * JS0[1] + C11 * JS1[1]);
+  const float GJm12 = 2.f * (C01 * JS0[2] + C11 * JS1[2]);
+  float gpc0 = fx * rz * vm[0];
+  float gpc1 = fy * rz * vm[1];
+  float gpc2 = -(fx * x * vm[0] + fy * y * vm[1]) * rz2;
+  if (xr <= lim_x && xr >= -lim_x)
+    gpc0 += -fx * rz2 * GJm02;
+  else
+    gpc2 += -fx * rz3 * GJm02 * tx;
+  if (yr <= lim_y && yr >= -lim_y)
+    gpc1 += -fy * rz2 * GJm12;
+  else
+    gpc2 += -fy * rz3 * GJm12 * ty;
+  gpc2 += -fx * rz2 * GJm00 - fy * rz2 * GJm11 + 2.f * fx * tx * rz3 * GJm02 +
+          2.f * fy * ty * rz3 * GJm12;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) v_p[j] += R[0][j] * gpc0 + R[1][j] * gpc1 + R[2][j] * gpc2;
+  // dL/dSigma = R^T (dL/dSc) R
+  float U[3][3];  // (dL/dSc) R
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    U[0][j] = g[0] * R[0][j] + g[1] * R[1][j] + g[2] * R[2][j];
+    U[1][j] = g[1] * R[0][j] + g[3] * R[1][j] + g[4] * R[2][j];
+    U[2][j] = g[2] * R[0][j] + g[4] * R[1][j] + g[5] * R[2][j];
+  }
+  auto col = [&](int i, int j) { return R[0][i] * U[0][j] + R[1][i] * U[1][j] + R[2][i] * U[2][j]; };
+  vS[0] += col(0, 0);
+  vS[1] += col(0, 1);
+  vS[2] += col(0, 2);
+  vS[3] += col(1, 1);
+  vS[4] += col(1, 2);
+  vS[5] += col(2, 2);
+  return true;
+}
 // The 59 gradients (CACHE order) of touched row t, whose table row is `r`.
 __device__ __forceinline__ void tide_row_grads(
     uint32_t t, int32_t r, const int32_t* __restrict__ visit_base,
@@ -548,52 +657,45 @@ __device__ __forceinline__ void tide_row_grads(
 #pragma unroll
   for (int k = 0; k < 48; ++k) v_sh[k] = 0.f;
   float v_p[3] = {0.f, 0.f, 0.f};
-  m3 v_S;
-#pragma unroll
-  for (int i = 0; i < 3; ++i)
-#pragma unroll
-    for (int j = 0; j < 3; ++j) v_S.m[i][j] = 0.f;
+  const float S6[6] = {Sigma.m[0][0], Sigma.m[0][1], Sigma.m[0][2],
+                       Sigma.m[1][1], Sigma.m[1][2], Sigma.m[2][2]};
+  float vS[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float v_op = 0.f;
 
-  // visits in camera order = the set bits of the row's visibility mask; the
-  // render projection is recomputed (bit-identical to the forward's) instead
-  // of reading the conic and radius back from the splat records
+  // visits in camera order = the set bits of the row's visibility mask
   // (cameras in lockstep across the wavefront: LDS broadcasts of the camera,
-  // and the lanes seeing camera c read consecutive splat-gradient records)
+  // and the lanes seeing camera c read consecutive splat-gradient records).
+  // The splat records' colour gradients are already zero where the forward
+  // clamped the colour (clamp_min(SH + 0.5, 0)), so the SH colour itself is
+  // not re-evaluated.
   const uint32_t mask = masks[r];
   const int32_t* vis = visits + visit_base[t];
   int j = 0;
   for (uint32_t c = 0; c < n_cams; ++c) {
     if (!((mask >> c) & 1u)) continue;
     const uint32_t e = (uint32_t)vis[j++];
-    const ProjResult pr =
-        project_forward(p, Sigma, s_cam.cam[c], W, H, eps2d, near_plane, far_plane, radius_clip);
-    if (pr.radius <= 0) continue;  // culled by the render projection: zero gradient
     const float* g = splat_grads + (uint64_t)e * 9;
     const float vm[2] = {g[0], g[1]};
     const float vc[3] = {g[2], g[3], g[4]};
-    float vcol[3] = {g[5], g[6], g[7]};
+    const float vcol[3] = {g[5], g[6], g[7]};
     v_op += g[8];
-    // colour = clamp_min(SH + 0.5, 0): gradient passes where SH + 0.5 >= 0
+    if (!tide_visit_backward(p, S6, s_cam.cam[c], s_cam.lim[c][0], s_cam.lim[c][1], eps2d,
+                             near_plane, far_plane, vm, vc, v_p, vS))
+      continue;
     const float dx = p[0] - s_cam.campos[c][0], dy = p[1] - s_cam.campos[c][1],
                 dz = p[2] - s_cam.campos[c][2];
-    float col[3];
-    sh_eval3(sh_degree, dx, dy, dz, sh, col);
-#pragma unroll
-    for (int k = 0; k < 3; ++k) vcol[k] = (col[k] + 0.5f >= 0.f) ? vcol[k] : 0.f;
     float vdir[3];
-    sh_vjp3<true>(sh_degree, dx, dy, dz, sh, vcol, v_sh, true, vdir);
-    const float conic[3] = {pr.conic[0], pr.conic[1], pr.conic[2]};
-    ProjGrad pg;
-    project_backward(p, Sigma, s_cam.cam[c], W, H, eps2d, conic, 0.f, vm, 0.f, vc, false, 0.f,
-                     false, pg);
+    sh_vjp3<true, true>(sh_degree, dx, dy, dz, sh, vcol, v_sh, true, vdir);
 #pragma unroll
-    for (int k = 0; k < 3; ++k) v_p[k] += pg.v_p[k] + vdir[k];
-#pragma unroll
-    for (int i = 0; i < 3; ++i)
-#pragma unroll
-      for (int j = 0; j < 3; ++j) v_S.m[i][j] += pg.v_Sigma.m[i][j];
+    for (int k = 0; k < 3; ++k) v_p[k] += vdir[k];
   }
+  m3 v_S;
+  v_S.m[0][0] = vS[0];
+  v_S.m[0][1] = v_S.m[1][0] = vS[1];
+  v_S.m[0][2] = v_S.m[2][0] = vS[2];
+  v_S.m[1][1] = vS[3];
+  v_S.m[1][2] = v_S.m[2][1] = vS[4];
+  v_S.m[2][2] = vS[5];
   // Sigma(q_n, s) -> (v_qn, v_s); then the activation VJPs:
   // exp: v_logscale = v_s * s; normalize: v_q = (v_qn - (v_qn.qn) qn) / max(|q|, eps);
   // sigmoid: v_logit = v_op * o * (1 - o).
@@ -621,7 +723,7 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
     float radius_clip, int sh_degree, const float* __restrict__ splat_grads,
     float* __restrict__ grads, uint32_t grad_stride) {
   __shared__ CamLDS s_cam;
-  load_cams_lds(tc, s_cam);
+  load_cams_lds(tc, s_cam, W, H);
   __syncthreads();
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_touched) return;
@@ -672,7 +774,7 @@ __global__ void __launch_bounds__(FUSED_THREADS) tide_project_bwd_optim_kernel(
     float radius_clip, int sh_degree, const float* __restrict__ splat_grads, TideOptim O) {
   __shared__ CamLDS s_cam;
   __shared__ float s_g[FUSED_THREADS / 64][64 * FUSED_PITCH];
-  load_cams_lds(tc, s_cam);
+  load_cams_lds(tc, s_cam, W, H);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t t0 = blockIdx.x * blockDim.x + (uint32_t)wv * 64u;  // the wavefront's first row
