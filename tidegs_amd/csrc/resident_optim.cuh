@@ -126,13 +126,15 @@ struct BlockCache {
 // multiply-adds (b * m + (1 - b) * g with one rounding of the sum), and
 // contraction is otherwise off, so that every kernel that inlines this
 // update rounds identically.
-template <bool SOPHIA>
+// POW2_BS: batch_size is a power of two, so g / batch_size is exactly
+// g * (1 / batch_size) (both round the same exact value once).
+template <bool SOPHIA, bool POW2_BS = false>
 __device__ __forceinline__ void optim_update(float gv, float& mv, float& vv, float& pv, float sc,
                                              float dsc, float beta1, float beta2, float one_m_b1,
                                              float one_m_b2, float eps, float batch_size,
                                              float rho, int update_h) {
 #pragma clang fp contract(off)
-  const float gg = gv / batch_size;
+  const float gg = POW2_BS ? gv * (1.0f / batch_size) : gv / batch_size;
   mv = __builtin_fmaf(beta1, mv, one_m_b1 * gg);
   if (SOPHIA) {
     if (update_h) vv = __builtin_fmaf(beta2, vv, (one_m_b2 * gg) * gg);

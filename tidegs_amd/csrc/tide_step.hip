@@ -29,6 +29,8 @@
 // Resident table columns (TideGS CACHE order, storage/block_reader.py:35-44):
 //   xyz 0..2 | log-scale 3..5 | quat 6..9 (w,x,y,z) | opacity logit 10 | SH 11..58
 // with SH coefficient k, channel c at column 11 + 3k + c.
+#include <cmath>
+
 #include "projection.cuh"
 #include "raster.cuh"
 #include "resident_optim.cuh"
@@ -765,7 +767,7 @@ struct TideOptim {
   int* error_flag;
 };
 
-template <bool SOPHIA>
+template <bool SOPHIA, bool POW2_BS>
 __global__ void __launch_bounds__(FUSED_THREADS) tide_project_bwd_optim_kernel(
     uint32_t n_touched, const int32_t* __restrict__ touched,
     const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
@@ -847,7 +849,7 @@ __global__ void __launch_bounds__(FUSED_THREADS) tide_project_bwd_optim_kernel(
       if (u < k) {
         const uint32_t d = (uint32_t)(__builtin_amdgcn_readlane(my_row, u0 + u) - (int32_t)r_first);
         float m1 = mv[u], v1 = vv[u], p1 = pv[u];
-        optim_update<SOPHIA>(gv[u], m1, v1, p1, sc, dsc, O.beta1, O.beta2, one_m_b1, one_m_b2,
+        optim_update<SOPHIA, POW2_BS>(gv[u], m1, v1, p1, sc, dsc, O.beta1, O.beta2, one_m_b1, one_m_b2,
                              O.eps, O.batch_size, O.rho, O.update_h);
         tgs_bstore(act ? m1 : mv[u], rm, voff_s, d * (uint32_t)SB);
         tgs_bstore(act ? v1 : vv[u], rv, voff_s, d * (uint32_t)SB);
@@ -1151,15 +1153,20 @@ extern "C" int tgs_tide_project_bwd_update(
   O.update_h = update_hessian;
   O.state_pitch = (int)state_pitch;
   O.error_flag = error_flag;
-#define TIDE_FUSED_LAUNCH(SOPHIA)                                                              \
-  hipLaunchKernelGGL(tide_project_bwd_optim_kernel<SOPHIA>,                                     \
+#define TIDE_FUSED_LAUNCH(SOPHIA, POW2)                                                          \
+  hipLaunchKernelGGL((tide_project_bwd_optim_kernel<SOPHIA, POW2>),                              \
                      dim3(tgs_blocks(n_touched, FUSED_THREADS)), dim3(FUSED_THREADS), 0, stream, \
                      n_touched, touched, visit_base, visits, masks, tc, params, row_stride, W, H, \
                      eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads, O)
-  if (optimizer == 1)
-    TIDE_FUSED_LAUNCH(true);
-  else
-    TIDE_FUSED_LAUNCH(false);
+  int bs_exp = 0;
+  const bool pow2 = batch_size > 0.f && std::frexp(batch_size, &bs_exp) == 0.5f;
+  if (optimizer == 1) {
+    if (pow2) TIDE_FUSED_LAUNCH(true, true);
+    else TIDE_FUSED_LAUNCH(true, false);
+  } else {
+    if (pow2) TIDE_FUSED_LAUNCH(false, true);
+    else TIDE_FUSED_LAUNCH(false, false);
+  }
 #undef TIDE_FUSED_LAUNCH
   TGS_RETURN_LAUNCH(name);
 }
