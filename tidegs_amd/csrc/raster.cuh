@@ -145,7 +145,7 @@ struct StagedGeo {
 
 #define RS_COVER_QUAD 0.f  // bounded: the row intervals come from the quadratic
 #define RS_COVER_ALL 1.f   // no bound (degenerate conic, non-finite values): every pixel
-#define RS_COVER_NONE 2.f  // never visible (opacity <= 1/255)
+#define RS_COVER_NONE 2.f  // never visible (log2 opacity below the alpha threshold)
 
 template <int CDIM>
 __device__ __forceinline__ StagedGeo stage_geo(const SplatData<CDIM>& s) {
@@ -153,20 +153,24 @@ __device__ __forceinline__ StagedGeo stage_geo(const SplatData<CDIM>& s) {
   o.g0 = make_float4(s.x, s.y, -0.5f * RS_LOG2E * s.a, -RS_LOG2E * s.b);
   const float L = __builtin_amdgcn_logf(s.op);  // log2; -inf for 0, NaN for < 0
   o.g1 = make_float2(-0.5f * RS_LOG2E * s.c, s.op > 0.f ? L : -INFINITY);
-  // alpha >= 1/255 needs sigma <= t = ln(255 op).  On {0.5 d^T Q d <= t} the
-  // extents are |dx| <= sqrt(2 t c / det), |dy| <= sqrt(2 t a / det).
-  const float t = logf(255.f * s.op);
+  // alpha >= 1/255 needs sigma <= t = ln(255 op) = (L - log2(1/255)) ln 2,
+  // from the same L as the per-pixel test: t < 0 exactly when no pixel can
+  // pass it.  On {0.5 d^T Q d <= t} the extents are |dx| <= sqrt(2 t c / det),
+  // |dy| <= sqrt(2 t a / det); the hardware reciprocal and square root
+  // (1 ulp) sit far inside the 0.1 % + 1e-3 margins.
+  const float t = (L - RS_LOG2_MIN_ALPHA) * 0.6931471805599453f;
   const float det = s.a * s.c - s.b * s.b;
   o.cov = make_float4(0.f, 0.f, 0.f, RS_COVER_ALL);
-  if (!(s.op > 0.f) || t <= 0.f) {
+  if (!(s.op > 0.f) || !(t >= 0.f)) {
     o.box = make_float4(INFINITY, -INFINITY, INFINITY, -INFINITY);  // never visible
     o.cov.w = RS_COVER_NONE;
   } else if (!(det > 0.f) || !(s.a > 0.f) || !(s.c > 0.f)) {
     o.box = make_float4(-INFINITY, INFINITY, -INFINITY, INFINITY);  // no bound: never cull
   } else {
     const float tt = t * 1.001f + 1e-3f;  // conservative margin over rounding
-    const float ex = sqrtf(2.f * tt * s.c / det) * 1.001f + 1e-3f;
-    const float ey = sqrtf(2.f * tt * s.a / det) * 1.001f + 1e-3f;
+    const float rdet = __builtin_amdgcn_rcpf(det);
+    const float ex = __builtin_amdgcn_sqrtf(2.f * tt * s.c * rdet) * 1.001f + 1e-3f;
+    const float ey = __builtin_amdgcn_sqrtf(2.f * tt * s.a * rdet) * 1.001f + 1e-3f;
     o.box = make_float4(s.x - ex, s.x + ex, s.y - ey, s.y + ey);
     // cover_row: n = -2A > 0; delta bounds the rounding of the per-pixel
     // evaluation (three FMAs: < 3 ulp of the largest term, itself <= M on
