@@ -61,20 +61,70 @@ def profiled_traffic(kernel: str):
     return None
 
 
-# MI355X VALU issue: one wave64 instruction per clock per CU, 256 CUs at 2.4 GHz
-VALU_ISSUE_PER_S = 256 * 2.4e9
+SIMDS = 1024  # 256 CUs x 4 SIMDs
+XCDS = 8      # GRBM_GUI_ACTIVE sums the 8 XCDs' busy clocks
 
 
 def profiled_valu(kernel: str):
-    """Wave64 VALU instructions per launch of `kernel` at cfg3 from the committed
-    rocprofv3 SQ_INSTS_VALU summary (profiles/*_lds_atomics.md), or None."""
+    """VALU counters of one launch of `kernel` at cfg3 from the committed
+    rocprofv3 PMC summary (profiles/*_valu.md): SQ_INSTS_VALU (wave64
+    instructions), SQ_ACTIVE_INST_VALU (VALU quad-cycles summed over waves),
+    SQ_THREAD_CYCLES_VALU (active lanes x VALU instructions), GRBM_GUI_ACTIVE
+    and the launch's duration in that run, or None."""
     import re
 
-    for f in sorted((ROOT / "profiles").glob("*_lds_atomics.md")):
-        m = re.search(rf"^valu_insts_per_launch {re.escape(kernel)}: (\d+)", f.read_text(), re.M)
+    for f in sorted((ROOT / "profiles").glob("*_valu.md")):
+        m = re.search(rf"^valu_counters {re.escape(kernel)}: (.*)$", f.read_text(), re.M)
         if m:
-            return int(m.group(1))
+            return {k: float(v) for k, v in re.findall(r"(\w+)=([0-9.eE+-]+)", m.group(1))}
     return None
+
+
+def valu_peak(dev, blocks: int = 8192, iters: int = 4096) -> float:
+    """Wave64 VALU instructions per second of a synthetic stream of independent
+    FMAs (tgs_valu_probe: 8 * iters per wavefront, 4 wavefronts per block),
+    best of three timed launches: the VALU roofline's peak on this machine."""
+    import torch
+
+    from tidegs_amd import _native as N
+
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    s = N.stream_handle(dev)
+    N.call("tgs_valu_probe", N.ptr(out), blocks, 64, s)  # warm-up
+    best = float("inf")
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        N.call("tgs_valu_probe", N.ptr(out), blocks, iters, s)
+        b.record()
+        b.synchronize()
+        best = min(best, a.elapsed_time(b) * 1e-3)
+    return blocks * 4 * iters * 8 / best
+
+
+def valu_roofline(c: dict, live_pairs: int, event_ms: float, peak: float):
+    """The compositing kernels are bound by VALU issue, not HBM.  frac is the
+    SIMDs' VALU-busy share measured in the committed PMC pass (rocprof's
+    VALUBusy: 4 x SQ_ACTIVE_INST_VALU quad-cycles / (1024 SIMDs x XCD clock
+    cycles), clock = GRBM_GUI_ACTIVE / 8 / duration).  Beside it: the
+    profiled wave64 VALU instruction count over this run's event time, against
+    the rate of a full-exec FMA stream on this machine (valu_peak); the
+    compositing kernels' instruction mix issues faster than that stream, so
+    this ratio can exceed 1 and is not the fraction.  And the lane work per
+    live (Gaussian, pixel) pair (pairs counted by this run's forward)."""
+    cycles = c["GRBM_GUI_ACTIVE"] / XCDS
+    busy = 4.0 * c["SQ_ACTIVE_INST_VALU"] / (SIMDS * cycles)
+    rate = c["SQ_INSTS_VALU"] / (event_ms * 1e-3)
+    out = {"bound": "valu", "frac": round(busy, 4), "measure": "rocprof VALUBusy (PMC pass)",
+           "insts_per_launch": int(c["SQ_INSTS_VALU"]),
+           "profiled_clock_GHz": round(cycles / c["duration_ns"], 3),
+           "profiled_ms": round(c["duration_ns"] * 1e-6, 3),
+           "insts_per_s": round(rate / 1e9, 1) * 1e9, "fma_stream_insts_per_s": round(peak / 1e9, 1) * 1e9}
+    if live_pairs:
+        out["live_pairs"] = int(live_pairs)
+        out["lane_slots_per_live_pair"] = round(c["SQ_INSTS_VALU"] * 64 / live_pairs, 1)
+        out["active_lane_insts_per_live_pair"] = round(c["SQ_THREAD_CYCLES_VALU"] / live_pairs, 1)
+    return out
 
 
 def _host_cpu():
@@ -294,13 +344,11 @@ def bench_step(args, dev):
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(d["GBs"] / HBM_PEAK_GBS, 4),
                     "traffic": profiled_traffic(dominant) if default_cfg else None}
-        # the compositing kernels are limited by VALU issue, not HBM: the
-        # profiled instruction count over the issue rate is their floor
+        # the compositing kernels are limited by VALU issue, not HBM
         valu = profiled_valu(dominant) if default_cfg else None
         if valu:
-            floor_ms = valu / VALU_ISSUE_PER_S * 1e3
-            roofline["valu"] = {"insts_per_launch": valu, "issue_floor_ms": round(floor_ms, 3),
-                                "frac": round(floor_ms / d["ms"], 4)}
+            roofline["valu"] = valu_roofline(valu, getattr(ts, "last_live_pairs", 0), d["ms"],
+                                             valu_peak(dev))
     bwd_names = ("raster_bwd", "project_bwd", "project_bwd_update")
     bwd_ms = sum(kernels[k]["ms"] for k in bwd_names if k in kernels)
     bwd_bytes = sum(kernels[k]["bytes"] for k in bwd_names if k in kernels)
@@ -326,7 +374,8 @@ def bench_step(args, dev):
                    "touched_rows": stats.touched_rows, "isects": stats.n_isects,
                    "isects_per_tile": round(stats.n_isects / (C * ts.tw * ts.th), 1),
                    **_tile_load(ts, stats),
-                   "optimizer_update": "split" if args.split_update else "fused"},
+                   "optimizer_update": "split" if args.split_update else "fused",
+                   "live_pairs": int(getattr(ts, "last_live_pairs", 0))},
         "bwd_hbm_GBs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1) if bwd_ms else None,
         "roofline": roofline,
         "stage_ms": stage_ms,

@@ -37,6 +37,12 @@ int tgs_abi_version(void);
 const char* tgs_last_error(void);
 /* Zero/constant fill used instead of hipMemsetAsync (kernel node under capture). */
 int tgs_fill_u32(void* ptr, uint64_t n_words, uint32_t value, tgs_stream_t stream);
+/* Measurement aid with no counterpart in the reference: `blocks` workgroups of
+ * 256 threads each run `iters` rounds of 8 independent fused multiply-adds
+ * (8 * iters wave64 v_fma_f32 per wavefront) and store their sums to
+ * out[blocks * 256].  Timing it gives the VALU issue rate that the VALU
+ * roofline of the compositing kernels is quoted against. */
+int tgs_valu_probe(float* out, uint32_t blocks, uint32_t iters, tgs_stream_t stream);
 
 /* ---- projection ------------------------------------------------------- */
 /* Replaces fully_fused_projection_fwd_tensor
@@ -363,12 +369,16 @@ int tgs_tide_isect_ids(uint32_t n_isects, const uint32_t* keys, const int32_t* f
  * v_alphas [C,H,W] (dL/dalpha, nullable: zero).
  * The forward also zeroes clear[0..clear_words) (nullable; 16-byte aligned,
  * clear_words a multiple of 4), normally the backward's splat_grads: the
- * stores overlap the compositing instead of taking a pass of their own. */
+ * stores overlap the compositing instead of taking a pass of their own.
+ * n_contrib [C,H,W] (nullable) receives each pixel's number of composited
+ * Gaussians, the (Gaussian, pixel) pairs the backward replays; gsplat has no
+ * such output (a measurement aid). */
 int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const float* backgrounds, uint32_t W,
                            uint32_t H, uint32_t tile_width, uint32_t tile_height,
                            const int32_t* tile_offsets, const int32_t* flatten_ids,
                            uint32_t n_isects, float* images, float* alphas, int32_t* last_ids,
-                           float* clear, uint64_t clear_words, tgs_stream_t stream);
+                           int32_t* n_contrib, float* clear, uint64_t clear_words,
+                           tgs_stream_t stream);
 int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const float* backgrounds, uint32_t W,
                            uint32_t H, uint32_t tile_width, uint32_t tile_height,
                            const int32_t* tile_offsets, const int32_t* flatten_ids,

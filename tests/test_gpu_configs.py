@@ -181,7 +181,7 @@ def test_cfg4_city_hot_tiles(gpu):
     last = torch.zeros((H, W), dtype=torch.int32, device=gpu)
     s = N.stream_handle(gpu)
     N.call("tgs_tide_rasterize_fwd", 1, N.ptr(L["splats"]), None, W, H, tw, th, N.ptr(d_offs),
-           N.ptr(d_flat), r_flat.size, N.ptr(img), N.ptr(alp), N.ptr(last), None, 0, s)
+           N.ptr(d_flat), r_flat.size, N.ptr(img), N.ptr(alp), N.ptr(last), None, None, 0, s)
     pix = np.zeros((H, W), bool)
     for t in tiles:
         pix[(t // tw) * 16:(t // tw) * 16 + 16, (t % tw) * 16:(t % tw) * 16 + 16] = True

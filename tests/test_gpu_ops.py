@@ -389,3 +389,22 @@ def test_tide_loss_kernel(gpu, B, H, W):
         loss = 0.8 * sums[2 * bi] / n + 0.2 * (1 - sums[2 * bi + 1] / n)
         assert abs(loss - loss_ref) < 1e-6
         assert rel_l2(to_np(v[bi]).transpose(2, 0, 1), grad_ref) < 1e-5
+
+
+def test_valu_probe_sums(gpu):
+    """tgs_valu_probe (the VALU-rate measurement kernel) computes what it
+    claims: per thread, 8 chains a_k <- fma(a_k, x, x/2) from a_k = tid + k,
+    summed; against the same recurrence in float64 (fp32 rounding only)."""
+    from tidegs_amd import _native as N
+
+    blocks, iters, x = 3, 40, np.float32(0.999999)
+    announce(f"valu probe: {blocks} blocks x {iters} rounds")
+    out = torch.full((blocks * 256,), float("nan"), device=gpu)
+    N.call("tgs_valu_probe", N.ptr(out), blocks, iters, N.stream_handle(gpu))
+    torch.cuda.synchronize(gpu)
+    tid = np.arange(256, dtype=np.float64)
+    a = tid[:, None] + np.arange(8)[None, :]
+    for _ in range(iters):
+        a = a * float(x) + float(x) * 0.5
+    ref = np.tile(a.sum(1), blocks)
+    np.testing.assert_allclose(to_np(out), ref, rtol=1e-5)

@@ -30,6 +30,7 @@ SIGNATURES = {
     "tgs_abi_version": (ctypes.c_int, []),
     "tgs_last_error": (ctypes.c_char_p, []),
     "tgs_fill_u32": (ctypes.c_int, [P, U64, U32, P]),
+    "tgs_valu_probe": (ctypes.c_int, [P, U32, U32, P]),
     "tgs_fully_fused_projection_fwd": (
         ctypes.c_int,
         [U32, U32, P, P, P, P, P, P, I32, I32, F32, F32, F32, F32, P, P, P, P, P, P],
@@ -107,7 +108,7 @@ SIGNATURES = {
     "tgs_tide_offset_encode": (ctypes.c_int, [U32, P, U32, U32, U32, U32, P, P]),
     "tgs_tide_isect_ids": (ctypes.c_int, [U32, P, P, P, P, P]),
     "tgs_tide_rasterize_fwd": (
-        ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, U64, P]),
+        ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, P, U64, P]),
     "tgs_tide_rasterize_bwd": (
         ctypes.c_int, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, P, P, P, P]),
     "tgs_pack_splats": (ctypes.c_int, [U64, P, P, P, P, P, P]),

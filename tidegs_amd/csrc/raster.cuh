@@ -357,7 +357,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     RasterGeom G, Src src, const float* __restrict__ backgrounds,
     const int32_t* __restrict__ tile_offsets, const int32_t* __restrict__ flatten_ids,
     float* __restrict__ render_colors, float* __restrict__ render_alphas,
-    int32_t* __restrict__ last_ids, float4* __restrict__ clear = nullptr, uint64_t clear_n4 = 0) {
+    int32_t* __restrict__ last_ids, float4* __restrict__ clear = nullptr, uint64_t clear_n4 = 0,
+    int32_t* __restrict__ n_contrib = nullptr) {
   constexpr int BLOCK = TILE * TILE;
   constexpr int WAVES = BLOCK / 64;
   constexpr int ROWS = 64 / TILE;  // pixel rows per wavefront
@@ -405,6 +406,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
 
   float T = 1.f;
   uint32_t cur_idx = 0;
+  int32_t n_comp = 0;  // Gaussians composited into this pixel
   bool done = !inside;
   float pix[CDIM];
 #pragma unroll
@@ -461,6 +463,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
 #pragma unroll
               for (int k = 0; k < CDIM; ++k) pix[k] += s_col[t][k] * vis;
               cur_idx = (uint32_t)(batch_start + t);
+              ++n_comp;
               T = next_T;
             }
           }
@@ -476,6 +479,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
       render_colors[pid * CDIM + k] =
           backgrounds ? pix[k] + T * backgrounds[cam * CDIM + k] : pix[k];
     last_ids[pid] = (int32_t)cur_idx;
+    if (n_contrib) n_contrib[pid] = n_comp;
   }
 }
 

@@ -1068,7 +1068,8 @@ extern "C" int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const flo
                                       uint32_t tile_height, const int32_t* tile_offsets,
                                       const int32_t* flatten_ids, uint32_t n_isects,
                                       float* images, float* alphas, int32_t* last_ids,
-                                      float* clear, uint64_t clear_words, hipStream_t stream) {
+                                      int32_t* n_contrib, float* clear, uint64_t clear_words,
+                                      hipStream_t stream) {
   TGS_CHECK_ARG(clear_words % 4 == 0 && (clear_words == 0 || clear) &&
                     ((uintptr_t)clear & 15u) == 0,
                 "tide_rasterize_fwd: clear needs a 16-byte aligned buffer of 4k words");
@@ -1081,7 +1082,7 @@ extern "C" int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const flo
   hipLaunchKernelGGL((raster_fwd_kernel<3, 16, PackedSplats>), dim3(C, tile_height, tile_width),
                      dim3(256), 0, stream, G, PackedSplats{(const float4*)splats}, backgrounds,
                      tile_offsets, flatten_ids, images, alphas, last_ids, (float4*)clear,
-                     (uint64_t)clear_words / 4);
+                     (uint64_t)clear_words / 4, n_contrib);
   TGS_RETURN_LAUNCH("tgs_tide_rasterize_fwd");
 }
 

@@ -414,7 +414,7 @@ class _RasterizeToPixels(torch.autograd.Function):
             records = _packed_splats(means2d, conics, colors, opacities)
             N.call("tgs_tide_rasterize_fwd", C, N.ptr(records), N.ptr(backgrounds), width, height,
                    tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids), flatten_ids.numel(),
-                   N.ptr(render_colors), N.ptr(render_alphas), N.ptr(last_ids), None, 0,
+                   N.ptr(render_colors), N.ptr(render_alphas), N.ptr(last_ids), None, None, 0,
                    _stream())
         else:
             N.call("tgs_rasterize_to_pixels_fwd", C, ch, N.ptr(means2d), N.ptr(conics),

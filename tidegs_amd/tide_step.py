@@ -186,6 +186,7 @@ class TideStep:
         self._events = []
         self.stage_ms: Dict[str, float] = {}
         self.last_visible_entries = 0
+        self.last_live_pairs = 0  # composited (Gaussian, pixel) pairs of the last timed step
 
     # ---- stage timing (HIP events on the launch stream) ----------------------
     def _begin(self, name: str):
@@ -383,9 +384,12 @@ class TideStep:
         sg_words = (max(V, 1) * 9 + 3) // 4 * 4
         sgrads = self._buf("splat_grads", sg_words, torch.float32)
         self._begin("raster_fwd")
+        # with timing, also each pixel's composited-Gaussian count (the live
+        # (Gaussian, pixel) pairs the backward replays)
+        n_contrib = self._buf("n_contrib", C * H * W, torch.int32) if self._timing else None
         N.call("tgs_tide_rasterize_fwd", C, N.ptr(splats), N.ptr(bg), W, H, tw, th,
                N.ptr(offsets), N.ptr(fids), n_isects, N.ptr(images), N.ptr(alphas),
-               N.ptr(last_ids), N.ptr(sgrads), sg_words, s)
+               N.ptr(last_ids), N.ptr(n_contrib), N.ptr(sgrads), sg_words, s)
         self._end()
         sums = self._buf("loss_sums", 2 * C, torch.float64)
         v_images = self._buf("v_images", C * H * W * 3, torch.float32)
@@ -427,6 +431,7 @@ class TideStep:
             self._end()
         if self._timing:
             self.last_visible_entries = int((splats[: V * 12].view(-1, 12)[:, 7] > 0).sum())
+            self.last_live_pairs = int(n_contrib.sum(dtype=torch.int64))
         self.last = dict(masks=masks, entries=entries[:V], cam_offsets=cam_offsets,
                          touched=touched[:T], visit_base=visit_base[:T + 1], visits=visits[:V],
                          splats=splats[: V * 12].view(-1, 12),
