@@ -259,8 +259,10 @@ extern "C" int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, f
 #define TL_D1 (TL_T + 2 * SS_R)   // 42: dm region
 #define TL_D2 (TL_T + 4 * SS_R)   // 52: input region
 #define TL_THREADS (TL_T * TL_T)  // 1024
-#define TL_HQ_PITCH 53            // >= TL_D1, 2 x 53 = 42 (mod 64)
-#define TL_H2_PITCH 48            // >= TL_T, 2 x 48 = 32 (mod 64)
+#define TL_IN_PITCH 53            // >= TL_D2, odd
+#define TL_HQ_PITCH 53            // >= TL_D1, odd, 2 x 53 = 42 (mod 64)
+#define TL_DM_PITCH 43            // >= TL_D1, odd
+#define TL_H2_PITCH 49            // >= TL_T, odd
 
 __global__ void __launch_bounds__(TL_THREADS, 8) tide_loss_kernel(int H, int W,
                                                                const float* __restrict__ images_hwc,
@@ -269,19 +271,19 @@ __global__ void __launch_bounds__(TL_THREADS, 8) tide_loss_kernel(int H, int W,
                                                                float g_ssim, float g_l1,
                                                                float* __restrict__ v_images_hwc,
                                                                double* __restrict__ sums) {
-  // phase-aliased LDS: inputs -> dm maps, horizontal sums -> backward sums
+  // phase-aliased LDS: inputs -> dm maps, horizontal sums -> backward sums.
+  // The horizontal passes give consecutive lanes consecutive rows (odd row
+  // pitches: distinct banks); the vertical passes give them consecutive
+  // columns, and 2 x 53 = 42 (mod 64 banks) puts the forward vertical pass's
+  // second group of lanes (two rows down) on the banks the first leaves free.
   __shared__ union {
     struct {
-      float sx[TL_D2][TL_D2];
-      float sy[TL_D2][TL_D2];
+      float sx[TL_D2][TL_IN_PITCH];
+      float sy[TL_D2][TL_IN_PITCH];
     } in;
-    float sdm[3][TL_D1][TL_D1];
+    float sdm[3][TL_D1][TL_DM_PITCH];
   } su;
   __shared__ union {
-    // row pitches chosen for the vertical passes' reads: consecutive work
-    // items of a wavefront sit two rows apart, and 2 x pitch = 42 (hq) or
-    // 32 (h2) modulo 64 banks puts the wave's second group of lanes on the
-    // banks the first group leaves free
     float hq[5][TL_D2][TL_HQ_PITCH];
     float h2[3][TL_D1][TL_H2_PITCH];
   } sv;
@@ -340,9 +342,10 @@ __global__ void __launch_bounds__(TL_THREADS, 8) tide_loss_kernel(int H, int W,
       }
     }
     // horizontal pass of x, y, x^2, y^2, xy: 52 rows x 42 columns, three
-    // consecutive columns per work item (13 inputs; each product formed once)
+    // consecutive columns per work item (13 inputs; each product formed once),
+    // consecutive items on consecutive rows
     for (int o = tid; o < TL_D2 * (TL_D1 / 3); o += TL_THREADS) {
-      const int r = o / (TL_D1 / 3), cb = (o - r * (TL_D1 / 3)) * 3;
+      const int cb = (o / TL_D2) * 3, r = o - (o / TL_D2) * TL_D2;
       float u[13], w[13];
 #pragma unroll
       for (int t = 0; t < 13; ++t) {
@@ -423,9 +426,10 @@ __global__ void __launch_bounds__(TL_THREADS, 8) tide_loss_kernel(int H, int W,
       }
     }
     __syncthreads();
-    // backward: horizontal pass (42 rows x 32 columns), two columns per item ...
+    // backward: horizontal pass (42 rows x 32 columns), two columns per item,
+    // consecutive items on consecutive rows ...
     for (int o = tid; o < TL_D1 * (TL_T / 2); o += TL_THREADS) {
-      const int r = o / (TL_T / 2), cb = (o - r * (TL_T / 2)) * 2;
+      const int cb = (o / TL_D1) * 2, r = o - (o / TL_D1) * TL_D1;
 #pragma unroll
       for (int m = 0; m < 3; ++m) {
         float v[12];
