@@ -347,6 +347,20 @@ __device__ __forceinline__ void lane_bits(const uint32_t* half, int n_list, int 
 }
 
 // ---------------------------------------------------------------------------
+// Workgroup order.  Workgroups start in linear-id order (x fastest) and go to
+// the 8 XCDs round-robin.  Both kernels take one camera at a time, so the
+// concurrent workgroups read one camera's splat records (which fit the
+// last-level cache); within the camera the forward walks tiles row-major and
+// the backward column-major, the faster order of each measured on the cfg3
+// and cfg4 scenes (forward 4.64 -> 4.28 ms, backward 10.66 -> 10.18 ms at
+// cfg3 against camera-fastest).
+//   forward grid  (tile_w, tile_h, C)
+//   backward grid (tile_h, tile_w, C)
+// ---------------------------------------------------------------------------
+inline dim3 raster_fwd_grid(const RasterGeom& G) { return dim3(G.tile_w, G.tile_h, G.C); }
+inline dim3 raster_bwd_grid(const RasterGeom& G) { return dim3(G.tile_h, G.tile_w, G.C); }
+
+// ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
 #define RF_BATCH 128  // Gaussians staged per batch
@@ -368,7 +382,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     // compositing keeps the vector units busy; each workgroup stores its own
     // slice of clear_n4 16-byte words.
     const uint64_t groups = (uint64_t)gridDim.x * gridDim.y * gridDim.z;
-    const uint64_t g = ((uint64_t)blockIdx.x * gridDim.y + blockIdx.y) * gridDim.z + blockIdx.z;
+    const uint64_t g = ((uint64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
     const uint64_t per = (clear_n4 + groups - 1) / groups;
     const uint64_t end = min(clear_n4, (g + 1) * per);
     for (uint64_t w = g * per + threadIdx.x; w < end; w += BLOCK)
@@ -383,8 +397,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
   __shared__ uint8_t s_list[WAVES][BATCH];
   __shared__ __align__(16) uint32_t s_emh[WAVES][2][BATCH];
 
-  const uint32_t cam = blockIdx.x;
-  const uint32_t ty = blockIdx.y, tx = blockIdx.z;
+  const uint32_t cam = blockIdx.z;
+  const uint32_t ty = blockIdx.y, tx = blockIdx.x;
   const uint32_t tile_id = ty * G.tile_w + tx;
   const uint32_t tr = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane((int)(tr >> 6));  // wave-uniform
@@ -554,8 +568,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   __shared__ float s_stage[WAVES][32 * (Sink::MAY_ABS ? NA : NV)];  // one owner group's values
   __shared__ int32_t s_gid[WAVES][32];            // and their Gaussian ids
 
-  const uint32_t cam = blockIdx.x;
-  const uint32_t ty = blockIdx.y, tx = blockIdx.z;
+  const uint32_t cam = blockIdx.z;
+  const uint32_t ty = blockIdx.x, tx = blockIdx.y;
   const uint32_t tile_id = ty * G.tile_w + tx;
   const uint32_t tr = threadIdx.x;
   static_assert(BATCH == 64, "one list entry per lane");

@@ -13,9 +13,8 @@ template <int CDIM, int TILE>
 static void launch_fwd(const RasterGeom& G, const SoASplats<CDIM>& src, const float* bg,
                        const int32_t* offsets, const int32_t* flat, float* colors, float* alphas,
                        int32_t* last, hipStream_t s) {
-  hipLaunchKernelGGL((raster_fwd_kernel<CDIM, TILE, SoASplats<CDIM>>),
-                     dim3(G.C, G.tile_h, G.tile_w), dim3(TILE * TILE), 0, s, G, src, bg, offsets,
-                     flat, colors, alphas, last);
+  hipLaunchKernelGGL((raster_fwd_kernel<CDIM, TILE, SoASplats<CDIM>>), raster_fwd_grid(G),
+                     dim3(TILE * TILE), 0, s, G, src, bg, offsets, flat, colors, alphas, last);
 }
 
 template <int CDIM, int TILE>
@@ -24,8 +23,8 @@ static void launch_bwd(const RasterGeom& G, const SoASplats<CDIM>& src, const So
                        const float* alphas, const int32_t* last, const float* v_colors,
                        const float* v_alphas, hipStream_t s) {
   hipLaunchKernelGGL((raster_bwd_kernel<CDIM, TILE, SoASplats<CDIM>, SoAGrads<CDIM>>),
-                     dim3(G.C, G.tile_h, G.tile_w), dim3(TILE * TILE), 0, s, G, src, dst, bg,
-                     offsets, flat, alphas, last, v_colors, v_alphas);
+                     raster_bwd_grid(G), dim3(TILE * TILE), 0, s, G, src, dst, bg, offsets, flat,
+                     alphas, last, v_colors, v_alphas);
 }
 
 template <int CDIM>
@@ -87,6 +86,8 @@ extern "C" int tgs_rasterize_to_pixels_fwd(
                 "rasterize_to_pixels_fwd: null splat pointer");
   TGS_CHECK_ARG(tile_width * tile_size >= image_width && tile_height * tile_size >= image_height,
                 "rasterize_to_pixels_fwd: tile grid does not cover the image");
+  TGS_CHECK_ARG(C <= 65535 && tile_width <= 65535 && tile_height <= 65535,
+                "rasterize_to_pixels_fwd: at most 65535 cameras and tiles per image side");
   const RasterGeom G{C, image_width, image_height, tile_width, tile_height, n_isects};
 #define TGS_FWD_CASE(D)                                                                      \
   case D:                                                                                    \
@@ -117,6 +118,8 @@ extern "C" int tgs_rasterize_to_pixels_bwd(
                 "rasterize_to_pixels_bwd: null pointer");
   TGS_CHECK_ARG(tile_width * tile_size >= image_width && tile_height * tile_size >= image_height,
                 "rasterize_to_pixels_bwd: tile grid does not cover the image");
+  TGS_CHECK_ARG(C <= 65535 && tile_width <= 65535 && tile_height <= 65535,
+                "rasterize_to_pixels_bwd: at most 65535 cameras and tiles per image side");
   const RasterGeom G{C, image_width, image_height, tile_width, tile_height, n_isects};
 #define TGS_BWD_CASE(D)                                                                         \
   case D:                                                                                       \

@@ -1078,9 +1078,11 @@ extern "C" int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const flo
   TGS_CHECK_ARG(tile_offsets && images && alphas && last_ids, "tide_rasterize_fwd: null");
   TGS_CHECK_ARG(n_isects == 0 || (splats && flatten_ids), "tide_rasterize_fwd: null splats");
   TGS_CHECK_ARG(tile_width * 16 >= W && tile_height * 16 >= H, "tide_rasterize_fwd: tile grid");
+  TGS_CHECK_ARG(C <= 65535 && tile_width <= 65535 && tile_height <= 65535,
+                "tide_rasterize_fwd: at most 65535 cameras and tiles per image side");
   const RasterGeom G{C, W, H, tile_width, tile_height, n_isects};
-  hipLaunchKernelGGL((raster_fwd_kernel<3, 16, PackedSplats>), dim3(C, tile_height, tile_width),
-                     dim3(256), 0, stream, G, PackedSplats{(const float4*)splats}, backgrounds,
+  hipLaunchKernelGGL((raster_fwd_kernel<3, 16, PackedSplats>), raster_fwd_grid(G), dim3(256), 0,
+                     stream, G, PackedSplats{(const float4*)splats}, backgrounds,
                      tile_offsets, flatten_ids, images, alphas, last_ids, (float4*)clear,
                      (uint64_t)clear_words / 4, n_contrib);
   TGS_RETURN_LAUNCH("tgs_tide_rasterize_fwd");
@@ -1098,9 +1100,11 @@ extern "C" int tgs_tide_rasterize_bwd(uint32_t C, const float* splats, const flo
                     splat_grads,
                 "tide_rasterize_bwd: null");
   TGS_CHECK_ARG(tile_width * 16 >= W && tile_height * 16 >= H, "tide_rasterize_bwd: tile grid");
+  TGS_CHECK_ARG(C <= 65535 && tile_width <= 65535 && tile_height <= 65535,
+                "tide_rasterize_bwd: at most 65535 cameras and tiles per image side");
   const RasterGeom G{C, W, H, tile_width, tile_height, n_isects};
-  hipLaunchKernelGGL((raster_bwd_kernel<3, 16, PackedSplats, PackedGrads>),
-                     dim3(C, tile_height, tile_width), dim3(256), 0, stream, G,
+  hipLaunchKernelGGL((raster_bwd_kernel<3, 16, PackedSplats, PackedGrads>), raster_bwd_grid(G),
+                     dim3(256), 0, stream, G,
                      PackedSplats{(const float4*)splats}, PackedGrads{splat_grads}, backgrounds,
                      tile_offsets, flatten_ids, alphas, last_ids, v_images, v_alphas);
   TGS_RETURN_LAUNCH("tgs_tide_rasterize_bwd");
