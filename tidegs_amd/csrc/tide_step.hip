@@ -637,13 +637,16 @@ __device__ __forceinline__ bool tide_visit_backward(const float p[3], const floa
   vS[5] += col(2, 2);
   return true;
 }
-// The 59 gradients (CACHE order) of touched row t, whose table row is `r`.
+// The 59 gradients (CACHE order) of touched row t, whose table row is `r`,
+// into out[0..58], the lane's own LDS row.  The row's SH coefficients are
+// staged in out[11..58] and read from there by the visit loop (48 fewer
+// registers), then overwritten by their gradients.
 __device__ __forceinline__ void tide_row_grads(
     uint32_t t, int32_t r, const int32_t* __restrict__ visit_base,
     const int32_t* __restrict__ visits, const uint32_t* __restrict__ masks, const CamLDS& s_cam,
     uint32_t n_cams, const float* params, uint32_t row_stride, int W, int H, float eps2d,
     float near_plane, float far_plane, float radius_clip, int sh_degree,
-    const float* __restrict__ splat_grads, float out[TIDE_ROW]) {
+    const float* __restrict__ splat_grads, float* out) {
   const float* row = params + (uint64_t)r * row_stride;
   const float p[3] = {row[0], row[1], row[2]};
   const float s[3] = {expf(row[3]), expf(row[4]), expf(row[5])};
@@ -651,9 +654,9 @@ __device__ __forceinline__ void tide_row_grads(
   normalize4(row + 6, qn, qinv);
   const m3 Sigma = covar_from_quat_scale(qn, s);
   const float opac = sigmoidf_(row[10]);
-  float sh[48];
+  const float* sh = out + 11;
 #pragma unroll
-  for (int k = 0; k < 48; ++k) sh[k] = row[11 + k];
+  for (int k = 0; k < 48; ++k) out[11 + k] = row[11 + k];
 
   float v_sh[48];
 #pragma unroll
@@ -686,6 +689,8 @@ __device__ __forceinline__ void tide_row_grads(
       continue;
     const float dx = p[0] - s_cam.campos[c][0], dy = p[1] - s_cam.campos[c][1],
                 dz = p[2] - s_cam.campos[c][2];
+    // the parked coefficients are read per visit, not hoisted into registers
+    asm volatile("" ::: "memory");
     float vdir[3];
     sh_vjp3<true, true>(sh_degree, dx, dy, dz, sh, vcol, v_sh, true, vdir);
 #pragma unroll
@@ -717,6 +722,10 @@ __device__ __forceinline__ void tide_row_grads(
   for (int k = 0; k < 48; ++k) out[11 + k] = v_sh[k];
 }
 
+// Odd LDS pitch of a parked row: accesses with lane = row and with lane =
+// column are both free of bank conflicts.
+#define ROW_PITCH 59
+
 __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
     uint32_t n_touched, const int32_t* __restrict__ touched,
     const int32_t* __restrict__ visit_base, const int32_t* __restrict__ visits,
@@ -725,18 +734,29 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
     float radius_clip, int sh_degree, const float* __restrict__ splat_grads,
     float* __restrict__ grads, uint32_t grad_stride) {
   __shared__ CamLDS s_cam;
+  __shared__ float s_g[4][64 * ROW_PITCH];
   load_cams_lds(tc, s_cam, W, H);
-  __syncthreads();
-  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_touched) return;
-  float g[TIDE_ROW];
-  tide_row_grads(t, touched[t], visit_base, visits, masks, s_cam, tc.C, params, row_stride, W, H,
-                 eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads, g);
-  float* out = grads + (uint64_t)t * grad_stride;
-#pragma unroll
-  for (int k = 0; k < TIDE_ROW; ++k) out[k] = g[k];
-  // zero the padding of a padded row so that the whole row is written
-  for (uint32_t k = TIDE_ROW; k < grad_stride; ++k) out[k] = 0.f;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t t0 = blockIdx.x * blockDim.x + (uint32_t)wv * 64u;  // the wavefront's first row
+  const uint32_t t = t0 + (uint32_t)lane;
+  float* sg = s_g[wv];
+  if (t < n_touched)
+    tide_row_grads(t, touched[t], visit_base, visits, masks, s_cam, tc.C, params, row_stride, W,
+                   H, eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads,
+                   sg + lane * ROW_PITCH);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (t0 >= n_touched) return;
+  const int n_w = n_touched - t0 < 64u ? (int)(n_touched - t0) : 64;
+  // row by row with lane = column; the padding of a padded row is zeroed so
+  // that the whole row is written
+  for (int u = 0; u < n_w; ++u) {
+    float* out = grads + (uint64_t)(t0 + u) * grad_stride;
+    for (uint32_t k = lane; k < grad_stride; k += 64)
+      out[k] = k < TIDE_ROW ? sg[u * ROW_PITCH + k] : 0.f;
+  }
 }
 
 // Projection backward fused with the resident optimizer update of the same
@@ -750,9 +770,8 @@ __global__ void __launch_bounds__(256) tide_project_bwd_kernel(
 // tgs_resident_adam_step / tgs_resident_sophia_step).  Rows are unique, so a
 // row's parameters are read (phase 1) and written (phase 2) by one
 // wavefront only.
-#define FUSED_PITCH 61  // odd LDS pitch: both phases' accesses are conflict-free
 #define FUSED_ROWS 32   // rows in flight per wavefront in phase 2
-#define FUSED_THREADS 128  // two wavefronts per workgroup
+#define FUSED_THREADS 64  // one wavefront per workgroup: 17.8 KB of LDS, 9 per CU
 
 struct TideOptim {
   OptimLayout L;
@@ -775,7 +794,7 @@ __global__ void __launch_bounds__(FUSED_THREADS) tide_project_bwd_optim_kernel(
     uint32_t row_stride, int W, int H, float eps2d, float near_plane, float far_plane,
     float radius_clip, int sh_degree, const float* __restrict__ splat_grads, TideOptim O) {
   __shared__ CamLDS s_cam;
-  __shared__ float s_g[FUSED_THREADS / 64][64 * FUSED_PITCH];
+  __shared__ float s_g[FUSED_THREADS / 64][64 * ROW_PITCH];
   load_cams_lds(tc, s_cam, W, H);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -785,11 +804,9 @@ __global__ void __launch_bounds__(FUSED_THREADS) tide_project_bwd_optim_kernel(
   int32_t my_row = 0;
   if (t < n_touched) {
     my_row = touched[t];
-    float g[TIDE_ROW];
     tide_row_grads(t, my_row, visit_base, visits, masks, s_cam, tc.C, params, row_stride, W, H,
-                   eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads, g);
-#pragma unroll
-    for (int k = 0; k < TIDE_ROW; ++k) sg[lane * FUSED_PITCH + k] = g[k];
+                   eps2d, near_plane, far_plane, radius_clip, sh_degree, splat_grads,
+                   sg + lane * ROW_PITCH);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -838,7 +855,7 @@ __global__ void __launch_bounds__(FUSED_THREADS) tide_project_bwd_optim_kernel(
     for (int u = 0; u < FUSED_ROWS; ++u) {
       if (u < k) {
         const uint32_t d = (uint32_t)(__builtin_amdgcn_readlane(my_row, u0 + u) - (int32_t)r_first);
-        gv[u] = act ? sg[(u0 + u) * FUSED_PITCH + lane] : 0.f;
+        gv[u] = act ? sg[(u0 + u) * ROW_PITCH + lane] : 0.f;
         mv[u] = tgs_bload(rm, voff_s, d * (uint32_t)SB);
         vv[u] = tgs_bload(rv, voff_s, d * (uint32_t)SB);
         pv[u] = tgs_bload(rp, voff_p, d * (uint32_t)PB);
