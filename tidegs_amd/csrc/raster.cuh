@@ -560,6 +560,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   __shared__ uint8_t s_list[WAVES][BATCH];
   __shared__ float4 s_box[BATCH];
   __shared__ float4 s_cov[BATCH];
+  __shared__ int32_t s_bin_max[WAVES];
   __shared__ float2 s_pair[WAVES][RB_PAIRS];  // (alpha T, v_sigma)
   __shared__ __align__(16) uint32_t s_emh[WAVES][2][BATCH];  // pixel mask halves of each list entry
   // first pair slot of each list entry's half: [0][li] that of lanes 0..31
@@ -591,7 +592,6 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   const int32_t range_end = (cam == G.C - 1 && tile_id == G.tile_w * G.tile_h - 1)
                                 ? (int32_t)G.n_isects
                                 : offs[tile_id + 1];
-  const int32_t n_batches = (range_end - range_start + BATCH - 1) / BATCH;
 
   const float T_final = 1.f - render_alphas[pid];
   float T = T_final;
@@ -614,6 +614,16 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   const float tf_term = T_final * v_ra - T_final * bg_dot;
   const int32_t bin_final = inside ? last_ids[pid] : -1;
   const int32_t wave_bin_final = tgs_wave_max_i32(bin_final);
+  // entries behind the tile's last contributor (any pixel's last_id) touch no
+  // pixel: the back-to-front walk starts at the last one
+  if (lane == 0) s_bin_max[wave] = wave_bin_final;
+  __syncthreads();
+  int32_t tile_bin_final = s_bin_max[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) tile_bin_final = max(tile_bin_final, s_bin_max[w]);
+  const int32_t live_end = min(range_end, tile_bin_final + 1);
+  const int32_t n_batches =
+      live_end > range_start ? (live_end - range_start + BATCH - 1) / BATCH : 0;
   const bool absg = sink.absgrad();
   const int nval = absg ? NA : NV;
   // owner role within a group of 32 entries: entry oe, pixel bits [32 oh, 32 oh + 32)
@@ -621,7 +631,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
 
   for (int32_t b = 0; b < n_batches; ++b) {
     __syncthreads();
-    const int32_t batch_end = range_end - 1 - BATCH * b;
+    const int32_t batch_end = live_end - 1 - BATCH * b;
     const int32_t batch_size = min(BATCH, batch_end + 1 - range_start);
     const int32_t idx = batch_end - (int32_t)tr;
     const bool have = (int)tr < BATCH && idx >= range_start;
