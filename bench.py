@@ -80,22 +80,29 @@ def profiled_valu(kernel: str):
     return None
 
 
-def valu_peak(dev, blocks: int = 8192, iters: int = 4096) -> float:
-    """Wave64 VALU instructions per second of a synthetic stream of independent
-    FMAs (tgs_valu_probe: 8 * iters per wavefront, 4 wavefronts per block),
-    best of three timed launches: the VALU roofline's peak on this machine."""
+# tgs_valu_probe's instruction forms, in its `form` order
+VALU_FORMS = ("mul_f32_vgpr", "mul_f32_sgpr", "add_u32_vgpr", "xor_b32_sgpr", "fma_f32_vgpr",
+              "exp_f32")
+
+
+def valu_peak(dev, blocks: int = 8192, iters: int = 4096, form: int = 0) -> float:
+    """Wave64 VALU instructions per second of a synthetic stream of one
+    instruction form (tgs_valu_probe: 8 * iters per wavefront, 4 wavefronts
+    per block), best of three timed launches.  Form 0, two-source FP32
+    multiplies on VGPRs, is the fastest VALU issue rate on this machine: the
+    VALU roofline's peak."""
     import torch
 
     from tidegs_amd import _native as N
 
     out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
     s = N.stream_handle(dev)
-    N.call("tgs_valu_probe", N.ptr(out), blocks, 64, s)  # warm-up
+    N.call("tgs_valu_probe", N.ptr(out), blocks, 64, form, s)  # warm-up
     best = float("inf")
     for _ in range(3):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        N.call("tgs_valu_probe", N.ptr(out), blocks, iters, s)
+        N.call("tgs_valu_probe", N.ptr(out), blocks, iters, form, s)
         b.record()
         b.synchronize()
         best = min(best, a.elapsed_time(b) * 1e-3)
@@ -103,23 +110,28 @@ def valu_peak(dev, blocks: int = 8192, iters: int = 4096) -> float:
 
 
 def valu_roofline(c: dict, live_pairs: int, event_ms: float, peak: float):
-    """The compositing kernels are bound by VALU issue, not HBM.  frac is the
-    SIMDs' VALU-busy share measured in the committed PMC pass (rocprof's
-    VALUBusy: 4 x SQ_ACTIVE_INST_VALU quad-cycles / (1024 SIMDs x XCD clock
-    cycles), clock = GRBM_GUI_ACTIVE / 8 / duration).  Beside it: the
-    profiled wave64 VALU instruction count over this run's event time, against
-    the rate of a full-exec FMA stream on this machine (valu_peak); the
-    compositing kernels' instruction mix issues faster than that stream, so
-    this ratio can exceed 1 and is not the fraction.  And the lane work per
-    live (Gaussian, pixel) pair (pairs counted by this run's forward)."""
+    """The compositing kernels are bound by instruction issue, not HBM.  frac =
+    the kernel's VALU issue rate (the committed PMC pass's wave64 VALU
+    instruction count per launch over this run's event time) / the fastest
+    VALU issue rate on this machine (valu_peak: two-source FP32 on VGPRs).
+    On gfx950 the issue rate depends on the instruction form: integer and
+    bit operations, operands in SGPRs or literals, and three-source FMAs
+    issue about half as often as that stream, transcendentals a quarter as
+    often; so a kernel's own issue limit lies below the peak and frac
+    understates how close it is to it.  Beside it: rocprof's VALU busy on a
+    four-cycles-per-instruction basis (4 x SQ_ACTIVE_INST_VALU / (1024 SIMDs x
+    XCD clock cycles), which exceeds 1 for two-cycle forms), and the lane
+    work per live (Gaussian, pixel) pair (pairs counted by this run's forward)."""
     cycles = c["GRBM_GUI_ACTIVE"] / XCDS
     busy = 4.0 * c["SQ_ACTIVE_INST_VALU"] / (SIMDS * cycles)
     rate = c["SQ_INSTS_VALU"] / (event_ms * 1e-3)
-    out = {"bound": "valu", "frac": round(busy, 4), "measure": "rocprof VALUBusy (PMC pass)",
+    out = {"bound": "valu", "frac": round(rate / peak, 4),
+           "measure": "VALU issue rate / two-source FP32 VGPR stream (tgs_valu_probe)",
            "insts_per_launch": int(c["SQ_INSTS_VALU"]),
+           "insts_per_s": round(rate / 1e9, 1) * 1e9, "peak_insts_per_s": round(peak / 1e9, 1) * 1e9,
+           "busy_4cycle_basis": round(busy, 4),
            "profiled_clock_GHz": round(cycles / c["duration_ns"], 3),
-           "profiled_ms": round(c["duration_ns"] * 1e-6, 3),
-           "insts_per_s": round(rate / 1e9, 1) * 1e9, "fma_stream_insts_per_s": round(peak / 1e9, 1) * 1e9}
+           "profiled_ms": round(c["duration_ns"] * 1e-6, 3)}
     if live_pairs:
         out["live_pairs"] = int(live_pairs)
         out["lane_slots_per_live_pair"] = round(c["SQ_INSTS_VALU"] * 64 / live_pairs, 1)
@@ -347,8 +359,11 @@ def bench_step(args, dev):
         # the compositing kernels are limited by VALU issue, not HBM
         valu = profiled_valu(dominant) if default_cfg else None
         if valu:
+            rates = {name: valu_peak(dev, form=f) for f, name in enumerate(VALU_FORMS)}
             roofline["valu"] = valu_roofline(valu, getattr(ts, "last_live_pairs", 0), d["ms"],
-                                             valu_peak(dev))
+                                             rates[VALU_FORMS[0]])
+            roofline["valu"]["form_insts_per_s"] = {k: round(v / 1e9, 1) * 1e9
+                                                    for k, v in rates.items()}
     bwd_names = ("raster_bwd", "project_bwd", "project_bwd_update")
     bwd_ms = sum(kernels[k]["ms"] for k in bwd_names if k in kernels)
     bwd_bytes = sum(kernels[k]["bytes"] for k in bwd_names if k in kernels)

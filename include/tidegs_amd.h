@@ -38,11 +38,15 @@ const char* tgs_last_error(void);
 /* Zero/constant fill used instead of hipMemsetAsync (kernel node under capture). */
 int tgs_fill_u32(void* ptr, uint64_t n_words, uint32_t value, tgs_stream_t stream);
 /* Measurement aid with no counterpart in the reference: `blocks` workgroups of
- * 256 threads each run `iters` rounds of 8 independent fused multiply-adds
- * (8 * iters wave64 v_fma_f32 per wavefront) and store their sums to
- * out[blocks * 256].  Timing it gives the VALU issue rate that the VALU
- * roofline of the compositing kernels is quoted against. */
-int tgs_valu_probe(float* out, uint32_t blocks, uint32_t iters, tgs_stream_t stream);
+ * 256 threads each run `iters` rounds of 8 independent operations of one
+ * instruction form (8 * iters wave64 VALU instructions per wavefront) and
+ * store their sums to out[blocks * 256].  form 0: v_mul_f32 on VGPRs (the
+ * fastest-issuing form: its rate is the peak the compositing kernels' VALU
+ * roofline is quoted against); 1: v_mul_f32 with an SGPR operand; 2:
+ * v_add_u32 on VGPRs; 3: v_xor_b32 with an SGPR operand; 4: v_fma_f32 on
+ * VGPRs; 5: v_exp_f32. */
+int tgs_valu_probe(float* out, uint32_t blocks, uint32_t iters, int32_t form,
+                   tgs_stream_t stream);
 
 /* ---- projection ------------------------------------------------------- */
 /* Replaces fully_fused_projection_fwd_tensor

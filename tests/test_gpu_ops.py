@@ -391,20 +391,42 @@ def test_tide_loss_kernel(gpu, B, H, W):
         assert rel_l2(to_np(v[bi]).transpose(2, 0, 1), grad_ref) < 1e-5
 
 
-def test_valu_probe_sums(gpu):
+@pytest.mark.parametrize("form", [0, 1, 2, 3, 4, 5])
+def test_valu_probe_sums(gpu, form):
     """tgs_valu_probe (the VALU-rate measurement kernel) computes what it
-    claims: per thread, 8 chains a_k <- fma(a_k, x, x/2) from a_k = tid + k,
-    summed; against the same recurrence in float64 (fp32 rounding only)."""
+    claims, per thread 8 chains from a_k = tid + k (u_k = 7 tid + k), summed,
+    against the same recurrences in float64 / integers: 0 a_k <- a_k z with
+    z = x - (tid mod 64) 1e-9 in float32; 1 a_k <- a_k x; 2 u_k <- u_k + 3 tid
+    + 1 (low 16 bits summed); 3 u_k <- u_k ^ bits(x); 4 a_k <- fma(a_k, z, y),
+    y = (tid mod 64) 1e-9; 5 a_k <- 2^-a_k from a_k = k / 10."""
     from tidegs_amd import _native as N
 
     blocks, iters, x = 3, 40, np.float32(0.999999)
-    announce(f"valu probe: {blocks} blocks x {iters} rounds")
+    announce(f"valu probe form {form}: {blocks} blocks x {iters} rounds")
     out = torch.full((blocks * 256,), float("nan"), device=gpu)
-    N.call("tgs_valu_probe", N.ptr(out), blocks, iters, N.stream_handle(gpu))
+    N.call("tgs_valu_probe", N.ptr(out), blocks, iters, form, N.stream_handle(gpu))
     torch.cuda.synchronize(gpu)
-    tid = np.arange(256, dtype=np.float64)
-    a = tid[:, None] + np.arange(8)[None, :]
-    for _ in range(iters):
-        a = a * float(x) + float(x) * 0.5
+    tid = np.arange(256)
+    lane = (tid % 64).astype(np.float32)
+    z = (x - lane * np.float32(1e-9)).astype(np.float64)
+    y = (lane * np.float32(1e-9)).astype(np.float64)
+    a = (tid[:, None] + np.arange(8)[None, :]).astype(np.float64)
+    u = tid[:, None] * 7 + np.arange(8)[None, :]  # int64: no wrap at these sizes
+    if form == 0:
+        a = a * z[:, None] ** iters
+    elif form == 1:
+        a = a * float(x) ** iters
+    elif form == 2:
+        a = ((u + iters * (3 * tid[:, None] + 1)) & 0xffff).astype(np.float64)
+    elif form == 3:
+        bits = int(np.float32(x).view(np.uint32))
+        a = ((u ^ bits if iters % 2 else u) & 0xffff).astype(np.float64)
+    elif form == 4:
+        for _ in range(iters):
+            a = a * z[:, None] + y[:, None]
+    else:
+        a = np.tile(np.arange(8) * 0.1, (256, 1))
+        for _ in range(iters):
+            a = 2.0 ** -a
     ref = np.tile(a.sum(1), blocks)
-    np.testing.assert_allclose(to_np(out), ref, rtol=1e-5)
+    np.testing.assert_allclose(to_np(out), ref, rtol=1e-4 if form == 5 else 1e-5)

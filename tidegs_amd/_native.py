@@ -30,7 +30,7 @@ SIGNATURES = {
     "tgs_abi_version": (ctypes.c_int, []),
     "tgs_last_error": (ctypes.c_char_p, []),
     "tgs_fill_u32": (ctypes.c_int, [P, U64, U32, P]),
-    "tgs_valu_probe": (ctypes.c_int, [P, U32, U32, P]),
+    "tgs_valu_probe": (ctypes.c_int, [P, U32, U32, ctypes.c_int32, P]),
     "tgs_fully_fused_projection_fwd": (
         ctypes.c_int,
         [U32, U32, P, P, P, P, P, P, I32, I32, F32, F32, F32, F32, P, P, P, P, P, P],
