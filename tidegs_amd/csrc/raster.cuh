@@ -269,16 +269,40 @@ __device__ __forceinline__ uint32_t cover_row(const float4& g0, const float2& g1
   return cov.w == RS_COVER_QUAD ? (in ? quad : 0u) : (cov.w == RS_COVER_ALL ? FULL : 0u);
 }
 
+// A staged Gaussian as one LDS record, so that a lane reading the entry it
+// walks needs one address computation (the record's base) and immediate
+// offsets for the rest.  Size 48 bytes at 3 channels.
+template <int CDIM>
+struct alignas(16) StagedRec {
+  float4 g0;  // x, y, A, B
+  float4 g1;  // C, L, -, -
+  float col[CDIM];
+};
+
+// Exponent coefficients of list entry t, from separate arrays or from records.
+struct GeoArrays {
+  const float4* g0;
+  const float2* g1;
+  __device__ __forceinline__ float4 G0(int t) const { return g0[t]; }
+  __device__ __forceinline__ float2 G1(int t) const { return g1[t]; }
+};
+template <int CDIM>
+struct GeoRecs {
+  const StagedRec<CDIM>* r;
+  __device__ __forceinline__ float4 G0(int t) const { return r[t].g0; }
+  __device__ __forceinline__ float2 G1(int t) const { return make_float2(r[t].g1.x, r[t].g1.y); }
+};
+
 // Pixel-row masks of the first n_list entries of a wavefront's list: lane
 // (e, r) computes entry li0 + e, row r.  The ROWS masks of an entry form its
 // 64-bit pixel mask (bit r * TILE + j = pixel (r, j) of the strip = lane
 // r * TILE + j), stored as two 32-bit halves: s_emh[0][li] holds lanes 0..31,
 // s_emh[1][li] lanes 32..63, so that a lane reads only its own half.
-template <int TILE, int BATCH>
-__device__ __forceinline__ void strip_masks(const uint8_t* s_list, int n_list, const float4* s_g0,
-                                            const float2* s_g1, const float4* s_box,
-                                            const float4* s_cov, uint32_t (*s_emh)[BATCH],
-                                            float px0, float py0, uint64_t alive) {
+template <int TILE, int BATCH, class Geo>
+__device__ __forceinline__ void strip_masks(const uint8_t* s_list, int n_list, const Geo geo,
+                                            const float4* s_box, const float4* s_cov,
+                                            uint32_t (*s_emh)[BATCH], float px0, float py0,
+                                            uint64_t alive) {
   using RM = typename std::conditional<TILE == 16, uint16_t, uint8_t>::type;
   constexpr int ROWS = 64 / TILE;
   constexpr int PER = 64 / ROWS;  // entries per pass
@@ -290,7 +314,7 @@ __device__ __forceinline__ void strip_masks(const uint8_t* s_list, int n_list, c
     if (li < n_list) {
       const int t = s_list[li];
       const uint32_t m =
-          cover_row<TILE>(s_g0[t], s_g1[t], s_box[t], s_cov[t], px0, py0 + (float)r);
+          cover_row<TILE>(geo.G0(t), geo.G1(t), s_box[t], s_cov[t], px0, py0 + (float)r);
       reinterpret_cast<RM*>(&s_emh[(r * TILE) >> 5][li])[((r * TILE) & 31) / TILE] =
           (RM)(m & alive_row);
     }
@@ -389,11 +413,9 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
       clear[w] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   constexpr int WORDS = BATCH / 32;
-  __shared__ float4 s_g0[BATCH];
-  __shared__ float2 s_g1[BATCH];
+  __shared__ StagedRec<CDIM> s_rec[BATCH];
   __shared__ float4 s_box[BATCH];
   __shared__ float4 s_cov[BATCH];
-  __shared__ float s_col[BATCH][CDIM];
   __shared__ uint8_t s_list[WAVES][BATCH];
   __shared__ __align__(16) uint32_t s_emh[WAVES][2][BATCH];
 
@@ -435,12 +457,12 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     if (have) src.load(flatten_ids[idx], s);
     if (have) {
       const StagedGeo sg = stage_geo<CDIM>(s);
-      s_g0[tr] = sg.g0;
-      s_g1[tr] = sg.g1;
+      s_rec[tr].g0 = sg.g0;
+      s_rec[tr].g1 = make_float4(sg.g1.x, sg.g1.y, 0.f, 0.f);
       s_box[tr] = sg.box;
       s_cov[tr] = sg.cov;
 #pragma unroll
-      for (int k = 0; k < CDIM; ++k) s_col[tr][k] = s.col[k];
+      for (int k = 0; k < CDIM; ++k) s_rec[tr].col[k] = s.col[k];
     }
     __syncthreads();
     const int32_t batch_size = min(BATCH, range_end - batch_start);
@@ -449,10 +471,16 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     uint64_t hits;
     const int n_list =
         build_wave_list<BATCH>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1, hits);
-    strip_masks<TILE, BATCH>(s_list[wave], n_list, s_g0, s_g1, s_box, s_cov, s_emh[wave], wx0,
-                             wy0, alive);
+    strip_masks<TILE, BATCH>(s_list[wave], n_list, GeoRecs<CDIM>{s_rec}, s_box, s_cov,
+                             s_emh[wave], wx0, wy0, alive);
     uint32_t mw[WORDS];
     lane_bits<WORDS, false>(s_emh[wave][(tr & 63) >> 5], n_list, 0, mw);
+    // the wavefront's list addressed from the lane index (a VGPR base, so the
+    // walk's address add pairs with other VALU work)
+    const uint8_t* my_list = &s_list[0][0] + (tr & ~63u) * (BATCH / 64);
+    // the batch start as a VGPR operand too (the contributor index add pairs)
+    int32_t bs_v;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(bs_v) : "s"(batch_start));
 #pragma unroll
     for (int W = 0; W < WORDS; ++W) {
       if (W * 32 >= n_list) break;
@@ -463,10 +491,11 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
         if (act) {
           const int bit = __builtin_ctz(m);
           m &= m - 1u;
-          const int t = s_list[wave][W * 32 + bit];
-          const float4 g0 = s_g0[t];
-          const float2 g1 = s_g1[t];
-          const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
+          const int t = my_list[W * 32 + bit];
+          const StagedRec<CDIM>& rec = s_rec[t];
+          const float4 g0 = rec.g0;
+          const float4 g1 = rec.g1;
+          const float power = raster_power(g0, make_float2(g1.x, g1.y), g0.x - px, g0.y - py);
           if (!(power > g1.y || power < RS_LOG2_MIN_ALPHA)) {
             const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
             const float next_T = T * (1.f - alpha);
@@ -475,8 +504,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
             } else {
               const float vis = alpha * T;
 #pragma unroll
-              for (int k = 0; k < CDIM; ++k) pix[k] += s_col[t][k] * vis;
-              cur_idx = (uint32_t)(batch_start + t);
+              for (int k = 0; k < CDIM; ++k) pix[k] += rec.col[k] * vis;
+              cur_idx = (uint32_t)(bs_v + t);
               ++n_comp;
               T = next_T;
             }
@@ -666,8 +695,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
     for (int W = 0; W < WORDS; ++W) m[W] = 0u;
     uint32_t n_pairs = 0;  // wave-uniform
     if (n_list) {
-      strip_masks<TILE, BATCH>(s_list[wave], n_list, s_g0, s_g1, s_box, s_cov, s_emh[wave], wx0,
-                               wy0, alive);
+      strip_masks<TILE, BATCH>(s_list[wave], n_list, GeoArrays{s_g0, s_g1}, s_box, s_cov,
+                               s_emh[wave], wx0, wy0, alive);
       uint32_t c_lo = 0u, c_hi = 0u;
       if (lane < n_list) {
         c_lo = (uint32_t)__popc(s_emh[wave][0][lane]);
