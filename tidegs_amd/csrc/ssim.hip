@@ -246,168 +246,168 @@ extern "C" int tgs_fused_ssim_bwd(int32_t B, int32_t CH, int32_t H, int32_t W, f
 // rendered images: per image b, L_b = (1-lambda) mean|I_b - gt'_b| +
 // lambda (1 - mean SSIM(I_b, gt'_b)), gt' = clamp(gt / gt_div, 0, 1), with
 // I [B,H,W,3] (HWC, as rendered) and gt [B,3,H,W] (CHW).  The loss is fixed,
-// so dL/dSSIM-map is the constant -lambda/N and the whole forward + backward
-// runs in one pass per 32x32 output tile and channel, keeping every
-// intermediate in LDS:
-//   inputs   x, y on the 52x52 region (tile + 2 x 5 halo each side);
-//   stats    mu, sigma over the 42x42 region (separable 11-tap window),
-//            giving SSIM (summed over the tile's own pixels) and
+// so dL/dSSIM-map is the constant -lambda/N and the forward and backward run
+// in one streaming pass:
+//   stats    mu, sigma (separable 11-tap window) giving SSIM and
 //            g dm/dmu1, g dm/dsigma1^2, g dm/dsigma12 (zero off the image);
-//   gradient G * (g dm) on the tile: f0 + 2 x f1 + y f2, plus the L1 term.
+//   gradient G * (g dm): f0 + 2 x f1 + y f2, plus the L1 term.
 // sums[2b] += sum|I-gt'|, sums[2b+1] += sum SSIM (double, caller-zeroed).
-#define TL_T 32                   // output tile edge
-#define TL_D1 (TL_T + 2 * SS_R)   // 42: dm region
-#define TL_D2 (TL_T + 4 * SS_R)   // 52: input region
-#define TL_THREADS (TL_T * TL_T)  // 1024
-#define TL_IN_PITCH 53            // >= TL_D2, odd
-#define TL_HQ_PITCH 53            // >= TL_D1, odd, 2 x 53 = 42 (mod 64)
-#define TL_DM_PITCH 43            // >= TL_D1, odd
-#define TL_H2_PITCH 49            // >= TL_T, odd
+//
+// One wavefront per (image, channel, strip of 44 output columns, band of
+// LR_BAND output rows); lane L holds column x0 - 10 + L, so the strip's
+// 64 columns cover the outputs and the 10-column halo on each side.  The
+// wavefront walks the band's input rows top to bottom (LR_BAND + 20 of them:
+// 10 rows of halo above and below) and keeps each stage's last 11 rows in
+// registers, so no row is filtered twice:
+//   input row r:   x, y into an 11-row LDS ring; horizontal window sums of
+//                  x, y, x^2, y^2, xy at the lane's column -> register ring H;
+//   stats row r-5: vertical window over H -> SSIM and the scaled partial maps
+//                  (zero off the image), through LDS to the lanes' neighbours;
+//                  horizontal window of the maps -> register ring Q;
+//   output r-10:   vertical window over Q, plus the L1 term -> dL/dI.
+// The three channel wavefronts of a strip and band share one workgroup (the
+// HWC image rows they read and write are the same lines).  The step loop is
+// unrolled by the ring length, so every ring index is a constant.
+#define LR_OUT 44                 // output columns per strip
+#define LR_BAND 123               // output rows per band (LR_BAND + 20 = 13 x 11)
+#define LR_ROWS (LR_BAND + 4 * SS_R)
+#define LR_RING 11
+static_assert(LR_ROWS % LR_RING == 0, "band rows must fill whole ring periods");
 
-__global__ void __launch_bounds__(TL_THREADS, 8) tide_loss_kernel(int H, int W,
-                                                               const float* __restrict__ images_hwc,
-                                                               const float* __restrict__ gt_chw,
-                                                               float gt_div, float C1, float C2,
-                                                               float g_ssim, float g_l1,
-                                                               float* __restrict__ v_images_hwc,
-                                                               double* __restrict__ sums) {
-  // phase-aliased LDS: inputs -> dm maps, horizontal sums -> backward sums.
-  // The horizontal passes give consecutive lanes consecutive rows (odd row
-  // pitches: distinct banks); the vertical passes give them consecutive
-  // columns, and 2 x 53 = 42 (mod 64 banks) puts the forward vertical pass's
-  // second group of lanes (two rows down) on the banks the first leaves free.
-  __shared__ union {
-    struct {
-      float sx[TL_D2][TL_IN_PITCH];
-      float sy[TL_D2][TL_IN_PITCH];
-    } in;
-    float sdm[3][TL_D1][TL_DM_PITCH];
-  } su;
-  __shared__ union {
-    float hq[5][TL_D2][TL_HQ_PITCH];
-    float h2[3][TL_D1][TL_H2_PITCH];
-  } sv;
-  __shared__ float red[2][TL_THREADS / 64];
-  auto& sx = su.in.sx;
-  auto& sy = su.in.sy;
-  auto& sdm = su.sdm;
-  auto& hq = sv.hq;
-  auto& h2 = sv.h2;
-  const int bidx = blockIdx.z;
-  const int x0 = blockIdx.x * TL_T, y0 = blockIdx.y * TL_T;
-  const int tid = threadIdx.x;
-  // output pixels of thread tid < 512: rows 2 rb2 + {0, 1} of column tx2
-  const int rb2 = (tid % (TL_T * TL_T / 2)) / TL_T, tx2 = tid % TL_T;
-  const int px2 = x0 + tx2, py2 = y0 + 2 * rb2;
-  const bool in2[2] = {px2 < W && py2 < H, px2 < W && py2 + 1 < H};
+__device__ __forceinline__ void lr_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ void __launch_bounds__(192) tide_loss_rows_kernel(int H, int W,
+                                                             const float* __restrict__ images_hwc,
+                                                             const float* __restrict__ gt_chw,
+                                                             float gt_div, float C1, float C2,
+                                                             float g_ssim, float g_l1,
+                                                             float* __restrict__ v_images_hwc,
+                                                             double* __restrict__ sums) {
+  // per channel wavefront: ring of (x, y) rows and one row of scaled partial
+  // maps, each padded by the window radius on both sides
+  __shared__ float2 s_xy[3][LR_RING][64 + 2 * SS_R];
+  __shared__ float4 s_dm[3][64 + 2 * SS_R];
+  const int c = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int b = blockIdx.z;
+  const int x0 = blockIdx.x * LR_OUT, y0 = blockIdx.y * LR_BAND;
+  const int xi = x0 - 2 * SS_R + lane;
+  const bool col_in = xi >= 0 && xi < W;
+  const bool col_out = col_in && lane >= 2 * SS_R && lane < 2 * SS_R + LR_OUT;
   const int HW = H * W;
-  const float* img = images_hwc + (int64_t)bidx * HW * 3;
-  const float* gtb = gt_chw + (int64_t)bidx * HW * 3;
-  float* vimg = v_images_hwc + (int64_t)bidx * HW * 3;
+  const float* img = images_hwc + (int64_t)b * HW * 3 + c;
+  const float* gtc = gt_chw + ((int64_t)b * 3 + c) * HW;
+  float* vimg = v_images_hwc + (int64_t)b * HW * 3 + c;
   const float rdiv = 1.f / gt_div;
+  float2(*xy)[64 + 2 * SS_R] = s_xy[c];
+  float4* dm = s_dm[c];
+  if (lane < 2 * SS_R) {
+    const int e = lane < SS_R ? lane : 64 + lane;  // pads 0..4 and 69..73
+#pragma unroll
+    for (int k = 0; k < LR_RING; ++k) xy[k][e] = make_float2(0.f, 0.f);
+    dm[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // raw image and target values of input row r at the lane's column, loaded
+  // from clamped (always valid) addresses without a branch, so that a fixed
+  // number of loads is in flight and the two-row prefetch really overlaps
+  const int xc = min(max(xi, 0), W - 1);
+  auto load_row = [&](int r, float& u, float& g) {
+    const int pix = min(max(r, 0), H - 1) * W + xc;
+    u = img[pix * 3];
+    g = gtc[pix];
+  };
+  // the window's distinct weights (the taps mirror about the centre) in
+  // VGPRs, so that every window product takes two VGPR sources (forms that
+  // issue in pairs on gfx950)
+  float wt[6];
+#pragma unroll
+  for (int t = 0; t < 6; ++t) asm volatile("v_mov_b32 %0, %1" : "=v"(wt[t]) : "s"(c_gauss[t]));
+  auto wgt = [&](int t) { return wt[t < 6 ? t : 10 - t]; };
+
+  float Hr[5][LR_RING];  // horizontal sums of the last 11 input rows
+  float Qr[3][LR_RING];  // horizontal sums of the partial maps, last 11 stats rows
+#pragma unroll
+  for (int k = 0; k < 5; ++k)
+#pragma unroll
+    for (int t = 0; t < LR_RING; ++t) Hr[k][t] = 0.f;
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int t = 0; t < LR_RING; ++t) Qr[k][t] = 0.f;
+  const int ys = y0 - 2 * SS_R;  // first input row
+  float u1, g1, u2, g2;          // raw inputs of the next two rows
+  load_row(ys, u1, g1);
+  load_row(ys + 1, u2, g2);
   float l1_acc = 0.f, m_acc = 0.f;
 
-  for (int c = 0; c < 3; ++c) {
-    const float* gtc = gtb + c * HW;
-    __syncthreads();
-    // inputs on the 52x52 region, consecutive threads on consecutive columns
-    for (int o = tid; o < TL_D2 * TL_D2; o += TL_THREADS) {
-      const int r = o / TL_D2, col = o - r * TL_D2;
-      const int yy = y0 + r - 2 * SS_R;
-      const int xx = x0 + col - 2 * SS_R;
-      float u = 0.f, w = 0.f;
-      if (xx >= 0 && yy >= 0 && xx < W && yy < H) {
-        const int pix = yy * W + xx;
-        u = img[pix * 3 + c];
-        // gt / gt_div, rounded like the division: product plus one
-        // residual correction
-        const float g = gtc[pix];
-        float q = g * rdiv;
-        q = fmaf(fmaf(-q, gt_div, g), rdiv, q);
-        w = fminf(fmaxf(q, 0.f), 1.f);
-      }
-      sx[r][col] = u;
-      sy[r][col] = w;
-    }
-    __syncthreads();
-    // threads below 512 keep the inputs of their two output pixels (rows
-    // 2 rb2 and 2 rb2 + 1 of column tx2) for the gradient at the end
-    float x_own[2] = {0.f, 0.f}, y_own[2] = {0.f, 0.f};
-    if (tid < TL_T * TL_T / 2) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        x_own[j] = sx[2 * rb2 + j + 2 * SS_R][tx2 + 2 * SS_R];
-        y_own[j] = sy[2 * rb2 + j + 2 * SS_R][tx2 + 2 * SS_R];
-        if (in2[j]) l1_acc += fabsf(x_own[j] - y_own[j]);
-      }
-    }
-    // horizontal pass of x, y, x^2, y^2, xy: 52 rows x 42 columns, three
-    // consecutive columns per work item (13 inputs; each product formed once),
-    // consecutive items on consecutive rows
-    for (int o = tid; o < TL_D2 * (TL_D1 / 3); o += TL_THREADS) {
-      const int cb = (o / TL_D2) * 3, r = o - (o / TL_D2) * TL_D2;
-      float u[13], w[13];
-#pragma unroll
-      for (int t = 0; t < 13; ++t) {
-        u[t] = sx[r][cb + t];
-        w[t] = sy[r][cb + t];
-      }
-#pragma unroll
-      for (int k = 0; k < 5; ++k) {
-        float v[13];
-#pragma unroll
-        for (int t = 0; t < 13; ++t)
-          v[t] = k == 0 ? u[t] : k == 1 ? w[t] : k == 2 ? u[t] * u[t] : k == 3 ? w[t] * w[t]
-                                                                               : u[t] * w[t];
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          float q = 0.f;
-#pragma unroll
-          for (int t = 0; t < 11; ++t) q += c_gauss[t] * v[j + t];
-          hq[k][r][cb + j] = q;
-        }
-      }
-    }
-    __syncthreads();
-    // vertical pass on the 42x42 region, two consecutive rows per work item:
-    // SSIM and the scaled partial maps (the inputs are dead: the dm maps take
-    // their place)
 #pragma unroll 1
-    for (int o = tid; o < (TL_D1 / 2) * TL_D1; o += TL_THREADS) {
-      const int rq = o / TL_D1, col = o - rq * TL_D1;
-      const int rb = 2 * rq;
-      float f[2][5];
+  for (int n0 = 0; n0 < LR_ROWS; n0 += LR_RING) {
 #pragma unroll
-      for (int k = 0; k < 5; ++k) {
-        float v[12];
+    for (int p = 0; p < LR_RING; ++p) {
+      const int n = n0 + p;
+      const int ri = ys + n;
+      // x and clamp(gt / gt_div, 0, 1) of row ri (zero off the image); the
+      // division is rounded like a division: product plus one residual correction
+      const bool ok = col_in && ri >= 0 && ri < H;
+      float q = g1 * rdiv;
+      q = fmaf(fmaf(-q, gt_div, g1), rdiv, q);
+      const float u = ok ? u1 : 0.f, w = ok ? fminf(fmaxf(q, 0.f), 1.f) : 0.f;
+      u1 = u2;
+      g1 = g2;
+      load_row(ri + 2, u2, g2);
+      // input row ri: ring slot p
+      xy[p][lane + SS_R] = make_float2(u, w);
+      lr_wave_sync();
+      {
+        float wx[11], wy[11], xv[11], yv[11];
 #pragma unroll
-        for (int t = 0; t < 12; ++t) v[t] = hq[k][rb + t][col];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          float acc = 0.f;
-#pragma unroll
-          for (int t = 0; t < 11; ++t) acc += c_gauss[t] * v[j + t];
-          f[j][k] = acc;
+        for (int t = 0; t < 11; ++t) {
+          const float2 v = xy[p][lane + t];
+          xv[t] = v.x;
+          yv[t] = v.y;
+          wx[t] = wgt(t) * v.x;
+          wy[t] = wgt(t) * v.y;
         }
-        // one map at a time: its sums are complete before the next map's loads
-        // (bounds the registers to 8 waves per SIMD)
-        asm volatile("" : "+v"(f[0][k]), "+v"(f[1][k])::"memory");
-      }
+        float h0 = wx[0], h1 = wy[0], h2 = wx[0] * xv[0], h3 = wy[0] * yv[0],
+              h4 = wx[0] * yv[0];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int r = rb + j;
-        const float mu1 = f[j][0], mu2 = f[j][1];
-        const float sigma1_sq = f[j][2] - mu1 * mu1;
-        const float sigma2_sq = f[j][3] - mu2 * mu2;
-        const float sigma12 = f[j][4] - mu1 * mu2;
+        for (int t = 1; t < 11; ++t) {
+          h0 += wx[t];
+          h1 += wy[t];
+          h2 = fmaf(wx[t], xv[t], h2);
+          h3 = fmaf(wy[t], yv[t], h3);
+          h4 = fmaf(wx[t], yv[t], h4);
+        }
+        Hr[0][p] = h0;
+        Hr[1][p] = h1;
+        Hr[2][p] = h2;
+        Hr[3][p] = h3;
+        Hr[4][p] = h4;
+      }
+      if (n >= 2 * SS_R) {
+        // stats row rs = ri - 5 from input rows ri - 10 .. ri (slots p+1 .. p+11)
+        const int rs = ri - SS_R;
+        float f[5];
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+          float acc = wgt(0) * Hr[k][(p + 1) % LR_RING];
+#pragma unroll
+          for (int t = 1; t < 11; ++t) acc = fmaf(wgt(t), Hr[k][(p + 1 + t) % LR_RING], acc);
+          f[k] = acc;
+        }
+        const float mu1 = f[0], mu2 = f[1];
+        const float sigma1_sq = f[2] - mu1 * mu1;
+        const float sigma2_sq = f[3] - mu2 * mu2;
+        const float sigma12 = f[4] - mu1 * mu2;
         const float Cc = 2.f * mu1 * mu2 + C1;
         const float D = 2.f * sigma12 + C2;
         const float A = mu1 * mu1 + mu2 * mu2 + C1;
         const float Bb = sigma1_sq + sigma2_sq + C2;
-        const int yy = y0 + r - SS_R, xx = x0 + col - SS_R;
-        const bool in_img = xx >= 0 && yy >= 0 && xx < W && yy < H;
         float d0 = 0.f, d1 = 0.f, d2 = 0.f;
-        if (in_img) {
+        if (col_in && rs >= 0 && rs < H) {
           // the partial maps of clm_kernels/ssim.cu:240-262 from two
           // reciprocals; A >= C1 and Bb >= C2 - (rounding) > 0, so the
           // hardware reciprocal (within 1 ulp) is safe here
@@ -417,78 +417,50 @@ __global__ void __launch_bounds__(TL_THREADS, 8) tide_loss_kernel(int H, int W,
           d0 = 2.f * rAB * (mu2 * D - mu2 * Cc + mu1 * CD * (rB - rA));
           d1 = -CD * rAB * rB;
           d2 = 2.f * Cc * rAB;
-          if (r >= SS_R && r < SS_R + TL_T && col >= SS_R && col < SS_R + TL_T)
-            m_acc += CD * rAB;
+          if (col_out && rs >= y0 && rs < y0 + LR_BAND) m_acc += CD * rAB;
         }
-        sdm[0][r][col] = g_ssim * d0;
-        sdm[1][r][col] = g_ssim * d1;
-        sdm[2][r][col] = g_ssim * d2;
-      }
-    }
-    __syncthreads();
-    // backward: horizontal pass (42 rows x 32 columns), two columns per item,
-    // consecutive items on consecutive rows ...
-    for (int o = tid; o < TL_D1 * (TL_T / 2); o += TL_THREADS) {
-      const int cb = (o / TL_D1) * 2, r = o - (o / TL_D1) * TL_D1;
+        dm[lane + SS_R] = make_float4(g_ssim * d0, g_ssim * d1, g_ssim * d2, 0.f);
+        lr_wave_sync();
+        float q0 = 0.f, q1 = 0.f, q2 = 0.f;
 #pragma unroll
-      for (int m = 0; m < 3; ++m) {
-        float v[12];
-#pragma unroll
-        for (int t = 0; t < 12; ++t) v[t] = sdm[m][r][cb + t];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          float q = 0.f;
-#pragma unroll
-          for (int t = 0; t < 11; ++t) q += c_gauss[t] * v[j + t];
-          h2[m][r][cb + j] = q;
+        for (int t = 0; t < 11; ++t) {
+          const float4 v = dm[lane + t];
+          q0 = fmaf(wgt(t), v.x, q0);
+          q1 = fmaf(wgt(t), v.y, q1);
+          q2 = fmaf(wgt(t), v.z, q2);
         }
+        Qr[0][p] = q0;
+        Qr[1][p] = q1;
+        Qr[2][p] = q2;
       }
-    }
-    __syncthreads();
-    // ... then vertical, two rows per item (threads below 512), and the
-    // gradient of those pixels
-    if (tid < TL_T * TL_T / 2) {
-      float f[2][3];
+      if (n >= 4 * SS_R) {
+        // output row ro = ri - 10 from stats rows ro - 5 .. ro + 5 (slots p+1 .. p+11)
+        const int ro = ri - 2 * SS_R;
+        float g3[3];
 #pragma unroll
-      for (int m = 0; m < 3; ++m) {
-        float v[12];
+        for (int k = 0; k < 3; ++k) {
+          float acc = wgt(0) * Qr[k][(p + 1) % LR_RING];
 #pragma unroll
-        for (int t = 0; t < 12; ++t) v[t] = h2[m][2 * rb2 + t][tx2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          float q = 0.f;
-#pragma unroll
-          for (int t = 0; t < 11; ++t) q += c_gauss[t] * v[j + t];
-          f[j][m] = q;
+          for (int t = 1; t < 11; ++t) acc = fmaf(wgt(t), Qr[k][(p + 1 + t) % LR_RING], acc);
+          g3[k] = acc;
+        }
+        if (col_out && ro < H) {
+          const float2 v = xy[(p + 1) % LR_RING][lane + SS_R];  // x, y of row ro
+          const float d = v.x - v.y;
+          l1_acc += fabsf(d);
+          vimg[(ro * W + xi) * 3] = g3[0] + 2.f * v.x * g3[1] + v.y * g3[2] +
+                                    (d > 0.f ? g_l1 : (d < 0.f ? -g_l1 : 0.f));
         }
       }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (in2[j]) {
-          const float d = x_own[j] - y_own[j];
-          vimg[((py2 + j) * W + px2) * 3 + c] = f[j][0] + 2.f * x_own[j] * f[j][1] +
-                                                y_own[j] * f[j][2] +
-                                                (d > 0.f ? g_l1 : (d < 0.f ? -g_l1 : 0.f));
-        }
-      }
+      // every lane has read this step's rows before the next step writes
+      lr_wave_sync();
     }
   }
   const float l1 = tgs_wave_sum(l1_acc);
   const float ms = tgs_wave_sum(m_acc);
-  const int lane = tid & 63, wave = tid >> 6;
   if (lane == 0) {
-    red[0][wave] = l1;
-    red[1][wave] = ms;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float a0 = 0.f, a1 = 0.f;
-    for (int w = 0; w < TL_THREADS / 64; ++w) {
-      a0 += red[0][w];
-      a1 += red[1][w];
-    }
-    atomicAdd(&sums[2 * bidx + 0], (double)a0);
-    atomicAdd(&sums[2 * bidx + 1], (double)a1);
+    atomicAdd(&sums[2 * b + 0], (double)l1);
+    atomicAdd(&sums[2 * b + 1], (double)ms);
   }
 }
 
@@ -499,8 +471,9 @@ extern "C" int tgs_tide_loss(int32_t B, int32_t H, int32_t W, const float* image
   TGS_CHECK_ARG(images_hwc && gt_chw && sums && v_images_hwc, "tide_loss: null pointer");
   TGS_CHECK_ARG((int64_t)H * W * 3 < (1ll << 31), "tide_loss: image too large");
   const float inv_n = 1.f / (float)((int64_t)3 * H * W);
-  dim3 grid((W + TL_T - 1) / TL_T, (H + TL_T - 1) / TL_T, B);
-  hipLaunchKernelGGL(tide_loss_kernel, grid, dim3(TL_THREADS), 0, stream, H, W, images_hwc, gt_chw,
+  TGS_CHECK_ARG(B <= 65535, "tide_loss: more than 65535 images");
+  dim3 grid((W + LR_OUT - 1) / LR_OUT, (H + LR_BAND - 1) / LR_BAND, B);
+  hipLaunchKernelGGL(tide_loss_rows_kernel, grid, dim3(192), 0, stream, H, W, images_hwc, gt_chw,
                      gt_div,
                      1e-4f, 9e-4f, -lambda_dssim * inv_n, (1.f - lambda_dssim) * inv_n,
                      v_images_hwc, sums);
