@@ -342,6 +342,9 @@ def bench_step(args, dev):
                 acc[k] = acc.get(k, 0.0) + v
         stage_ms = {k: round(v / reps, 4) for k, v in acc.items()}
         stats = st
+        # one more step, untimed, with the forward counting the composited
+        # (Gaussian, pixel) pairs (its counting walk is slower than the plain one)
+        ts.step(sc.viewmats, sc.Ks, sc.gt, count_pairs=True)
     P = sc.width * sc.height
     kernels = _stage_kernels(ts, stats, args, stage_ms, C, P)
     default_cfg = (args.workload == "cfg3" and

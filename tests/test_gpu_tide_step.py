@@ -57,6 +57,35 @@ def test_tide_step_grads_match_oracle(gpu, with_bg, pitch):
         assert err < 1e-4, (name, err)
 
 
+def test_counting_forward_matches_plain(gpu):
+    """The forward variant that also counts each pixel's composited Gaussians
+    (bench live-pair statistic) renders bit-identically to the plain one; its
+    counts are zero exactly where nothing composites and bounded by the
+    pixel's tile list."""
+    announce("tide step counting forward")
+    sc = _scene(seed=4)
+    ts = TideStep(sc.params.to(gpu).contiguous(), sc.width, sc.height, batch_size=sc.n_cams)
+    ts.forward_backward(sc.viewmats, sc.Ks, sc.gt)
+    plain = {k: to_np(ts.last[k]).copy() for k in ("images", "alphas", "last_ids", "v_images")}
+    ts.forward_backward(sc.viewmats, sc.Ks, sc.gt, count_pairs=True)
+    for k, v in plain.items():
+        np.testing.assert_array_equal(to_np(ts.last[k]), v, err_msg=k)
+    n = to_np(ts.last["n_contrib"])
+    alphas = plain["alphas"]
+    assert ((n == 0) == (alphas == 0)).all()
+    offs = to_np(ts.last["offsets"]).reshape(sc.n_cams, -1)
+    n_isects = len(to_np(ts.last["flatten_ids"]))
+    flat = offs.reshape(-1)
+    ends = np.append(flat[1:], n_isects).reshape(offs.shape)
+    per_tile = ends - offs  # list length of each (camera, tile)
+    tw = offs.shape[1] // ((sc.height + 15) // 16)
+    for c in range(sc.n_cams):
+        ty, tx = np.divmod(np.arange(sc.height * sc.width), sc.width)
+        lim = per_tile[c][(ty // 16) * tw + tx // 16].reshape(sc.height, sc.width)
+        assert (n[c] <= lim).all()
+    assert ts.last_live_pairs == int(n.sum())
+
+
 def test_tide_step_isect_bit_exact(gpu):
     announce("tide step isect")
     sc = _scene(seed=2)

@@ -390,7 +390,9 @@ inline dim3 raster_bwd_grid(const RasterGeom& G) { return dim3(G.tile_h, G.tile_
 #define RF_BATCH 128  // Gaussians staged per batch
 
 // (up to 4 channels the forward fits 64 VGPRs: 8 wavefronts per SIMD)
-template <int CDIM, int TILE, class Src>
+// COUNT: also count each pixel's composited Gaussians into n_contrib (a
+// measurement aid; the plain variant leaves that counter out of the walk)
+template <int CDIM, int TILE, class Src, bool COUNT = false>
 __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kernel(
     RasterGeom G, Src src, const float* __restrict__ backgrounds,
     const int32_t* __restrict__ tile_offsets, const int32_t* __restrict__ flatten_ids,
@@ -486,7 +488,9 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
       if (W * 32 >= n_list) break;
       uint32_t m = done ? 0u : mw[W];
       while (true) {
-        const bool act = m != 0u && !done;
+        // a lane that reaches the threshold clears m, so m != 0 is its
+        // whole loop condition
+        const bool act = m != 0u;
         if (!tgs_ballot(act)) break;
         if (act) {
           const int bit = __builtin_ctz(m);
@@ -496,20 +500,22 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
           const float4 g0 = rec.g0;
           const float4 g1 = rec.g1;
           const float power = raster_power(g0, make_float2(g1.x, g1.y), g0.x - px, g0.y - py);
-          if (!(power > g1.y || power < RS_LOG2_MIN_ALPHA)) {
-            const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
-            const float next_T = T * (1.f - alpha);
-            if (next_T <= 1e-4f) {
-              done = true;
-            } else {
-              const float vis = alpha * T;
+          // predicated rather than branched (one exec level in the loop):
+          // a Gaussian failing the alpha test, or the one that would take T
+          // to the threshold, adds exactly zero
+          const bool pass = !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
+          const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
+          const float next_T = T * (1.f - alpha);
+          const bool stop = pass && next_T <= 1e-4f;
+          const bool comp = pass && !stop;
+          m = stop ? 0u : m;
+          done = done || stop;
+          const float vis = comp ? alpha * T : 0.f;
 #pragma unroll
-              for (int k = 0; k < CDIM; ++k) pix[k] += rec.col[k] * vis;
-              cur_idx = (uint32_t)(bs_v + t);
-              ++n_comp;
-              T = next_T;
-            }
-          }
+          for (int k = 0; k < CDIM; ++k) pix[k] = fmaf(rec.col[k], vis, pix[k]);
+          cur_idx = comp ? (uint32_t)(bs_v + t) : cur_idx;
+          if (COUNT) n_comp += comp ? 1 : 0;
+          T = comp ? next_T : T;
         }
       }
     }
@@ -522,7 +528,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
       render_colors[pid * CDIM + k] =
           backgrounds ? pix[k] + T * backgrounds[cam * CDIM + k] : pix[k];
     last_ids[pid] = (int32_t)cur_idx;
-    if (n_contrib) n_contrib[pid] = n_comp;
+    if (COUNT) n_contrib[pid] = n_comp;
   }
 }
 

@@ -1098,10 +1098,16 @@ extern "C" int tgs_tide_rasterize_fwd(uint32_t C, const float* splats, const flo
   TGS_CHECK_ARG(C <= 65535 && tile_width <= 65535 && tile_height <= 65535,
                 "tide_rasterize_fwd: at most 65535 cameras and tiles per image side");
   const RasterGeom G{C, W, H, tile_width, tile_height, n_isects};
-  hipLaunchKernelGGL((raster_fwd_kernel<3, 16, PackedSplats>), raster_fwd_grid(G), dim3(256), 0,
-                     stream, G, PackedSplats{(const float4*)splats}, backgrounds,
-                     tile_offsets, flatten_ids, images, alphas, last_ids, (float4*)clear,
-                     (uint64_t)clear_words / 4, n_contrib);
+  if (n_contrib)
+    hipLaunchKernelGGL((raster_fwd_kernel<3, 16, PackedSplats, true>), raster_fwd_grid(G),
+                       dim3(256), 0, stream, G, PackedSplats{(const float4*)splats}, backgrounds,
+                       tile_offsets, flatten_ids, images, alphas, last_ids, (float4*)clear,
+                       (uint64_t)clear_words / 4, n_contrib);
+  else
+    hipLaunchKernelGGL((raster_fwd_kernel<3, 16, PackedSplats>), raster_fwd_grid(G), dim3(256), 0,
+                       stream, G, PackedSplats{(const float4*)splats}, backgrounds,
+                       tile_offsets, flatten_ids, images, alphas, last_ids, (float4*)clear,
+                       (uint64_t)clear_words / 4, nullptr);
   TGS_RETURN_LAUNCH("tgs_tide_rasterize_fwd");
 }
 

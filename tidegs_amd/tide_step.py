@@ -183,10 +183,11 @@ class TideStep:
         self._bufs: Dict[str, torch.Tensor] = {}
         self.last: Dict[str, torch.Tensor] = {}
         self._timing = False
+        self._count_pairs = False
         self._events = []
         self.stage_ms: Dict[str, float] = {}
         self.last_visible_entries = 0
-        self.last_live_pairs = 0  # composited (Gaussian, pixel) pairs of the last timed step
+        self.last_live_pairs = 0  # composited (Gaussian, pixel) pairs of the last counting step
 
     # ---- stage timing (HIP events on the launch stream) ----------------------
     def _begin(self, name: str):
@@ -233,9 +234,16 @@ class TideStep:
         return ev
 
     # ---- stages -----------------------------------------------------------
-    def forward_backward(self, viewmats: torch.Tensor, Ks: torch.Tensor, gt: torch.Tensor):
-        """Everything up to the compact gradients; returns (touched, grads, stats)."""
-        return self._run(viewmats, Ks, gt, update=False)
+    def forward_backward(self, viewmats: torch.Tensor, Ks: torch.Tensor, gt: torch.Tensor,
+                         count_pairs: bool = False):
+        """Everything up to the compact gradients; returns (touched, grads, stats).
+        ``count_pairs`` as for :meth:`step` (the per-pixel counts are left in
+        ``self.last["n_contrib"]``)."""
+        self._count_pairs = bool(count_pairs)
+        try:
+            return self._run(viewmats, Ks, gt, update=False)
+        finally:
+            self._count_pairs = False
 
     def _run(self, viewmats: torch.Tensor, Ks: torch.Tensor, gt: torch.Tensor, update: bool):
         """The batch's stages.  With ``update`` the last stage applies the
@@ -386,7 +394,7 @@ class TideStep:
         self._begin("raster_fwd")
         # with timing, also each pixel's composited-Gaussian count (the live
         # (Gaussian, pixel) pairs the backward replays)
-        n_contrib = self._buf("n_contrib", C * H * W, torch.int32) if self._timing else None
+        n_contrib = self._buf("n_contrib", C * H * W, torch.int32) if self._count_pairs else None
         N.call("tgs_tide_rasterize_fwd", C, N.ptr(splats), N.ptr(bg), W, H, tw, th,
                N.ptr(offsets), N.ptr(fids), n_isects, N.ptr(images), N.ptr(alphas),
                N.ptr(last_ids), N.ptr(n_contrib), N.ptr(sgrads), sg_words, s)
@@ -431,6 +439,7 @@ class TideStep:
             self._end()
         if self._timing:
             self.last_visible_entries = int((splats[: V * 12].view(-1, 12)[:, 7] > 0).sum())
+        if self._count_pairs:
             self.last_live_pairs = int(n_contrib.sum(dtype=torch.int64))
         self.last = dict(masks=masks, entries=entries[:V], cam_offsets=cam_offsets,
                          touched=touched[:T], visit_base=visit_base[:T + 1], visits=visits[:V],
@@ -439,7 +448,8 @@ class TideStep:
                          flatten_ids=fids[:n_isects], offsets=offsets[:n_buckets].view(C, th, tw),
                          images=images.view(C, H, W, 3), alphas=alphas.view(C, H, W),
                          last_ids=last_ids.view(C, H, W), v_images=v_images.view(C, H, W, 3),
-                         splat_grads=sgrads[: V * 9].view(-1, 9), grads=grads, campos=campos)
+                         splat_grads=sgrads[: V * 9].view(-1, 9), grads=grads, campos=campos,
+                         n_contrib=n_contrib.view(C, H, W) if n_contrib is not None else None)
         stats = StepStats(n_cameras=C, visible_per_camera=tot[:C], touched_rows=T, entries=V,
                           n_isects=n_isects, loss_sums=sums.view(C, 2), optimizer=opt_stats,
                           isects_per_camera=[isect_segs[c + 1] - isect_segs[c] for c in range(C)])
@@ -451,13 +461,17 @@ class TideStep:
         return self.optimizer.step(self._iteration, self.gaussians, touched, comps)
 
     def step(self, viewmats: torch.Tensor, Ks: torch.Tensor, gt: torch.Tensor,
-             timing: bool = False) -> StepStats:
+             timing: bool = False, count_pairs: bool = False) -> StepStats:
         """One batch: forward, backward and the resident optimizer update.
 
         With ``timing`` the stages are bracketed by HIP events on the launch
-        stream and their times (ms) are left in ``self.stage_ms``.
+        stream and their times (ms) are left in ``self.stage_ms``.  With
+        ``count_pairs`` the forward also counts each pixel's composited
+        Gaussians (a slower variant of its walk) and leaves their sum in
+        ``self.last_live_pairs``.
         """
         self._timing = bool(timing)
+        self._count_pairs = bool(count_pairs)
         self._events = []
         try:
             if self.fuse_update:
@@ -471,5 +485,6 @@ class TideStep:
                 self._collect()
         finally:
             self._timing = False
+            self._count_pairs = False
             self.optimizer.kernel_hooks = None
         return stats
