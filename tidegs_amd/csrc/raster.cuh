@@ -764,24 +764,27 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
             const float4 g0 = s_g0[t];
             const float2 g1 = s_g1[t];
             const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
-            if (!(power > g1.y || power < RS_LOG2_MIN_ALPHA)) {
-              const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
-              const float alpha = fminf(0.999f, raw);
-              const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
-              T *= ra;
-              const float fac = alpha * T;
-              // v_alpha = sum_k (c_k T - buffer_k ra) v_rc_k + ra tf_term
-              float cv = 0.f;
+            // predicated rather than branched: a pixel failing the exact
+            // test keeps T and the colour buffer and writes (0, 0), the value
+            // its zeroed slot already holds
+            const bool pass = !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
+            const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
+            const float alpha = fminf(0.999f, raw);
+            const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
+            const float Tn = T * ra;
+            T = pass ? Tn : T;
+            // v_alpha = sum_k (c_k T - buffer_k ra) v_rc_k + ra tf_term
+            float cv = 0.f;
 #pragma unroll
-              for (int k = 0; k < CDIM; ++k) cv = fmaf(s_col[t][k], v_rc[k], cv);
-              const float v_alpha = fmaf(T, cv, ra * (tf_term - buffer_dot));
-              buffer_dot = fmaf(fac, cv, buffer_dot);
-              // reference: the sigma terms only where alpha was not clamped
-              const float v_sigma = raw <= 0.999f ? -raw * v_alpha : 0.f;
-              const uint32_t slot = (uint32_t)s_poh[wave][half][li] - base +
-                                    (uint32_t)__popc(s_emh[wave][half][li] & lt_half);
-              s_pair[wave][slot] = make_float2(fac, v_sigma);
-            }
+            for (int k = 0; k < CDIM; ++k) cv = fmaf(s_col[t][k], v_rc[k], cv);
+            const float v_alpha = fmaf(Tn, cv, ra * (tf_term - buffer_dot));
+            const float fac = pass ? alpha * Tn : 0.f;
+            buffer_dot = fmaf(fac, cv, buffer_dot);
+            // reference: the sigma terms only where alpha was not clamped
+            const float v_sigma = pass && raw <= 0.999f ? -raw * v_alpha : 0.f;
+            const uint32_t slot = (uint32_t)s_poh[wave][half][li] - base +
+                                  (uint32_t)__popc(s_emh[wave][half][li] & lt_half);
+            s_pair[wave][slot] = make_float2(fac, v_sigma);
           }
         }
       }
