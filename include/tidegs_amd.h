@@ -362,6 +362,19 @@ int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offsets, uint32_t
                         const uint64_t* entry_rects, const int64_t* cum_tiles,
                         uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
                         int32_t* flatten_ids, tgs_stream_t stream);
+/* The same emission without per-entry offsets (the form TideStep uses): the
+ * depth-ordered entries in blocks of 2048 (tgs_tide_isect_emit_blocks of
+ * them); tgs_tide_isect_block_sums writes each block's rectangle-area sum
+ * (uint32), the caller scans those sums (tgs_exclusive_scan_u32 -> block_base)
+ * and tgs_tide_isect_emit_blocked writes keys and flatten ids exactly as
+ * tgs_tide_isect_emit does.  Same 2^31 intersection limit. */
+uint32_t tgs_tide_isect_emit_blocks(uint32_t n_entries);
+int tgs_tide_isect_block_sums(uint32_t n_entries, const uint64_t* entry_rects,
+                              uint32_t* block_sums, tgs_stream_t stream);
+int tgs_tide_isect_emit_blocked(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,
+                                const uint64_t* entry_rects, const uint32_t* block_base,
+                                uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
+                                int32_t* flatten_ids, tgs_stream_t stream);
 int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, uint32_t C,
                            uint32_t tile_width, uint32_t tile_height, uint32_t tile_n_bits,
                            int32_t* offsets, tgs_stream_t stream);

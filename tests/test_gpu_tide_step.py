@@ -86,6 +86,55 @@ def test_counting_forward_matches_plain(gpu):
     assert ts.last_live_pairs == int(n.sum())
 
 
+@pytest.mark.parametrize("V,C", [(1, 1), (2047, 2), (2049, 3), (50_000, 16)])
+def test_blocked_emit_matches_offset_emit(gpu, V, C):
+    """tgs_tide_isect_emit_blocked (block area sums + scan + in-block prefix
+    sums) writes the same keys and flatten ids as the per-entry form (count,
+    int64 inclusive scan, emit), on random rectangles with empty ones and
+    camera boundaries inside and across blocks."""
+    announce(f"blocked isect emission V={V} C={C}")
+    from tidegs_amd import _native as N
+    lib = N.load()
+    rng = np.random.default_rng(V + C)
+    tw, th = 120, 68
+    x0 = rng.integers(0, tw, V)
+    y0 = rng.integers(0, th, V)
+    x1 = np.minimum(x0 + rng.integers(0, 5, V), tw)  # width 0 gives empty rectangles
+    y1 = np.minimum(y0 + rng.integers(0, 4, V), th)
+    rc = (x0 | (x1 << 8) | (y0 << 16) | (y1 << 24)).astype(np.uint64)
+    ids = rng.integers(0, 1 << 30, V).astype(np.uint64)
+    rects = torch.from_numpy(((rc << np.uint64(32)) | ids).view(np.int64)).to(gpu)
+    cuts = np.sort(rng.choice(np.arange(1, V), size=min(C - 1, V - 1), replace=False)) if V > 1 else []
+    cam_off = torch.tensor(np.concatenate([[0], cuts, [V] * (C - len(cuts))]).astype(np.int32),
+                           device=gpu)
+    n_isects = int(((x1 - x0) * (y1 - y0)).sum())
+    tile_bits = (tw * th).bit_length()
+    s = N.stream_handle()
+    tiles = torch.empty(V, dtype=torch.int32, device=gpu)
+    cum = torch.empty(V, dtype=torch.int64, device=gpu)
+    ws = torch.empty(lib.tgs_scan_workspace_size(V), dtype=torch.uint8, device=gpu)
+    N.call("tgs_tide_isect_count", V, N.ptr(rects), N.ptr(tiles), s)
+    N.call("tgs_inclusive_scan_i32_i64", N.ptr(tiles), N.ptr(cum), V, N.ptr(ws), ws.numel(), s)
+    cap = max(n_isects, 1)
+    k_ref = torch.empty(cap, dtype=torch.int32, device=gpu)
+    f_ref = torch.empty(cap, dtype=torch.int32, device=gpu)
+    N.call("tgs_tide_isect_emit", V, N.ptr(cam_off), C, N.ptr(rects), N.ptr(cum), tw, tile_bits,
+           N.ptr(k_ref), N.ptr(f_ref), s)
+    nb = lib.tgs_tide_isect_emit_blocks(V)
+    sums = torch.empty(nb, dtype=torch.int32, device=gpu)
+    base = torch.empty(nb, dtype=torch.int32, device=gpu)
+    ws2 = torch.empty(lib.tgs_scan_workspace_size(nb), dtype=torch.uint8, device=gpu)
+    N.call("tgs_tide_isect_block_sums", V, N.ptr(rects), N.ptr(sums), s)
+    N.call("tgs_exclusive_scan_u32", N.ptr(sums), N.ptr(base), nb, N.ptr(ws2), ws2.numel(), s)
+    k = torch.empty(cap, dtype=torch.int32, device=gpu)
+    f = torch.empty(cap, dtype=torch.int32, device=gpu)
+    N.call("tgs_tide_isect_emit_blocked", V, N.ptr(cam_off), C, N.ptr(rects), N.ptr(base), tw,
+           tile_bits, N.ptr(k), N.ptr(f), s)
+    assert int(cum[-1]) == n_isects
+    np.testing.assert_array_equal(to_np(k)[:n_isects], to_np(k_ref)[:n_isects])
+    np.testing.assert_array_equal(to_np(f)[:n_isects], to_np(f_ref)[:n_isects])
+
+
 def test_tide_step_isect_bit_exact(gpu):
     announce("tide step isect")
     sc = _scene(seed=2)

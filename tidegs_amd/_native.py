@@ -105,6 +105,9 @@ SIGNATURES = {
     "tgs_tide_isect_count": (ctypes.c_int, [U32, P, P, P]),
     "tgs_tide_isect_segments": (ctypes.c_int, [U32, P, P, P, P]),
     "tgs_tide_isect_emit": (ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P]),
+    "tgs_tide_isect_emit_blocks": (U32, [U32]),
+    "tgs_tide_isect_block_sums": (ctypes.c_int, [U32, P, P, P]),
+    "tgs_tide_isect_emit_blocked": (ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P]),
     "tgs_tide_offset_encode": (ctypes.c_int, [U32, P, U32, U32, U32, U32, P, P]),
     "tgs_tide_isect_ids": (ctypes.c_int, [U32, P, P, P, P, P]),
     "tgs_tide_rasterize_fwd": (

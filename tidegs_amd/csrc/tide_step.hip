@@ -477,6 +477,91 @@ __global__ void __launch_bounds__(256) tide_isect_emit_kernel(
     }
 }
 
+// Emission with block-local offsets: the depth-ordered entries are taken in
+// blocks of EMIT_ENTRIES; tide_isect_block_sums_kernel sums each block's
+// rectangle areas, the host-side launch scans those sums (exclusive), and
+// the emission kernel turns a block's base into its entries' first
+// intersection slots with wave prefix sums.  Entry k * 256 + t of a block is
+// item k of thread t, so each round of stores covers 256 consecutive entries
+// (the per-entry int64 offsets of the count + scan form are never written).
+#define EMIT_ITEMS 8
+#define EMIT_ENTRIES (256 * EMIT_ITEMS)
+
+__global__ void __launch_bounds__(256) tide_isect_block_sums_kernel(
+    uint32_t n_entries, const uint64_t* __restrict__ rects, uint32_t* __restrict__ block_sums) {
+  __shared__ uint32_t s_w[4];
+  const uint32_t base = blockIdx.x * EMIT_ENTRIES;
+  const uint32_t* hi = reinterpret_cast<const uint32_t*>(rects) + 1;
+  uint32_t rc[EMIT_ITEMS];
+#pragma unroll
+  for (int k = 0; k < EMIT_ITEMS; ++k) {
+    const uint32_t e = base + (uint32_t)k * 256u + threadIdx.x;
+    rc[k] = e < n_entries ? hi[2ull * e] : 0u;
+  }
+  uint32_t acc = 0u;
+#pragma unroll
+  for (int k = 0; k < EMIT_ITEMS; ++k) acc += rect_tiles(rc[k]);
+  const uint32_t inc = wave_incl_scan(acc);
+  if ((threadIdx.x & 63u) == 63u) s_w[threadIdx.x >> 6] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) block_sums[blockIdx.x] = s_w[0] + s_w[1] + s_w[2] + s_w[3];
+}
+
+__global__ void __launch_bounds__(256) tide_isect_emit_blocked_kernel(
+    uint32_t n_entries, const int32_t* __restrict__ cam_offsets, uint32_t C,
+    const uint64_t* __restrict__ rects, const uint32_t* __restrict__ block_base, uint32_t tw,
+    uint32_t tile_n_bits, uint32_t* __restrict__ keys, int32_t* __restrict__ flatten_ids) {
+  __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
+  __shared__ uint32_t s_tot[EMIT_ITEMS][4];  // per round, each wavefront's area sum
+  if (threadIdx.x <= C) s_off[threadIdx.x] = cam_offsets[threadIdx.x];
+  const uint32_t base = blockIdx.x * EMIT_ENTRIES;
+  const uint32_t wave = threadIdx.x >> 6;
+  uint64_t v[EMIT_ITEMS];
+#pragma unroll
+  for (int k = 0; k < EMIT_ITEMS; ++k) {
+    const uint32_t e = base + (uint32_t)k * 256u + threadIdx.x;
+    v[k] = e < n_entries ? rects[e] : 0ull;  // an empty rectangle past the end
+  }
+  uint32_t excl[EMIT_ITEMS];  // area prefix within the round's wavefront
+#pragma unroll
+  for (int k = 0; k < EMIT_ITEMS; ++k) {
+    const uint32_t a = rect_tiles((uint32_t)(v[k] >> 32));
+    const uint32_t inc = wave_incl_scan(a);
+    excl[k] = inc - a;
+    if ((threadIdx.x & 63u) == 63u) s_tot[k][wave] = inc;
+  }
+  __syncthreads();
+  uint32_t run = block_base[blockIdx.x];  // first slot of the round
+  uint32_t c = 0;                         // camera of the thread's entries (ascending)
+#pragma unroll
+  for (int k = 0; k < EMIT_ITEMS; ++k) {
+    uint32_t before = 0u, round = 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < 4; ++w) {
+      const uint32_t t = s_tot[k][w];
+      before += w < wave ? t : 0u;
+      round += t;
+    }
+    const uint32_t e = base + (uint32_t)k * 256u + threadIdx.x;
+    if (e < n_entries) {
+      while (c + 1 < C && (uint32_t)s_off[c + 1] <= e) ++c;
+      const uint32_t rc = (uint32_t)(v[k] >> 32);
+      const uint32_t x0 = rc & 255u, x1 = (rc >> 8) & 255u, y0 = (rc >> 16) & 255u,
+                     y1 = rc >> 24;
+      const uint32_t cam_enc = c << tile_n_bits;
+      const int32_t id = (int32_t)(uint32_t)v[k];
+      uint32_t cur = run + before + excl[k];
+      for (uint32_t y = y0; y < y1; ++y)
+        for (uint32_t x = x0; x < x1; ++x) {
+          keys[cur] = cam_enc | (y * tw + x);
+          flatten_ids[cur] = id;
+          ++cur;
+        }
+    }
+    run += round;
+  }
+}
+
 // isect_offset_encode (isect_tiles.cu:234-301) over camera|tile keys.
 #define OFFSET_KEYS 8  // sorted keys per thread of the offset encoder
 
@@ -1052,6 +1137,36 @@ extern "C" int tgs_tide_isect_emit(uint32_t n_entries, const int32_t* cam_offset
                      stream, n_entries, cam_offsets, C, entry_rects, cum_tiles, tile_width,
                      tile_n_bits, keys, flatten_ids);
   TGS_RETURN_LAUNCH("tgs_tide_isect_emit");
+}
+
+extern "C" uint32_t tgs_tide_isect_emit_blocks(uint32_t n_entries) {
+  return (uint32_t)(((uint64_t)n_entries + EMIT_ENTRIES - 1) / EMIT_ENTRIES);
+}
+
+extern "C" int tgs_tide_isect_block_sums(uint32_t n_entries, const uint64_t* entry_rects,
+                                         uint32_t* block_sums, hipStream_t stream) {
+  if (n_entries == 0) return TGS_OK;
+  TGS_CHECK_ARG(entry_rects && block_sums, "tide_isect_block_sums: null");
+  hipLaunchKernelGGL(tide_isect_block_sums_kernel, dim3(tgs_tide_isect_emit_blocks(n_entries)),
+                     dim3(256), 0, stream, n_entries, entry_rects, block_sums);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_block_sums");
+}
+
+extern "C" int tgs_tide_isect_emit_blocked(uint32_t n_entries, const int32_t* cam_offsets,
+                                           uint32_t C, const uint64_t* entry_rects,
+                                           const uint32_t* block_base, uint32_t tile_width,
+                                           uint32_t tile_n_bits, uint32_t* keys,
+                                           int32_t* flatten_ids, hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  if (n_entries == 0) return TGS_OK;
+  TGS_CHECK_ARG(cam_offsets && entry_rects && block_base && keys && flatten_ids,
+                "tide_isect_emit_blocked: null");
+  TGS_CHECK_ARG(tile_n_bits <= 16, "tide_isect_emit_blocked: tile_n_bits must be <= 16");
+  hipLaunchKernelGGL(tide_isect_emit_blocked_kernel, dim3(tgs_tide_isect_emit_blocks(n_entries)),
+                     dim3(256), 0, stream, n_entries, cam_offsets, C, entry_rects, block_base,
+                     tile_width, tile_n_bits, keys, flatten_ids);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_emit_blocked");
 }
 
 extern "C" int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, uint32_t C,

@@ -327,14 +327,17 @@ class TideStep:
             counts_ready = self._record()
 
         # 3. intersections in the reference's (camera, tile, depth, entry) order:
-        #    depth sort of the entries per camera, count + scan, emission in depth
-        #    order, stable sort of the tile bits per camera, bucket offsets
+        #    depth sort of the entries per camera, per-block area sums + scan,
+        #    emission in depth order, stable sort of the tile bits per camera,
+        #    bucket offsets
         cam_segs = _segments([sum(tot[:c]) for c in range(C + 1)])
         dkeys2 = self._buf("depth_keys2", cap_v, torch.int32)
         rects2 = self._buf("entry_rects2", cap_v, torch.int64)
-        tiles = self._buf("tiles", cap_v, torch.int32)
-        cum = self._buf("cum_tiles", cap_v, torch.int64)
-        ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(max(V, 1)), torch.uint8)
+        # emission in blocks of entries: each block's rectangle-area sum, scanned
+        n_eb = lib.tgs_tide_isect_emit_blocks(max(V, 1))
+        eb_sums = self._buf("emit_block_sums", n_eb, torch.int32)
+        eb_base = self._buf("emit_block_base", n_eb, torch.int32)
+        ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(n_eb), torch.uint8)
         self._begin("isect_scan")
         if V:
             sel = ctypes.c_int(0)
@@ -344,8 +347,8 @@ class TideStep:
                    ctypes.byref(sel), s)
             if sel.value:
                 rects = rects2
-            N.call("tgs_tide_isect_count", V, N.ptr(rects), N.ptr(tiles), s)
-            N.call("tgs_inclusive_scan_i32_i64", N.ptr(tiles), N.ptr(cum), V, N.ptr(ws),
+            N.call("tgs_tide_isect_block_sums", V, N.ptr(rects), N.ptr(eb_sums), s)
+            N.call("tgs_exclusive_scan_u32", N.ptr(eb_sums), N.ptr(eb_base), n_eb, N.ptr(ws),
                    ws.numel(), s)
         self._end()
         isects_ready.synchronize()  # host read 2: the depth sort keeps the GPU busy
@@ -364,8 +367,8 @@ class TideStep:
         offsets = self._buf("offsets", n_buckets, torch.int32)
         self._begin("isect_sort")
         if n_isects:
-            N.call("tgs_tide_isect_emit", V, N.ptr(cam_offsets), C, N.ptr(rects), N.ptr(cum), tw,
-                   tile_bits, N.ptr(keys), N.ptr(fids), s)
+            N.call("tgs_tide_isect_emit_blocked", V, N.ptr(cam_offsets), C, N.ptr(rects),
+                   N.ptr(eb_base), tw, tile_bits, N.ptr(keys), N.ptr(fids), s)
             sel = ctypes.c_int(0)
             tws = self._buf("sort_ws2", lib.tgs_segmented_sort_workspace_size(n_isects, C),
                             torch.uint8)
