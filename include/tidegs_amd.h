@@ -321,7 +321,10 @@ int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* masks, const u
  * entry index in the low word; isect_tiles.cu:55-70).  Tile grid at most
  * 255 x 255.  n_touched_dev (device, may be null) holds the touched-row
  * count when the host does not know it yet; n_touched is then the launch's
- * capacity (rows beyond the device count do nothing). */
+ * capacity (rows beyond the device count do nothing).  isect_totals (device,
+ * may be null) receives the per-camera intersection counts [C] (int64, the
+ * sums of the rectangles' areas; the call zeroes it first), so the host can
+ * size the intersection buffers while the depth sort runs. */
 int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touched_dev,
                          const int32_t* touched, const int32_t* visit_base,
                          const int32_t* visits, const uint32_t* masks, uint32_t C,
@@ -331,7 +334,7 @@ int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touched_dev,
                          float far_plane, float radius_clip, int32_t sh_degree,
                          uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
                          float* splats, uint32_t* depth_keys, uint64_t* entry_rects,
-                         tgs_stream_t stream);
+                         int64_t* isect_totals, tgs_stream_t stream);
 /* Intersections of the batch in the order of the reference's sort
  * (isect_tiles.cu:73-98,189-227: camera, tile, depth bits, entry).  After
  * tgs_segmented_sort_pairs_u32 of (depth_keys, entry_rects) per camera:

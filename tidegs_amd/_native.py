@@ -100,7 +100,7 @@ SIGNATURES = {
     "tgs_tide_project_fwd": (
         ctypes.c_int,
         [U32, P, P, P, P, P, U32, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, I32, U32, U32,
-         U32, P, P, P, P]),
+         U32, P, P, P, P, P]),
     "tgs_tide_isect_totals": (ctypes.c_int, [U32, P, P, P, U32, P, P]),
     "tgs_tide_isect_count": (ctypes.c_int, [U32, P, P, P]),
     "tgs_tide_isect_segments": (ctypes.c_int, [U32, P, P, P, P]),

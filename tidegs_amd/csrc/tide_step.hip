@@ -294,8 +294,9 @@ __device__ __forceinline__ uint32_t rect_tiles(uint32_t rc) {
 }
 
 // Projection + SH colour of one (camera, row) entry e into the packed splat
-// record, its depth key and its tile rectangle.
-__device__ __forceinline__ void project_entry(
+// record, its depth key and its tile rectangle; returns the rectangle's area
+// (the entry's intersection count).
+__device__ __forceinline__ uint32_t project_entry(
     const float p[3], const m3& Sigma, float opac, const float* sh, const Cam& cam,
     const float* campos, int W, int H, float eps2d, float near_plane, float far_plane,
     float radius_clip, int sh_degree, uint32_t tile_size, uint32_t tw, uint32_t th, uint32_t e,
@@ -310,7 +311,7 @@ __device__ __forceinline__ void project_entry(
     out[2] = make_float4(0.f, 0.f, 0.f, 0.f);
     depth_keys[e] = 0xffffffffu;
     entry_rects[e] = (uint64_t)e;  // empty rectangle
-    return;
+    return 0u;
   }
   float col[3];
   sh_eval3(sh_degree, p[0] - campos[0], p[1] - campos[1], p[2] - campos[2], sh, col);
@@ -335,11 +336,15 @@ __device__ __forceinline__ void project_entry(
   // depth > near_plane > 0, so the float bits order like the depths
   depth_keys[e] = __float_as_uint(r.depth);
   entry_rects[e] = ((uint64_t)pack_rect(x0, x1, y0, y1) << 32) | e;
+  return (x1 - x0) * (y1 - y0);  // x1 >= x0 and y1 >= y0 (clamped floor / ceil)
 }
 
 // One thread per touched row: the row (59 floats) is read once and projected
 // into every camera it is visible in (its visits, in camera order, are the
-// set bits of its visibility mask); SH coefficients stay in registers.
+// set bits of its visibility mask); SH coefficients stay in registers.  With
+// isect_totals (zeroed by the launch) the per-camera intersection counts are
+// summed too: a wave sum per camera step, LDS counters per workgroup, one
+// 64-bit atomic per camera and workgroup.
 __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
     uint32_t n_touched, const uint32_t* __restrict__ n_touched_dev,
     const int32_t* __restrict__ touched,
@@ -348,13 +353,20 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
     uint32_t row_stride, int W, int H, float eps2d, float near_plane, float far_plane,
     float radius_clip, int sh_degree, uint32_t tile_size, uint32_t tw, uint32_t th,
     float4* __restrict__ splats,
-    uint32_t* __restrict__ depth_keys, uint64_t* __restrict__ entry_rects) {
+    uint32_t* __restrict__ depth_keys, uint64_t* __restrict__ entry_rects,
+    int64_t* __restrict__ isect_totals) {
   __shared__ CamLDS s_cam;
+  __shared__ uint32_t s_area[TIDE_MAX_CAMS];
   load_cams_lds(tc, s_cam);
+  if (threadIdx.x < TIDE_MAX_CAMS) s_area[threadIdx.x] = 0u;
   __syncthreads();
+  const uint32_t limit = n_touched_dev ? min(*n_touched_dev, n_touched) : n_touched;
+  if (blockIdx.x * blockDim.x >= limit) return;  // the whole workgroup
+  // rows past the touched count stay in the loop (empty visibility mask) so
+  // the wave sums run on full wavefronts
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= (n_touched_dev ? min(*n_touched_dev, n_touched) : n_touched)) return;
-  const uint32_t n = (uint32_t)touched[t];
+  const bool active = t < limit;
+  const uint32_t n = active ? (uint32_t)touched[t] : 0u;
   const float* row = params + (uint64_t)n * row_stride;
   const float p[3] = {row[0], row[1], row[2]};
   const m3 Sigma = row_covariance(row);
@@ -362,19 +374,30 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
   float sh[48];
 #pragma unroll
   for (int k = 0; k < 48; ++k) sh[k] = row[11 + k];
-  const uint32_t mask = masks[n];
-  const int32_t* vis = visits + visit_base[t];
+  const uint32_t mask = active ? masks[n] : 0u;
+  const int32_t* vis = visits + (active ? visit_base[t] : 0);
   // cameras in lockstep across the wavefront: the camera's constants are an
   // LDS broadcast, and the lanes seeing camera c write consecutive entries of
   // its list (coalesced records)
   int j = 0;
   for (uint32_t c = 0; c < tc.C; ++c) {
+    uint32_t area = 0u;
     if ((mask >> c) & 1u) {
       const uint32_t e = (uint32_t)vis[j++];
-      project_entry(p, Sigma, opac, sh, s_cam.cam[c], s_cam.campos[c], W, H, eps2d, near_plane,
-                    far_plane, radius_clip, sh_degree, tile_size, tw, th, e, splats, depth_keys,
-                    entry_rects);
+      area = project_entry(p, Sigma, opac, sh, s_cam.cam[c], s_cam.campos[c], W, H, eps2d,
+                           near_plane, far_plane, radius_clip, sh_degree, tile_size, tw, th, e,
+                           splats, depth_keys, entry_rects);
     }
+    if (isect_totals) {
+      const uint32_t wsum = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan(area), 63);
+      if ((threadIdx.x & 63u) == 0u && wsum) atomicAdd(&s_area[c], wsum);
+    }
+  }
+  if (isect_totals) {
+    __syncthreads();
+    if (threadIdx.x < tc.C && s_area[threadIdx.x])
+      atomicAdd((unsigned long long*)&isect_totals[threadIdx.x],
+                (unsigned long long)s_area[threadIdx.x]);
   }
 }
 
@@ -1064,10 +1087,12 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touche
                                     int32_t sh_degree, uint32_t tile_size, uint32_t tile_width,
                                     uint32_t tile_height,
                                     float* splats, uint32_t* depth_keys, uint64_t* entry_rects,
-                                    hipStream_t stream) {
+                                    int64_t* isect_totals, hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;
-  if (n_touched == 0) return TGS_OK;
+  if (isect_totals)
+    hipLaunchKernelGGL(tide_zero_i64_kernel, dim3(1), dim3(64), 0, stream, isect_totals, C);
+  if (n_touched == 0) TGS_RETURN_LAUNCH("tgs_tide_project_fwd");
   TGS_CHECK_ARG(touched && visit_base && visits && masks && params && viewmats && Ks && campos &&
                     splats && depth_keys && entry_rects,
                 "tide_project_fwd: null");
@@ -1083,7 +1108,7 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touche
                      params, row_stride,
                      W, H,
                      eps2d, near_plane, far_plane, radius_clip, sh_degree, tile_size, tile_width,
-                     tile_height, (float4*)splats, depth_keys, entry_rects);
+                     tile_height, (float4*)splats, depth_keys, entry_rects, isect_totals);
   TGS_RETURN_LAUNCH("tgs_tide_project_fwd");
 }
 

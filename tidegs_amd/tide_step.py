@@ -301,18 +301,16 @@ class TideStep:
         splats = self._buf("splats", cap_v * 12, torch.float32)
         dkeys = self._buf("depth_keys", cap_v, torch.int32)
         rects = self._buf("entry_rects", cap_v, torch.int64)
+        # the projection also sums the per-camera intersection counts (the
+        # rectangles' areas); they go to the host while the depth sort runs
+        isect_tot = self._buf("isect_totals", C, torch.int64)
         self._begin("project_fwd")
         N.call("tgs_tide_project_fwd", n, N.ptr(totals) + 4 * C, N.ptr(touched),
                N.ptr(visit_base), N.ptr(visits), N.ptr(masks), C, N.ptr(P), self.row_stride,
                N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H, self.eps2d, self.near, self.far,
                0.0, self.sh_degree, self.TILE, tw, th, N.ptr(splats), N.ptr(dkeys), N.ptr(rects),
-               s)
+               N.ptr(isect_tot), s)
         self._end()
-        # per-camera intersection counts (sums of the rectangles' areas) go to
-        # the host while the depth sort runs
-        isect_tot = self._buf("isect_totals", C, torch.int64)
-        N.call("tgs_tide_isect_totals", cap_v, N.ptr(totals) + 4 * (C + 1), N.ptr(rects),
-               N.ptr(cam_offsets), C, N.ptr(isect_tot), s)
         isect_host = self._pinned("isect_totals", C, torch.int64)
         isect_host.copy_(isect_tot, non_blocking=True)
         isects_ready = self._record()
