@@ -287,7 +287,7 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_hist_kernel(const K* __res
 // (digit, position) order and written out by consecutive threads, so each
 // digit's run of the tile is one contiguous store.
 template <typename K, typename V>
-__global__ void __launch_bounds__(SORT_THREADS) radix_scatter_kernel(
+__global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_eu(4))) radix_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, RadixSegs sg, int shift,
     uint32_t mask, const uint32_t* __restrict__ hist_scan, K* __restrict__ keys_out,
     V* __restrict__ vals_out) {
