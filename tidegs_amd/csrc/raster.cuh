@@ -442,16 +442,17 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
                                 : offs[tile_id + 1];
   const int32_t n_batches = (range_end - range_start + BATCH - 1) / BATCH;
 
-  float T = 1.f;
+  // T > 0 while the pixel composites; a stopped pixel (or one outside the
+  // image) holds -T, so the sign is its done flag and |T| its transmittance
+  float T = inside ? 1.f : -1.f;
   uint32_t cur_idx = 0;
   int32_t n_comp = 0;  // Gaussians composited into this pixel
-  bool done = !inside;
   float pix[CDIM];
 #pragma unroll
   for (int k = 0; k < CDIM; ++k) pix[k] = 0.f;
 
   for (int32_t b = 0; b < n_batches; ++b) {
-    if (__syncthreads_count(done) >= BLOCK) break;
+    if (__syncthreads_count(T < 0.f) >= BLOCK) break;
     const int32_t batch_start = range_start + BATCH * b;
     const int32_t idx = batch_start + (int32_t)tr;
     const bool have = (int)tr < BATCH && idx < range_end;
@@ -468,7 +469,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     }
     __syncthreads();
     const int32_t batch_size = min(BATCH, range_end - batch_start);
-    const uint64_t alive = tgs_ballot(!done);
+    const uint64_t alive = tgs_ballot(T > 0.f);
     if (!alive) continue;
     uint64_t hits;
     const int n_list =
@@ -486,40 +487,37 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
 #pragma unroll
     for (int W = 0; W < WORDS; ++W) {
       if (W * 32 >= n_list) break;
-      uint32_t m = done ? 0u : mw[W];
-      while (true) {
-        // a lane that reaches the threshold clears m, so m != 0 is its
-        // whole loop condition
+      uint32_t m = T < 0.f ? 0u : mw[W];
+      // every lane runs the body (no exec-mask branches): a lane with no
+      // entry left reads staged record 0 and changes nothing; a Gaussian
+      // failing the alpha test, or the one that would take T to the
+      // threshold, adds exactly zero; a lane reaching the threshold clears m
+      if (tgs_ballot(m != 0u)) do {
         const bool act = m != 0u;
-        if (!tgs_ballot(act)) break;
-        if (act) {
-          const int bit = __builtin_ctz(m);
-          m &= m - 1u;
-          const int t = my_list[W * 32 + bit];
-          const StagedRec<CDIM>& rec = s_rec[t];
-          const float4 g0 = rec.g0;
-          const float4 g1 = rec.g1;
-          const float power = raster_power(g0, make_float2(g1.x, g1.y), g0.x - px, g0.y - py);
-          // predicated rather than branched (one exec level in the loop):
-          // a Gaussian failing the alpha test, or the one that would take T
-          // to the threshold, adds exactly zero
-          const bool pass = !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
-          const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
-          const float next_T = T * (1.f - alpha);
-          const bool stop = pass && next_T <= 1e-4f;
-          const bool comp = pass && !stop;
-          m = stop ? 0u : m;
-          done = done || stop;
-          const float vis = comp ? alpha * T : 0.f;
+        const int bit = __builtin_ctz(m | 0x80000000u);  // 31 where m is empty
+        m &= m - 1u;
+        const int te = my_list[W * 32 + bit];
+        const int t = act ? te : 0;
+        const StagedRec<CDIM>& rec = s_rec[t];
+        const float4 g0 = rec.g0;
+        const float4 g1 = rec.g1;
+        const float power = raster_power(g0, make_float2(g1.x, g1.y), g0.x - px, g0.y - py);
+        const bool pass = act && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
+        const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
+        const float next_T = T * (1.f - alpha);
+        const bool stop = pass && next_T <= 1e-4f;
+        const bool comp = pass && !stop;
+        m = stop ? 0u : m;
+        const float vis = comp ? alpha * T : 0.f;
 #pragma unroll
-          for (int k = 0; k < CDIM; ++k) pix[k] = fmaf(rec.col[k], vis, pix[k]);
-          cur_idx = comp ? (uint32_t)(bs_v + t) : cur_idx;
-          if (COUNT) n_comp += comp ? 1 : 0;
-          T = comp ? next_T : T;
-        }
-      }
+        for (int k = 0; k < CDIM; ++k) pix[k] = fmaf(rec.col[k], vis, pix[k]);
+        cur_idx = comp ? (uint32_t)(bs_v + t) : cur_idx;
+        if (COUNT) n_comp += comp ? 1 : 0;
+        T = comp ? next_T : (stop ? -T : T);
+      } while (tgs_ballot(m != 0u));
     }
   }
+  T = fabsf(T);
   if (inside) {
     const uint64_t pid = img + (uint64_t)i * G.W + j;
     render_alphas[pid] = 1.f - T;
