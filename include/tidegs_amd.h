@@ -560,6 +560,16 @@ int tgs_cull_block_spheres(const float* bounds, uint32_t nb, float* centers, flo
 int tgs_cull_blocks(const float* centers, const float* radii, const int64_t* block_ids,
                     uint32_t n, const float* planes, uint32_t C, uint32_t* masks,
                     tgs_stream_t stream);
+/* Legacy cone + distance test of FrustumCuller.cull(use_6plane=False)
+ * (gaussian_block.py:465-510): visible[i] = |centers[i] - cam| <= threshold
+ * and (cosine between (centers[i] - cam) and the unit forward axis > -0.3 or
+ * distance < 1e-6); float64 arithmetic.  The caller passes the normalized
+ * forward axis (view row 2) and threshold = min(scene_radius / 2, 100) *
+ * margin (50 * margin without a scene radius), as the reference computes
+ * them. */
+int tgs_cull_blocks_cone(const float* centers, uint32_t nb, double cam_x, double cam_y,
+                         double cam_z, double fwd_x, double fwd_y, double fwd_z,
+                         double threshold, uint8_t* visible, tgs_stream_t stream);
 
 /* ---- on-disk block store (host code, no GPU) ------------------------------ */
 /* Parallel reads of n blocks of the base/patch files (replaces the per-block

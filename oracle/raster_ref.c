@@ -26,6 +26,10 @@ static REAL rmin(REAL a, REAL b) { return a < b ? a : b; }
 
 static REAL rexp(REAL x) { return (REAL)exp((double)x); }
 
+/* the largest channel count the reference instantiates
+ * (rasterize_to_pixels_fwd.cu:261-283) */
+#define ORACLE_MAX_D 513
+
 /* means2d [*,2], conics [*,3], colors [*,D], opac [*]; offsets [C,th,tw];
  * outputs colors [C,H,W,D], alphas [C,H,W], last_ids [C,H,W]. */
 void FN(oracle_raster_fwd)(int C, int D, const REAL* means2d, const REAL* conics,
@@ -33,7 +37,7 @@ void FN(oracle_raster_fwd)(int C, int D, const REAL* means2d, const REAL* conics
                            int H, int tile, int tw, int th, const int32_t* offsets,
                            const int32_t* flat, int n_isects, REAL* out_colors, REAL* out_alphas,
                            int32_t* last_ids) {
-  REAL pix[64];
+  REAL pix[ORACLE_MAX_D];
   for (int c = 0; c < C; ++c) {
     for (int i = 0; i < H; ++i) {
       for (int j = 0; j < W; ++j) {
@@ -79,7 +83,7 @@ void FN(oracle_raster_bwd)(int C, int D, const REAL* means2d, const REAL* conics
                            const int32_t* last_ids, const REAL* v_out, const REAL* v_alpha_out,
                            double* v_means2d, double* v_conics, double* v_colors, double* v_opac,
                            double* v_abs) {
-  REAL buffer[64], v_rc[64];
+  REAL buffer[ORACLE_MAX_D], v_rc[ORACLE_MAX_D];
   for (int c = 0; c < C; ++c) {
     for (int i = 0; i < H; ++i) {
       for (int j = 0; j < W; ++j) {

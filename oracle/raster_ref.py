@@ -133,7 +133,7 @@ def rasterize_fwd(means2d, conics, colors, opac, W, H, tile_size, offsets, flatt
     flatten_ids = np.ascontiguousarray(flatten_ids, dtype=np.int32)
     C, th, tw = offsets.shape
     D = colors.shape[-1]
-    assert D <= 64
+    assert D <= 513
     out_c = np.zeros((C, H, W, D), dtype=dtype)
     out_a = np.zeros((C, H, W), dtype=dtype)
     last = np.zeros((C, H, W), dtype=np.int32)

@@ -96,8 +96,40 @@ def test_update_block_bounds_then_cull(gpu):
     assert culler.block_radius >= float(r.max()) - 1e-6
     with pytest.raises(ValueError, match="out-of-range"):
         culler.cull_subset(None, eye, eye, [4000])
-    with pytest.raises(NotImplementedError):
-        culler.cull(None, eye, eye, use_6plane=False)
     with pytest.raises(ValueError, match="cameras per launch"):
         culler.cull_masks(np.zeros((33, 6, 4), np.float32))
     assert np.array_equal(extract_frustum_planes(eye, eye), K.planes(eye, eye))
+
+
+@pytest.mark.parametrize("scene_radius,margin", [(None, 1.0), (60.0, 1.3), (500.0, 0.5)])
+def test_legacy_cone_cull(gpu, scene_radius, margin):
+    """cull(use_6plane=False) and cull_subset(use_6plane=False) against the
+    oracle's restatement of the reference's legacy cone + distance test; the
+    float64 kernel and the reference's numpy expressions agree everywhere
+    except within rounding of the two thresholds, which the blocks here
+    avoid by construction (they are checked to stay clear of them)."""
+    announce(f"legacy cone culling scene_radius={scene_radius} margin={margin}")
+    rng = np.random.default_rng(5)
+    b = _blocks(6, 20000, lo=-120.0, hi=120.0)
+    culler = FrustumCuller(b, scene_radius=scene_radius, device=gpu)
+    c, _ = K.spheres(b)
+    cam = np.array([3.0, -2.0, 5.0], dtype=np.float32)
+    view = np.eye(4, dtype=np.float32)
+    view[:3, :3] = np.linalg.qr(rng.standard_normal((3, 3)))[0].astype(np.float32)
+    reach = (min(scene_radius * 0.5, 100.0) if scene_radius is not None else 50.0) * margin
+    axis = view[2, :3].astype(np.float64)
+    axis /= np.linalg.norm(axis)
+    rel = c.astype(np.float64) - cam
+    dist = np.linalg.norm(rel, axis=1)
+    cosine = rel @ axis / dist
+    clear = (np.abs(dist - reach) > 1e-4 * reach) & (np.abs(cosine + 0.3) > 1e-5)
+    assert clear.mean() > 0.99
+    got = np.zeros(len(c), bool)
+    got[culler.cull(cam, view, None, margin=margin, use_6plane=False)] = True
+    ref = np.zeros(len(c), bool)
+    ref[K.cone(c, cam, view, scene_radius=scene_radius, margin=margin)] = True
+    np.testing.assert_array_equal(got[clear], ref[clear])
+    assert 0 < got.sum() < len(c)
+    ids = rng.choice(len(c), 500, replace=False)
+    sub = culler.cull_subset(cam, view, None, ids, margin=margin, use_6plane=False)
+    assert sub == [int(i) for i in ids if got[i]]

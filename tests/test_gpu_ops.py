@@ -308,8 +308,13 @@ def _raster_case(gpu, seed, C=2, D=3, W=200, H=120, tile=16, packed=False):
 @pytest.mark.parametrize("D,tile,bg,packed,absgrad", [
     (3, 16, False, False, False), (3, 16, True, False, True), (1, 16, False, False, False),
     (4, 8, True, False, False), (5, 16, False, False, False), (32, 16, False, True, False),
-    (3, 16, False, True, True)])
+    (3, 16, False, True, True), (33, 16, True, False, False), (64, 16, False, True, False),
+    (65, 8, True, False, False)])
 def test_rasterize_fwd_bwd(gpu, D, tile, bg, packed, absgrad):
+    """Drop-in rasterize_to_pixels forward and backward against the oracle's
+    restatement of rasterize_to_pixels_fwd/bwd.cu, over channel counts the
+    kernels instantiate, padded ones (5) and ones run in 32-channel launches
+    (33, 64, 65)."""
     announce(f"raster D={D} tile={tile} bg={bg} packed={packed} absgrad={absgrad}")
     C, W, H = 2, 200, 120
     m2d, conics, colors, opacs, offs, flat = _raster_case(gpu, seed=10 + D, C=C, D=D, W=W, H=H,
@@ -365,6 +370,47 @@ def test_fused_ssim(gpu):
     assert rel_l2(to_np(da.grad), ref) < 1e-5
     val = fused_ssim(a.to(gpu), b.to(gpu), padding="valid")
     assert abs(float(val) - float(rm[:, :, 5:-5, 5:-5].mean())) < 1e-5
+
+
+@pytest.mark.parametrize("D,tile,bg", [(3, 16, True), (4, 16, False), (40, 8, True)])
+def test_rasterize_masks(gpu, D, tile, bg):
+    """Tile masks: a skipped tile's pixels hold the background (zero without
+    one) with alpha 0 and pass no gradient; the other pixels and all gradients
+    equal the oracle's with the skipped pixels' output gradients zeroed."""
+    announce(f"raster masks D={D} tile={tile} bg={bg}")
+    C, W, H = 2, 200, 120
+    m2d, conics, colors, opacs, offs, flat = _raster_case(gpu, seed=70 + D, C=C, D=D, W=W, H=H,
+                                                          tile=tile, packed=False)
+    g = torch.Generator().manual_seed(7 + D)
+    bgs = torch.rand((C, D), generator=g).to(gpu) if bg else None
+    th, tw = offs.shape[1], offs.shape[2]
+    masks = torch.rand((C, th, tw), generator=g) > 0.3
+    leaves = [t.clone().requires_grad_() for t in (m2d, conics, colors, opacs)]
+    rc, ra = ops.rasterize_to_pixels(*leaves, W, H, tile, offs, flat, backgrounds=bgs,
+                                     masks=masks.to(gpu))
+    ref_c, ref_a, ref_last = R.rasterize_fwd(
+        to_np(m2d).reshape(-1, 2), to_np(conics).reshape(-1, 3), to_np(colors).reshape(-1, D),
+        to_np(opacs).reshape(-1), W, H, tile, to_np(offs), to_np(flat),
+        backgrounds=to_np(bgs) if bg else None)
+    pm = masks.numpy().repeat(tile, 1).repeat(tile, 2)[:, :H, :W]
+    exp_c = np.where(pm[..., None], ref_c, to_np(bgs)[:, None, None, :] if bg else 0.0)
+    exp_a = np.where(pm, ref_a, 0.0)
+    assert rel_l2(to_np(rc), exp_c) < 1e-5
+    np.testing.assert_array_equal(to_np(ra)[..., 0][~pm], 0.0)
+    assert rel_l2(to_np(ra)[..., 0], exp_a) < 1e-5
+    wc = torch.randn(rc.shape, generator=g)
+    wa = torch.randn(ra.shape, generator=g)
+    ((rc * wc.to(gpu)).sum() + (ra * wa.to(gpu)).sum()).backward()
+    wc_m = to_np(wc) * pm[..., None]
+    wa_m = to_np(wa)[..., 0] * pm
+    vm, vc, vcol, vo, _ = R.rasterize_bwd(
+        to_np(m2d).reshape(-1, 2), to_np(conics).reshape(-1, 3), to_np(colors).reshape(-1, D),
+        to_np(opacs).reshape(-1), W, H, tile, to_np(offs), to_np(flat), ref_a, ref_last,
+        wc_m, v_alphas=wa_m, backgrounds=to_np(bgs) if bg else None)
+    assert rel_l2(to_np(leaves[0].grad).reshape(-1, 2), vm) < 1e-4
+    assert rel_l2(to_np(leaves[1].grad).reshape(-1, 3), vc) < 1e-4
+    assert rel_l2(to_np(leaves[2].grad).reshape(-1, D), vcol) < 1e-4
+    assert rel_l2(to_np(leaves[3].grad).reshape(-1), vo) < 1e-4
 
 
 @pytest.mark.parametrize("B,H,W", [(1, 70, 130), (2, 37, 21)])

@@ -1,6 +1,7 @@
-"""Host-side index-width guards of the fused step (tidegs_amd.tide_step): a
-batch whose 32-bit entry/visit counts or int32 intersection ranges would wrap
-is refused before any launch (checked on synthetic totals; no GPU)."""
+"""Host-side guards, checked without a GPU: the fused step's index widths
+(tidegs_amd.tide_step: a batch whose 32-bit entry/visit counts or int32
+intersection ranges would wrap is refused before any launch, on synthetic
+totals) and the drop-in rasterizer's launch plan and refusals."""
 import pytest
 
 from tidegs_amd.tide_step import MAX_ISECTS, check_batch_capacity, check_isect_count
@@ -22,3 +23,28 @@ def test_isect_count():
     for bad in (MAX_ISECTS + 1, 1 << 32, -1):
         with pytest.raises(RuntimeError, match="int32"):
             check_isect_count(bad)
+
+
+def test_rasterize_absgrad_above_32_channels_refused():
+    """|dL/dmean2d| needs every channel's share of dL/dalpha in one launch, so
+    the drop-in refuses absgrad above 32 channels before touching the GPU."""
+    import torch
+    from tidegs_amd import gsplat_ops as ops
+    C, n, D = 1, 4, 40
+    with pytest.raises(NotImplementedError, match="absgrad"):
+        ops.rasterize_to_pixels(torch.zeros(C, n, 2), torch.zeros(C, n, 3), torch.zeros(C, n, D),
+                                torch.zeros(C, n), 32, 32, 16,
+                                torch.zeros(C, 2, 2, dtype=torch.int32),
+                                torch.zeros(0, dtype=torch.int32), absgrad=True)
+
+
+def test_channel_chunks():
+    """Launch plan of the drop-in rasterizer: one launch (padded to an
+    instantiated count) up to 32 channels, runs of 32 above."""
+    from tidegs_amd.gsplat_ops import _channel_chunks
+    assert _channel_chunks(3) == [(0, 3, 3)]
+    assert _channel_chunks(5) == [(0, 5, 8)]
+    assert _channel_chunks(32) == [(0, 32, 32)]
+    assert _channel_chunks(33) == [(0, 32, 32), (32, 1, 1)]
+    assert _channel_chunks(45) == [(0, 32, 32), (32, 13, 16)]
+    assert _channel_chunks(513)[-1] == (512, 1, 1) and len(_channel_chunks(513)) == 17

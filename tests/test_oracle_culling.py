@@ -65,3 +65,22 @@ def test_perspective_planes_and_float64_agreement():
     tie = np.abs(margin).min(axis=1) < 1e-4
     assert len(got) > 100
     assert {i for i in got ^ want if not tie[i]} == set()
+
+
+def test_legacy_cone_closed_form():
+    """The legacy cone + distance test on blocks whose answer is fixed by
+    geometry: camera at the origin looking down +z (view row 2 = +z), reach
+    50 (no scene radius): ahead within reach visible, ahead beyond it not,
+    straight behind not, at the camera visible, and across the cosine -0.3
+    boundary of a known direction."""
+    view = np.eye(4, dtype=np.float32)
+    cam = np.zeros(3, dtype=np.float32)
+    s = np.sqrt(1.0 - 0.31 ** 2)
+    centers = np.array([[0, 0, 10], [0, 0, 49], [0, 0, 51], [0, 0, -10], [0, 0, 0],
+                        [s * 20, 0, -0.29 * 20], [s * 20, 0, -0.31 * 20], [40, 0, 0]],
+                       dtype=np.float32)
+    assert K.cone(centers, cam, view) == [0, 1, 4, 5, 7]
+    # the reach scales with the margin and follows min(scene_radius / 2, 100)
+    assert K.cone(centers, cam, view, margin=1.1) == [0, 1, 2, 4, 5, 7]
+    assert K.cone(centers, cam, view, scene_radius=30.0) == [0, 4]
+    assert K.cone(centers, cam, view, scene_radius=1000.0) == [0, 1, 2, 4, 5, 7]

@@ -150,6 +150,7 @@ SIGNATURES = {
     "tgs_init_pack_rows": (ctypes.c_int, [P, P, P, P, P, F32, U64, P, P]),
     "tgs_cull_block_spheres": (ctypes.c_int, [P, U32, P, P, P]),
     "tgs_cull_blocks": (ctypes.c_int, [P, P, P, U32, P, U32, P, P]),
+    "tgs_cull_blocks_cone": (ctypes.c_int, [P, U32] + [ctypes.c_double] * 7 + [P, P]),
 }
 
 

@@ -160,20 +160,39 @@ class FrustumCuller:
                 out.append(np.nonzero(m & np.uint32(1 << c))[0].tolist())
         return out
 
+    def cone_flags(self, camera_position, view_matrix, margin: float = 1.0) -> torch.Tensor:
+        """Device uint8 flags of the legacy cone + distance test
+        (gaussian_block.py:465-510) for every block: within
+        min(scene_radius / 2, 100) * margin of the camera (50 * margin without
+        a scene radius) and either at it or at a cosine > -0.3 from its
+        forward axis (view row 2)."""
+        max_view_distance = (min(self.scene_radius * 0.5, 100.0) if self.scene_radius is not None
+                             else 50.0)
+        threshold = max_view_distance * margin
+        fwd = np.asarray(view_matrix, dtype=np.float64)[2, :3]
+        fwd = fwd / (np.linalg.norm(fwd) + 1e-8)
+        cam = np.asarray(camera_position, dtype=np.float64).reshape(3)
+        flags = torch.empty(self.num_blocks, dtype=torch.uint8, device=self.device)
+        with self._lock:
+            N.call("tgs_cull_blocks_cone", N.ptr(self.centers), self.num_blocks, float(cam[0]),
+                   float(cam[1]), float(cam[2]), float(fwd[0]), float(fwd[1]), float(fwd[2]),
+                   float(threshold), N.ptr(flags), N.stream_handle(self.device))
+        return flags
+
     def cull(self, camera_position, view_matrix, projection_matrix, margin: float = 1.0,
              use_6plane: bool = True) -> List[int]:
-        """Visible blocks of one camera, ascending (gaussian_block.py:341-354)."""
+        """Visible blocks of one camera, ascending (gaussian_block.py:341-354);
+        ``use_6plane=False`` runs the legacy cone + distance test."""
         if not use_6plane:
-            raise NotImplementedError("only the 6-plane test is provided (the reference's "
-                                      "default, arguments/__init__.py:311)")
+            flags = self.cone_flags(camera_position, view_matrix, margin)
+            return torch.nonzero(flags).flatten().cpu().tolist()
         return self.cull_batch([view_matrix], [projection_matrix])[0]
 
     def cull_subset(self, camera_position, view_matrix, projection_matrix, block_ids,
                     margin: float = 1.0, use_6plane: bool = True) -> List[int]:
         """The 6-plane test on ``block_ids`` only, in their given order
-        (gaussian_block.py:356-399)."""
-        if not use_6plane:
-            raise NotImplementedError("only the 6-plane test is provided")
+        (gaussian_block.py:356-399); ``use_6plane=False`` keeps the ids the
+        legacy full-scene test finds visible, in their given order."""
         if isinstance(block_ids, set):
             block_ids = sorted(block_ids)
         ids = np.asarray(block_ids, dtype=np.int64)
@@ -181,6 +200,9 @@ class FrustumCuller:
             return []
         if np.any(ids < 0) or np.any(ids >= self.num_blocks):
             raise ValueError("block_ids contains an out-of-range block")
+        if not use_6plane:
+            flags = self.cone_flags(camera_position, view_matrix, margin).cpu().numpy()
+            return ids[flags[ids] != 0].tolist()
         planes = extract_frustum_planes(view_matrix, projection_matrix)[None]
         m = self.cull_masks(planes, block_ids=ids).cpu().numpy()
         return ids[m != 0].tolist()

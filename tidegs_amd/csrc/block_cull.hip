@@ -91,7 +91,38 @@ __global__ __launch_bounds__(CULL_THREADS) void cull_blocks_kernel(
   masks[i] = bits;
 }
 
+// Legacy cone + distance test (gaussian_block.py:465-510): block i is
+// visible when |c_i - cam| <= threshold and either the direction to it has
+// cosine > -0.3 with the camera's forward axis or it sits at the camera
+// (distance < 1e-6).  Evaluated in float64, so its decisions equal the
+// reference's numpy evaluation except within rounding of the two thresholds.
+__global__ __launch_bounds__(CULL_THREADS) void cull_cone_kernel(
+    const float* __restrict__ centers, uint32_t nb, double cx, double cy, double cz, double fx,
+    double fy, double fz, double threshold, uint8_t* __restrict__ visible) {
+  const uint32_t i = blockIdx.x * CULL_THREADS + threadIdx.x;
+  if (i >= nb) return;
+  const double tx = (double)centers[3 * (uint64_t)i] - cx;
+  const double ty = (double)centers[3 * (uint64_t)i + 1] - cy;
+  const double tz = (double)centers[3 * (uint64_t)i + 2] - cz;
+  const double dist = sqrt(tx * tx + ty * ty + tz * tz);
+  const double rn = 1.0 / (dist + 1e-8);
+  const double dot = tx * rn * fx + ty * rn * fy + tz * rn * fz;
+  visible[i] = (uint8_t)(dist <= threshold && (dot > -0.3 || dist < 1e-6));
+}
+
 }  // namespace
+
+extern "C" int tgs_cull_blocks_cone(const float* centers, uint32_t nb, double cam_x, double cam_y,
+                                    double cam_z, double fwd_x, double fwd_y, double fwd_z,
+                                    double threshold, uint8_t* visible, hipStream_t stream) {
+  const char* name = "tgs_cull_blocks_cone";
+  if (nb == 0) return TGS_OK;
+  TGS_CHECK_ARG(centers && visible, "%s: null pointer", name);
+  hipLaunchKernelGGL(cull_cone_kernel, dim3(tgs_blocks(nb, CULL_THREADS)), dim3(CULL_THREADS), 0,
+                     stream, centers, nb, cam_x, cam_y, cam_z, fwd_x, fwd_y, fwd_z, threshold,
+                     visible);
+  TGS_RETURN_LAUNCH(name);
+}
 
 extern "C" int tgs_cull_block_spheres(const float* bounds, uint32_t nb, float* centers,
                                       float* radii, hipStream_t stream) {

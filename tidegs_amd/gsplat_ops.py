@@ -27,6 +27,37 @@ from torch import Tensor
 from . import _native as N
 
 _SUPPORTED_CHANNELS = (1, 2, 3, 4, 8, 16, 32)
+_CHUNK = 32  # channels per launch above 32
+
+
+def _pad_channels(ch: int) -> int:
+    """The smallest instantiated channel count >= ch (ch <= 32)."""
+    return next(d for d in _SUPPORTED_CHANNELS if d >= ch)
+
+
+def _pad_last(t: Optional[Tensor], width: int) -> Optional[Tensor]:
+    """``t`` zero-padded along its last dimension to ``width`` (contiguous)."""
+    if t is None:
+        return None
+    if t.shape[-1] == width:
+        return t.contiguous()
+    pad = torch.zeros(*t.shape[:-1], width - t.shape[-1], dtype=t.dtype, device=t.device)
+    return torch.cat([t, pad], -1).contiguous()
+
+
+def _channel_chunks(ch: int):
+    """(first channel, channels, launched channels) of each launch: one launch
+    up to 32 channels, else consecutive runs of 32 and a padded remainder."""
+    if ch <= _CHUNK:
+        return [(0, ch, _pad_channels(ch))]
+    return [(s, min(_CHUNK, ch - s), _pad_channels(min(_CHUNK, ch - s)))
+            for s in range(0, ch, _CHUNK)]
+
+
+def _pixel_mask(masks: Tensor, tile_size: int, height: int, width: int) -> Tensor:
+    """[C, H, W] bool: the tile mask of every pixel."""
+    m = masks.to(torch.bool)
+    return m.repeat_interleave(tile_size, 1).repeat_interleave(tile_size, 2)[:, :height, :width]
 
 
 def _stream() -> int:
@@ -397,45 +428,76 @@ def _packed_splats(means2d, conics, colors, opacities) -> Tensor:
 
 class _RasterizeToPixels(torch.autograd.Function):
     """3 channels at tile 16 without absgrad (TideGS's case) run the packed
-    record kernels; every other shape runs the SoA kernels."""
+    record kernels; every other shape runs the SoA kernels, other channel
+    counts zero-padded to an instantiated one.  Above 32 channels the kernels
+    run once per run of 32 channels: compositing (T, alphas, last ids) is the
+    same in every launch, the colour outputs and gradients are per launch, and
+    the geometry gradients, linear in each channel's share of dL/dalpha,
+    accumulate over the launches (dL/dalpha and the background term enter
+    the first launch only).  ``masks`` [C, tile rows, tile columns] (False =
+    skip the tile): the tile's pixels take the background (or zero) with
+    alpha 0 and pass no gradient."""
 
     @staticmethod
     def forward(ctx, means2d, conics, colors, opacities, backgrounds, width, height, tile_size,
-                isect_offsets, flatten_ids, absgrad):
+                isect_offsets, flatten_ids, absgrad, masks):
         C = isect_offsets.shape[0]
         th, tw = isect_offsets.shape[1], isect_offsets.shape[2]
         ch = colors.shape[-1]
         dev = means2d.device
-        render_colors = torch.empty((C, height, width, ch), dtype=torch.float32, device=dev)
         render_alphas = torch.empty((C, height, width, 1), dtype=torch.float32, device=dev)
         last_ids = torch.empty((C, height, width), dtype=torch.int32, device=dev)
         records = None
         if ch == 3 and tile_size == 16 and not absgrad:
+            render_colors = torch.empty((C, height, width, ch), dtype=torch.float32, device=dev)
             records = _packed_splats(means2d, conics, colors, opacities)
             N.call("tgs_tide_rasterize_fwd", C, N.ptr(records), N.ptr(backgrounds), width, height,
                    tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids), flatten_ids.numel(),
                    N.ptr(render_colors), N.ptr(render_alphas), N.ptr(last_ids), None, None, 0,
                    _stream())
         else:
-            N.call("tgs_rasterize_to_pixels_fwd", C, ch, N.ptr(means2d), N.ptr(conics),
-                   N.ptr(colors), N.ptr(opacities), N.ptr(backgrounds), width, height, tile_size,
-                   tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids), flatten_ids.numel(),
-                   N.ptr(render_colors), N.ptr(render_alphas), N.ptr(last_ids), _stream())
+            outs = []
+            for s0, w, cw in _channel_chunks(ch):
+                col = _pad_last(colors[..., s0:s0 + w], cw)
+                bg = _pad_last(backgrounds[:, s0:s0 + w], cw) if backgrounds is not None else None
+                rc = torch.empty((C, height, width, cw), dtype=torch.float32, device=dev)
+                N.call("tgs_rasterize_to_pixels_fwd", C, cw, N.ptr(means2d), N.ptr(conics),
+                       N.ptr(col), N.ptr(opacities), N.ptr(bg), width, height, tile_size,
+                       tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids), flatten_ids.numel(),
+                       N.ptr(rc), N.ptr(render_alphas), N.ptr(last_ids), _stream())
+                outs.append(rc if cw == w else rc[..., :w])
+            render_colors = outs[0] if len(outs) == 1 else torch.cat(outs, -1)
+            render_colors = render_colors.contiguous()
+        kernel_alphas = render_alphas
+        pmask = None
+        if masks is not None:
+            pmask = _pixel_mask(masks, tile_size, height, width)
+            fill = (backgrounds[:, None, None, :] if backgrounds is not None
+                    else torch.zeros((), dtype=torch.float32, device=dev))
+            render_colors = torch.where(pmask[..., None], render_colors, fill)
+            render_alphas = torch.where(pmask[..., None], render_alphas,
+                                        torch.zeros((), dtype=torch.float32, device=dev))
         ctx.save_for_backward(means2d, conics, colors, opacities, backgrounds, isect_offsets,
-                              flatten_ids, render_alphas, last_ids, records)
+                              flatten_ids, kernel_alphas, render_alphas, last_ids, records, pmask)
         ctx.width, ctx.height, ctx.tile_size, ctx.absgrad = width, height, tile_size, absgrad
         return render_colors, render_alphas
 
     @staticmethod
     def backward(ctx, v_render_colors, v_render_alphas):
         (means2d, conics, colors, opacities, backgrounds, isect_offsets, flatten_ids,
-         render_alphas, last_ids, records) = ctx.saved_tensors
+         render_alphas, out_alphas, last_ids, records, pmask) = ctx.saved_tensors
         C = isect_offsets.shape[0]
         th, tw = isect_offsets.shape[1], isect_offsets.shape[2]
         ch = colors.shape[-1]
         v_render_colors = (torch.zeros((C, ctx.height, ctx.width, ch), device=means2d.device)
                            if v_render_colors is None else v_render_colors.contiguous())
+        v_out_colors = v_render_colors
         v_render_alphas = None if v_render_alphas is None else v_render_alphas.contiguous()
+        if pmask is not None:
+            # a skipped tile's pixels do not depend on the Gaussians
+            v_render_colors = (v_render_colors * pmask[..., None]).contiguous()
+            if v_render_alphas is not None:
+                v_render_alphas = (v_render_alphas * pmask[..., None]).contiguous()
         v_means2d = torch.zeros_like(means2d)
         v_conics = torch.zeros_like(conics)
         v_colors = torch.zeros_like(colors)
@@ -451,20 +513,28 @@ class _RasterizeToPixels(torch.autograd.Function):
             N.call("tgs_unpack_splat_grads", n, N.ptr(grads), N.ptr(v_means2d), N.ptr(v_conics),
                    N.ptr(v_colors), N.ptr(v_opacities), _stream())
         else:
-            N.call("tgs_rasterize_to_pixels_bwd", C, ch, N.ptr(means2d), N.ptr(conics),
-                   N.ptr(colors), N.ptr(opacities), N.ptr(backgrounds), ctx.width, ctx.height,
-                   ctx.tile_size, tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids),
-                   flatten_ids.numel(), N.ptr(render_alphas), N.ptr(last_ids),
-                   N.ptr(v_render_colors), N.ptr(v_render_alphas), N.ptr(v_abs),
-                   N.ptr(v_means2d), N.ptr(v_conics), N.ptr(v_colors), N.ptr(v_opacities),
-                   _stream())
+            for j, (s0, w, cw) in enumerate(_channel_chunks(ch)):
+                col = _pad_last(colors[..., s0:s0 + w], cw)
+                bg = _pad_last(backgrounds[:, s0:s0 + w], cw) if backgrounds is not None else None
+                vrc = _pad_last(v_render_colors[..., s0:s0 + w], cw)
+                vcol = v_colors if cw == ch else torch.zeros(
+                    (*colors.shape[:-1], cw), dtype=torch.float32, device=means2d.device)
+                N.call("tgs_rasterize_to_pixels_bwd", C, cw, N.ptr(means2d), N.ptr(conics),
+                       N.ptr(col), N.ptr(opacities), N.ptr(bg), ctx.width, ctx.height,
+                       ctx.tile_size, tw, th, N.ptr(isect_offsets), N.ptr(flatten_ids),
+                       flatten_ids.numel(), N.ptr(render_alphas), N.ptr(last_ids),
+                       N.ptr(vrc), N.ptr(v_render_alphas if j == 0 else None), N.ptr(v_abs),
+                       N.ptr(v_means2d), N.ptr(v_conics), N.ptr(vcol), N.ptr(v_opacities),
+                       _stream())
+                if vcol is not v_colors:
+                    v_colors[..., s0:s0 + w] = vcol[..., :w]
         if ctx.absgrad:
             ctx.saved_tensors[0].absgrad = v_abs
         v_backgrounds = None
         if ctx.needs_input_grad[4]:
-            v_backgrounds = (v_render_colors * (1.0 - render_alphas)).sum(dim=(1, 2))
+            v_backgrounds = (v_out_colors * (1.0 - out_alphas)).sum(dim=(1, 2))
         return (v_means2d, v_conics, v_colors, v_opacities, v_backgrounds, None, None, None,
-                None, None, None)
+                None, None, None, None)
 
 
 def rasterize_to_pixels(
@@ -485,11 +555,13 @@ def rasterize_to_pixels(
     """Alpha-composite sorted Gaussians into pixels (gsplat rasterize_to_pixels).
 
     Returns ``(render_colors [C,H,W,D], render_alphas [C,H,W,1])``
-    (``engine.py:550-561``).  Channel counts outside {1,2,3,4,8,16,32} are
-    zero-padded to the next supported count and sliced back.
+    (``engine.py:550-561``).  Any channel count: up to 32 the kernels run at the
+    next instantiated count (zero-padded channels, sliced back), above 32 once
+    per run of 32 channels (the reference instantiates 1-5, 8, 9, 16, 17, 32,
+    33, ... 512, 513: ``rasterize_to_pixels_fwd.cu:261-283``).  ``masks``
+    [C, tile rows, tile columns]: tiles marked False render the background
+    with alpha 0 and pass no gradient.
     """
-    if masks is not None:
-        raise NotImplementedError("tile masks are not part of the reference kernel this mirrors")
     C = isect_offsets.shape[0]
     ch = colors.shape[-1]
     if packed:
@@ -498,19 +570,15 @@ def rasterize_to_pixels(
         assert means2d.shape[0] == C and colors.shape[:2] == means2d.shape[:2]
     if backgrounds is not None:
         assert backgrounds.shape == (C, ch), backgrounds.shape
-    pad = 0
-    if ch not in _SUPPORTED_CHANNELS:
-        target = next((d for d in _SUPPORTED_CHANNELS if d > ch), None)
-        if target is None:
-            raise RuntimeError(f"rasterize_to_pixels: {ch} channels exceeds 32")
-        pad = target - ch
-        colors = torch.cat([colors, torch.zeros(*colors.shape[:-1], pad, device=colors.device)], -1)
-        if backgrounds is not None:
-            backgrounds = torch.cat(
-                [backgrounds, torch.zeros(*backgrounds.shape[:-1], pad, device=backgrounds.device)], -1)
+    if absgrad and ch > _CHUNK:
+        # |dL/dmean2d| per pixel needs every channel's share of dL/dalpha at once
+        raise NotImplementedError("rasterize_to_pixels: absgrad with more than 32 channels")
     tile_width = math.ceil(image_width / float(tile_size))
     tile_height = math.ceil(image_height / float(tile_size))
     assert isect_offsets.shape == (C, tile_height, tile_width), isect_offsets.shape
+    if masks is not None:
+        assert masks.shape == (C, tile_height, tile_width), masks.shape
+        masks = masks.to(means2d.device)
     means2d, conics, colors, opacities = (t.contiguous() for t in (means2d, conics, colors, opacities))
     backgrounds = backgrounds.contiguous() if backgrounds is not None else None
     isect_offsets = isect_offsets.contiguous()
@@ -518,9 +586,6 @@ def rasterize_to_pixels(
     N.require_cuda(means2d, conics, colors, opacities, backgrounds, isect_offsets, flatten_ids,
                    names=["means2d", "conics", "colors", "opacities", "backgrounds",
                           "isect_offsets", "flatten_ids"])
-    render_colors, render_alphas = _RasterizeToPixels.apply(
+    return _RasterizeToPixels.apply(
         means2d, conics, colors, opacities, backgrounds, int(image_width), int(image_height),
-        int(tile_size), isect_offsets, flatten_ids, absgrad)
-    if pad:
-        render_colors = render_colors[..., :ch]
-    return render_colors, render_alphas
+        int(tile_size), isect_offsets, flatten_ids, absgrad, masks)
