@@ -190,6 +190,18 @@ int tgs_segmented_sort_pairs_u32(uint32_t* keys, void* vals, uint32_t* keys_alt,
                                  const uint32_t* seg_offsets, int begin_bit, int end_bit,
                                  void* workspace, size_t workspace_bytes, int* selector,
                                  tgs_stream_t stream);
+/* The same sort on key_bits bits of min(key - key_base, 2^key_bits - 1), keys
+ * below key_base counting as key_base: when the keys lie in [key_base,
+ * key_base + 2^key_bits - 1) this is their full order in fewer or narrower
+ * passes, and keys above the range (a sentinel such as 0xffffffff) all tie
+ * after it in input order.  No counterpart in the reference (its sort takes
+ * a bit range only); used by the fused step's depth sort. */
+int tgs_segmented_sort_pairs_u32_range(uint32_t* keys, void* vals, uint32_t* keys_alt,
+                                       void* vals_alt, uint32_t value_bytes, uint64_t n,
+                                       uint32_t n_segments, const uint32_t* seg_offsets,
+                                       uint32_t key_base, int key_bits, void* workspace,
+                                       size_t workspace_bytes, int* selector,
+                                       tgs_stream_t stream);
 /* Replaces isect_offset_encode_tensor (isect_tiles.cu:234-301); offsets [C,th,tw]. */
 int tgs_isect_offset_encode(uint64_t n_isects, const int64_t* isect_ids, uint32_t C,
                             uint32_t tile_width, uint32_t tile_height, int32_t* offsets,
@@ -298,12 +310,15 @@ int tgs_tide_camera_centers(uint32_t C, const float* viewmats, float* campos, tg
 uint32_t tgs_tide_row_blocks(uint64_t n_rows);
 /* Packed-projection visibility (gsplat fully_fused_projection_packed_fwd.cu:
  * 50-131) of every row in every camera: masks [N] (bit c = camera c), and
- * per-block counts [(C+2)*nb] (per camera, touched rows, visits). */
+ * per-block counts [(C+2)*nb] (per camera, touched rows, visits).  With
+ * depth_range (device, may be null; 128 uint32), 64 {min, max} pairs whose
+ * min over the mins and max over the maxes are the smallest and largest float
+ * bits of the visible entries' depths (pairs that saw none hold {~0, 0}). */
 int tgs_tide_visibility(uint64_t n_rows, const float* params, uint32_t row_stride, uint32_t C,
                         const float* viewmats, const float* Ks, const float* campos, int32_t W,
                         int32_t H, float eps2d,
                         float near_plane, float far_plane, float radius_clip, uint32_t* masks,
-                        uint32_t* counts, tgs_stream_t stream);
+                        uint32_t* counts, uint32_t* depth_range, tgs_stream_t stream);
 /* Compaction from offs = exclusive scan of counts: entries (concatenated
  * per-camera filters, ascending rows, base_engine.py:388-425), touched rows,
  * visit lists per touched row (entries in camera order), totals [C+3]

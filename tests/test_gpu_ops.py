@@ -285,6 +285,52 @@ def test_segmented_sort_pairs_u32(gpu, segs, bits, vbytes):
         np.testing.assert_array_equal(vo[a:b], vals[order])
 
 
+@pytest.mark.parametrize("segs,key_bits", [([0, 70_000], 25), ([0, 5000, 5000, 90_000, 131_073], 19),
+                                           ([0, 40_000], 32)])
+def test_segmented_sort_pairs_u32_range(gpu, segs, key_bits):
+    """The range form sorts keys in [base, base + 2^bits - 1) into the same
+    order as a full stable sort, with the 0xffffffff sentinels (culled depth
+    entries) tied after them in input order and keys below the base first."""
+    import ctypes
+    from tidegs_amd import _native as N
+    announce(f"segmented range sort segs={segs} bits={key_bits}")
+    n = segs[-1]
+    rng = np.random.default_rng(n + key_bits)
+    base = 0x41200000 if key_bits < 32 else 0
+    span = (1 << key_bits) - 1 if key_bits < 32 else 0xFFFFFFFF
+    keys = (base + rng.integers(0, span, size=n, dtype=np.uint64)).astype(np.uint32)
+    keys[: n // 4] = keys[n // 4: 2 * (n // 4)]  # duplicates exercise stability
+    keys[rng.random(n) < 0.05] = 0xFFFFFFFF
+    if key_bits < 32:
+        keys[rng.random(n) < 0.01] = base - 7  # below the range: ranked as the base
+    vals = np.arange(n, dtype=np.int64) * 5 + (1 << 40)
+    k = torch.from_numpy(keys.view(np.int32)).to(gpu)
+    v = torch.from_numpy(vals).to(gpu)
+    k2, v2 = torch.empty_like(k), torch.empty_like(v)
+    lib = N.load()
+    ws = torch.empty(lib.tgs_segmented_sort_workspace_size(n, len(segs) - 1), dtype=torch.uint8,
+                     device=gpu)
+    sel = ctypes.c_int(0)
+    host = (ctypes.c_uint32 * len(segs))(*segs)
+    N.call("tgs_segmented_sort_pairs_u32_range", N.ptr(k), N.ptr(v), N.ptr(k2), N.ptr(v2), 8, n,
+           len(segs) - 1, host, base, key_bits, N.ptr(ws), ws.numel(), ctypes.byref(sel),
+           N.stream_handle())
+    ko, vo = (k2, v2) if sel.value else (k, v)
+    ko = to_np(ko).view(np.uint32)
+    vo = to_np(vo)
+    cap = np.uint64(span)
+    rel = np.minimum(np.maximum(keys.astype(np.int64) - base, 0).astype(np.uint64), cap)
+    for a, b in zip(segs[:-1], segs[1:]):
+        order = np.argsort(rel[a:b], kind="stable") + a
+        np.testing.assert_array_equal(ko[a:b], keys[order])
+        np.testing.assert_array_equal(vo[a:b], vals[order])
+        # the keys inside the range come out in their full stable order
+        ins = np.flatnonzero((keys[a:b] >= base) & (keys[a:b] != 0xFFFFFFFF)) + a
+        full = ins[np.argsort(keys[ins], kind="stable")]
+        out_in = (ko[a:b] >= base) & (ko[a:b] != 0xFFFFFFFF)
+        np.testing.assert_array_equal(vo[a:b][out_in], vals[full])
+
+
 def _raster_case(gpu, seed, C=2, D=3, W=200, H=120, tile=16, packed=False):
     sc, radii, m2d, depths, conics, opac = _projected(gpu, seed=seed, C=C, W=W, H=H)
     tw, th = -(-W // tile), -(-H // tile)

@@ -48,3 +48,21 @@ def test_channel_chunks():
     assert _channel_chunks(33) == [(0, 32, 32), (32, 1, 1)]
     assert _channel_chunks(45) == [(0, 32, 32), (32, 13, 16)]
     assert _channel_chunks(513)[-1] == (512, 1, 1) and len(_channel_chunks(513)) == 17
+
+
+def test_depth_key_range():
+    """Key range of the depth sort: the visible keys and the slack map below
+    2^bits - 1 (where the culled sentinel ties), bits as few as that allows;
+    nothing visible ({~0, 0} from the device) sorts on all 32 bits."""
+    from tidegs_amd.tide_step import DEPTH_KEY_SLACK, depth_key_range
+    import numpy as np
+    lo, hi = int(np.float32(24.0).view(np.uint32)), int(np.float32(146.0).view(np.uint32))
+    base, bits = depth_key_range(lo, hi)
+    assert base == lo - DEPTH_KEY_SLACK
+    assert (hi + DEPTH_KEY_SLACK) - base < (1 << bits) - 1
+    assert (hi + DEPTH_KEY_SLACK) - base >= (1 << (bits - 1)) - 1
+    assert bits == 25
+    assert depth_key_range(-1, 0) == (0, 32)  # int32 views of {~0, 0}
+    assert depth_key_range(5, 5)[1] == ((5 + DEPTH_KEY_SLACK) - 0 + 1).bit_length()
+    base, bits = depth_key_range(0x7F000000, 0x7F7FFFFF)
+    assert bits <= 32 and 0x7F7FFFFF + DEPTH_KEY_SLACK - base < (1 << bits) - 1

@@ -76,6 +76,10 @@ SIGNATURES = {
         [P, P, P, P, U32, U64, U32, P, ctypes.c_int, ctypes.c_int, P, SZ,
          ctypes.POINTER(ctypes.c_int), P],
     ),
+    "tgs_segmented_sort_pairs_u32_range": (
+        ctypes.c_int,
+        [P, P, P, P, U32, U64, U32, P, U32, ctypes.c_int, P, SZ, ctypes.POINTER(ctypes.c_int), P],
+    ),
     "tgs_isect_offset_encode": (ctypes.c_int, [U64, P, U32, U32, U32, P, P]),
     "tgs_rasterize_supported_channels": (ctypes.c_int, [ctypes.POINTER(I32), I32]),
     "tgs_rasterize_to_pixels_fwd": (
@@ -95,7 +99,7 @@ SIGNATURES = {
     "tgs_tide_camera_centers": (ctypes.c_int, [U32, P, P, P]),
     "tgs_tide_row_blocks": (U32, [U64]),
     "tgs_tide_visibility": (
-        ctypes.c_int, [U64, P, U32, U32, P, P, P, I32, I32, F32, F32, F32, F32, P, P, P]),
+        ctypes.c_int, [U64, P, U32, U32, P, P, P, I32, I32, F32, F32, F32, F32, P, P, P, P]),
     "tgs_tide_compact": (ctypes.c_int, [U64, U32, P, P, P, P, P, P, P, P, P, P]),
     "tgs_tide_project_fwd": (
         ctypes.c_int,

@@ -208,6 +208,10 @@ struct RadixSegs {
   uint32_t n;                             // number of segments (>= 1)
   uint32_t key_off[RADIX_MAX_SEGS + 1];   // key_off[0] = 0, key_off[n] = n_keys
   uint32_t tile_base[RADIX_MAX_SEGS + 1]; // first tile of each segment
+  // 32-bit keys are ranked as min(key - key_base, key_cap) (keys below the
+  // base as 0): an order-preserving map of a key range onto its low bits, with
+  // every key past the range tied at key_cap.  (0, ~0) ranks the keys as they are.
+  uint32_t key_base = 0, key_cap = 0xffffffffu;
 };
 
 struct TileRange {
@@ -234,8 +238,17 @@ __device__ __forceinline__ TileRange radix_tile(const RadixSegs& sg, uint32_t b)
 }
 
 template <typename K>
-__device__ __forceinline__ uint32_t digit_of(K key, int shift, uint32_t mask) {
-  return (uint32_t)(key >> shift) & mask;
+__device__ __forceinline__ uint32_t digit_of(K key, const RadixSegs& sg, int shift,
+                                            uint32_t mask) {
+  if constexpr (sizeof(K) == 4) {
+    // max-then-subtract is a clamped (saturating) subtract; the same select
+    // written as (k < base ? 0 : min(k - base, cap)) compiles for gfx950 to an
+    // unclamped subtract, so keys below the base would wrap
+    const uint32_t r = min(max((uint32_t)key, sg.key_base) - sg.key_base, sg.key_cap);
+    return (r >> shift) & mask;
+  } else {
+    return (uint32_t)(key >> shift) & mask;
+  }
 }
 
 template <typename K>
@@ -263,7 +276,7 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_hist_kernel(const K* __res
   for (int r = 0; r < SORT_ITEMS; ++r) {
     const uint32_t i = (uint32_t)r * SORT_THREADS + threadIdx.x;
     const bool valid = i < tr.count;
-    const uint32_t d = valid ? digit_of(kr[r], shift, mask) : 0u;
+    const uint32_t d = valid ? digit_of(kr[r], sg, shift, mask) : 0u;
     const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)d);
     const uint64_t vm = tgs_ballot(valid);
     const uint64_t same = tgs_ballot(valid && d == d0);
@@ -325,7 +338,7 @@ __global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_
   for (int r = 0; r < SORT_ITEMS; ++r) {
     const uint32_t li = wbase + (uint32_t)r * 64u + lane;
     const bool valid = li < tr.count;
-    const uint32_t d = digit_of(k[r], shift, mask);
+    const uint32_t d = digit_of(k[r], sg, shift, mask);
     uint64_t peers = tgs_ballot(valid);
     const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)d);
     if (tgs_ballot(valid && d == d0) != peers) {  // else every valid lane shares d0
@@ -361,7 +374,7 @@ __global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_
   for (int r = 0; r < SORT_ITEMS; ++r) {
     const uint32_t li = wbase + (uint32_t)r * 64u + lane;
     if (li < tr.count) {
-      const uint32_t d = digit_of(k[r], shift, mask);
+      const uint32_t d = digit_of(k[r], sg, shift, mask);
       const uint32_t pos = s_start[d] + s_wh[wave][d] + rk[r];
       s_k[pos] = k[r];
       s_v[pos] = v[r];
@@ -370,7 +383,7 @@ __global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_
   __syncthreads();
   for (uint32_t j = threadIdx.x; j < tr.count; j += SORT_THREADS) {
     const K kk = s_k[j];
-    const uint32_t o = s_gofs[digit_of(kk, shift, mask)] + j;
+    const uint32_t o = s_gofs[digit_of(kk, sg, shift, mask)] + j;
     keys_out[o] = kk;
     vals_out[o] = s_v[j];
   }
@@ -557,12 +570,46 @@ extern "C" int tgs_radix_sort_pairs_noalloc(uint64_t* keys, uint32_t* vals, uint
 // Segmented stable sort of uint32 keys with 4- or 8-byte values: each segment
 // [seg_offsets[s], seg_offsets[s+1]) is sorted on its own.  seg_offsets is a
 // HOST array of n_segments+1 non-decreasing offsets from 0 to n.
+static int segmented_sort_u32(uint32_t* keys, void* vals, uint32_t* keys_alt, void* vals_alt,
+                              uint32_t value_bytes, uint64_t n, uint32_t n_segments,
+                              const uint32_t* seg_offsets, uint32_t key_base, uint32_t key_cap,
+                              int begin_bit, int end_bit, void* workspace, size_t workspace_bytes,
+                              int* selector, hipStream_t stream);
+
 extern "C" int tgs_segmented_sort_pairs_u32(uint32_t* keys, void* vals, uint32_t* keys_alt,
                                             void* vals_alt, uint32_t value_bytes, uint64_t n,
                                             uint32_t n_segments, const uint32_t* seg_offsets,
                                             int begin_bit, int end_bit, void* workspace,
                                             size_t workspace_bytes, int* selector,
                                             hipStream_t stream) {
+  return segmented_sort_u32(keys, vals, keys_alt, vals_alt, value_bytes, n, n_segments,
+                            seg_offsets, 0u, 0xffffffffu, begin_bit, end_bit, workspace,
+                            workspace_bytes, selector, stream);
+}
+
+// The same sort on key_bits bits of min(key - key_base, 2^key_bits - 1) (keys
+// below key_base as 0): a key range known to lie in [key_base, key_base +
+// 2^key_bits - 1) is sorted in fewer or narrower passes, and keys past it
+// (a sentinel such as 0xffffffff) tie at the top, in their input order.
+extern "C" int tgs_segmented_sort_pairs_u32_range(uint32_t* keys, void* vals, uint32_t* keys_alt,
+                                                  void* vals_alt, uint32_t value_bytes, uint64_t n,
+                                                  uint32_t n_segments,
+                                                  const uint32_t* seg_offsets, uint32_t key_base,
+                                                  int key_bits, void* workspace,
+                                                  size_t workspace_bytes, int* selector,
+                                                  hipStream_t stream) {
+  TGS_CHECK_ARG(key_bits >= 1 && key_bits <= 32, "segmented_sort_range: key_bits in [1, 32]");
+  const uint32_t cap = key_bits == 32 ? 0xffffffffu : (1u << key_bits) - 1u;
+  return segmented_sort_u32(keys, vals, keys_alt, vals_alt, value_bytes, n, n_segments,
+                            seg_offsets, key_base, cap, 0, key_bits, workspace, workspace_bytes,
+                            selector, stream);
+}
+
+static int segmented_sort_u32(uint32_t* keys, void* vals, uint32_t* keys_alt, void* vals_alt,
+                              uint32_t value_bytes, uint64_t n, uint32_t n_segments,
+                              const uint32_t* seg_offsets, uint32_t key_base, uint32_t key_cap,
+                              int begin_bit, int end_bit, void* workspace, size_t workspace_bytes,
+                              int* selector, hipStream_t stream) {
   TGS_CHECK_ARG(selector != nullptr, "segmented_sort: null selector");
   *selector = 0;
   if (n <= 1 || end_bit <= begin_bit) return TGS_OK;
@@ -578,6 +625,8 @@ extern "C" int tgs_segmented_sort_pairs_u32(uint32_t* keys, void* vals, uint32_t
                 "segmented_sort: segments must cover [0, n)");
   RadixSegs sg{};
   sg.n = n_segments;
+  sg.key_base = key_base;
+  sg.key_cap = key_cap;
   uint32_t tiles = 0;
   for (uint32_t s = 0; s < n_segments; ++s) {
     TGS_CHECK_ARG(seg_offsets[s + 1] >= seg_offsets[s], "segmented_sort: offsets decrease");

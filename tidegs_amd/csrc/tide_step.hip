@@ -82,11 +82,12 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-
 // with the 0.1 floor.
 __device__ __forceinline__ bool packed_visible(const float p[3], const m3& Sigma, const Cam& cam,
                                                int W, int H, float eps2d, float near_plane,
-                                               float far_plane, float radius_clip) {
+                                               float far_plane, float radius_clip, float& depth) {
   float pc[3];
 #pragma unroll
   for (int i = 0; i < 3; ++i)
     pc[i] = cam.R[i][0] * p[0] + cam.R[i][1] * p[1] + cam.R[i][2] * p[2] + cam.t[i];
+  depth = pc[2];
   if (pc[2] < near_plane || pc[2] > far_plane) return false;
   m3 Rc;
 #pragma unroll
@@ -132,32 +133,60 @@ __device__ __forceinline__ m3 row_covariance(const float* __restrict__ row) {
   return covar_from_quat_scale(qn, s);
 }
 
+#define TIDE_RANGE_SLOTS 64  // {min, max} pairs of the depth-key range
+
 // ---------------------------------------------------------------------------
 // Visibility + per-block counts.  counts layout (uint32, block-minor):
 //   [c * nb + b]        visible rows of camera c in block b   (c < C)
 //   [C * nb + b]        touched rows in block b
 //   [(C+1) * nb + b]    visits (sum of popcount(mask)) in block b
+// With depth_range (TIDE_RANGE_SLOTS {min, max} pairs set to {~0, 0} by the
+// launch), the smallest and largest float bits of the visible entries' depths
+// (positive, so ordered like the depths) are folded in, workgroup b into
+// pair b mod TIDE_RANGE_SLOTS (atomics on one pair from every workgroup would
+// serialize): the depth sort's key range is the min / max over the pairs.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(VIS_THREADS) tide_visibility_kernel(
     uint64_t n_rows, const float* __restrict__ params, uint32_t row_stride, TideCams tc, int W,
     int H, float eps2d, float near_plane, float far_plane, float radius_clip,
-    uint32_t* __restrict__ masks, uint32_t* __restrict__ counts) {
+    uint32_t* __restrict__ masks, uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ depth_range) {
   __shared__ CamLDS s_cam;
   __shared__ uint32_t s_cnt[TIDE_MAX_CAMS + 2];
+  __shared__ uint32_t s_rng[2];
   load_cams_lds(tc, s_cam);
   if (threadIdx.x < TIDE_MAX_CAMS + 2) s_cnt[threadIdx.x] = 0;
+  if (threadIdx.x < 2) s_rng[threadIdx.x] = threadIdx.x == 0 ? 0xffffffffu : 0u;
   __syncthreads();
   const uint64_t n = (uint64_t)blockIdx.x * VIS_THREADS + threadIdx.x;
   const uint32_t nb = gridDim.x;
   uint32_t mask = 0;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
   if (n < n_rows) {
     const float* row = params + n * row_stride;
     const float p[3] = {row[0], row[1], row[2]};
     const m3 Sigma = row_covariance(row);
-    for (uint32_t c = 0; c < tc.C; ++c)
-      if (packed_visible(p, Sigma, s_cam.cam[c], W, H, eps2d, near_plane, far_plane, radius_clip))
+    for (uint32_t c = 0; c < tc.C; ++c) {
+      float depth;
+      if (packed_visible(p, Sigma, s_cam.cam[c], W, H, eps2d, near_plane, far_plane, radius_clip,
+                         depth)) {
         mask |= 1u << c;
+        kmin = min(kmin, __float_as_uint(depth));
+        kmax = max(kmax, __float_as_uint(depth));
+      }
+    }
     masks[n] = mask;
+  }
+  if (depth_range) {  // wave min / max first: one LDS update per wavefront
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, off, 64));
+      kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
+    }
+    if ((threadIdx.x & 63) == 0 && kmax >= kmin) {
+      atomicMin(&s_rng[0], kmin);
+      atomicMax(&s_rng[1], kmax);
+    }
   }
   const int lane = threadIdx.x & 63;
   for (uint32_t c = 0; c < tc.C; ++c) {
@@ -169,6 +198,15 @@ __global__ void __launch_bounds__(VIS_THREADS) tide_visibility_kernel(
   atomicAdd(&s_cnt[tc.C + 1], (uint32_t)__popc(mask));
   __syncthreads();
   if (threadIdx.x < tc.C + 2) counts[(uint64_t)threadIdx.x * nb + blockIdx.x] = s_cnt[threadIdx.x];
+  if (depth_range && threadIdx.x == 0 && s_rng[1] >= s_rng[0]) {
+    uint32_t* slot = depth_range + 2 * (blockIdx.x % TIDE_RANGE_SLOTS);
+    atomicMin(&slot[0], s_rng[0]);
+    atomicMax(&slot[1], s_rng[1]);
+  }
+}
+
+__global__ void tide_range_init_kernel(uint32_t* __restrict__ r) {
+  if (threadIdx.x < 2 * TIDE_RANGE_SLOTS) r[threadIdx.x] = (threadIdx.x & 1u) ? 0u : 0xffffffffu;
 }
 
 // offs = exclusive scan of counts (same layout).  Writes:
@@ -1043,17 +1081,20 @@ extern "C" int tgs_tide_visibility(uint64_t n_rows, const float* params, uint32_
                                    const float* viewmats, const float* Ks, const float* campos,
                                    int32_t W, int32_t H, float eps2d, float near_plane,
                                    float far_plane, float radius_clip, uint32_t* masks,
-                                   uint32_t* counts, hipStream_t stream) {
+                                   uint32_t* counts, uint32_t* depth_range, hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;
-  if (n_rows == 0) return TGS_OK;
+  if (depth_range)
+    hipLaunchKernelGGL(tide_range_init_kernel, dim3(1), dim3(2 * TIDE_RANGE_SLOTS), 0, stream,
+                       depth_range);
+  if (n_rows == 0) TGS_RETURN_LAUNCH("tgs_tide_visibility");
   TGS_CHECK_ARG(params && viewmats && Ks && campos && masks && counts, "tide_visibility: null");
   TGS_CHECK_ARG(n_rows < (1ull << 31), "tide_visibility: at most 2^31-1 rows");
   TGS_CHECK_ARG(row_stride >= TIDE_ROW, "tide step: row_stride must be >= %d", TIDE_ROW);
   TideCams tc{viewmats, Ks, campos, C};
   hipLaunchKernelGGL(tide_visibility_kernel, dim3(tgs_tide_row_blocks(n_rows)), dim3(VIS_THREADS),
                      0, stream, n_rows, params, row_stride, tc, W, H, eps2d, near_plane, far_plane,
-                     radius_clip, masks, counts);
+                     radius_clip, masks, counts, depth_range);
   TGS_RETURN_LAUNCH("tgs_tide_visibility");
 }
 

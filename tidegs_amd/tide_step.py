@@ -119,6 +119,25 @@ def check_isect_count(n_isects: int) -> None:
             f"tile offsets and flatten ids (max {MAX_ISECTS}); use fewer cameras per batch")
 
 
+# ulps of slack around the visibility pass's depth-key range (its depths and
+# the projection's are the same float expression)
+DEPTH_KEY_SLACK = 256
+RANGE_SLOTS = 64  # {min, max} pairs the visibility pass spreads the range over
+
+
+def depth_key_range(lo: int, hi: int) -> tuple:
+    """(key_base, key_bits) of the depth sort from the smallest and largest
+    visible depth keys (uint32 float bits): every key of [lo - slack,
+    hi + slack] maps below 2^key_bits - 1, where the culled entries' sentinel
+    0xffffffff ties after them; (0, 32) when nothing is visible."""
+    lo, hi = lo & 0xFFFFFFFF, hi & 0xFFFFFFFF
+    if hi < lo:
+        return 0, 32
+    base = max(0, lo - DEPTH_KEY_SLACK)
+    top = min(hi + DEPTH_KEY_SLACK, 0xFFFFFFFE)
+    return base, min((top - base + 1).bit_length(), 32)
+
+
 def _segments(offsets) -> "ctypes.Array":
     """Host uint32 array of segment offsets for tgs_segmented_sort_pairs_u32."""
     return (ctypes.c_uint32 * len(offsets))(*[int(o) for o in offsets])
@@ -269,10 +288,13 @@ class TideStep:
         masks = self._buf("masks", n, torch.int32)
         counts = self._buf("counts", (C + 2) * nb, torch.int32)
         self._begin("visibility")
+        # totals [C+3+128]: V_c..., T, sum V, visits (compaction), then 64
+        # {min, max} pairs of the depth keys' range (visibility)
+        totals = self._buf("totals", C + 3 + 2 * RANGE_SLOTS, torch.int32)
         N.call("tgs_tide_visibility", n, N.ptr(P), self.row_stride, C, N.ptr(viewmats), N.ptr(Ks),
                N.ptr(campos),
                W, H, self.eps2d, self.near, self.far, self.radius_clip, N.ptr(masks),
-               N.ptr(counts), s)
+               N.ptr(counts), N.ptr(totals) + 4 * (C + 3), s)
         offs = self._buf("offs", (C + 2) * nb, torch.int32)
         ws = self._buf("scan_ws", lib.tgs_scan_workspace_size((C + 2) * nb), torch.uint8)
         N.call("tgs_exclusive_scan_u32", N.ptr(counts), N.ptr(offs), (C + 2) * nb, N.ptr(ws),
@@ -281,7 +303,6 @@ class TideStep:
         visits = self._buf("visits", C * n, torch.int32)
         touched = self._buf("touched", n, torch.int32)
         visit_base = self._buf("visit_base", n + 1, torch.int32)
-        totals = self._buf("totals", C + 3, torch.int32)
         cam_offsets = self._buf("cam_offsets", C + 1, torch.int32)
         N.call("tgs_tide_compact", n, C, N.ptr(masks), N.ptr(counts), N.ptr(offs), N.ptr(entries),
                N.ptr(touched), N.ptr(visit_base), N.ptr(visits), N.ptr(totals),
@@ -289,7 +310,7 @@ class TideStep:
         self._end()
         # the totals (V per camera, T, V) go to the host while the projection
         # runs: its launch covers every row and reads T on the device
-        tot_host = self._pinned("totals", C + 3, torch.int32)
+        tot_host = self._pinned("totals", C + 3 + 2 * RANGE_SLOTS, torch.int32)
         tot_host.copy_(totals, non_blocking=True)
         totals_ready = self._record()
 
@@ -340,9 +361,13 @@ class TideStep:
         if V:
             sel = ctypes.c_int(0)
             dws = self._buf("sort_ws", lib.tgs_segmented_sort_workspace_size(V, C), torch.uint8)
-            N.call("tgs_segmented_sort_pairs_u32", N.ptr(dkeys), N.ptr(rects), N.ptr(dkeys2),
-                   N.ptr(rects2), 8, V, C, cam_segs, 0, 32, N.ptr(dws), dws.numel(),
-                   ctypes.byref(sel), s)
+            # depth keys ranked relative to the visible range: 25 bits at cfg3,
+            # four 6-7 bit passes instead of four 8-bit ones
+            rng = [v & 0xFFFFFFFF for v in tot[C + 3:]]
+            key_base, key_bits = depth_key_range(min(rng[0::2]), max(rng[1::2]))
+            N.call("tgs_segmented_sort_pairs_u32_range", N.ptr(dkeys), N.ptr(rects),
+                   N.ptr(dkeys2), N.ptr(rects2), 8, V, C, cam_segs, key_base, key_bits,
+                   N.ptr(dws), dws.numel(), ctypes.byref(sel), s)
             if sel.value:
                 rects = rects2
             N.call("tgs_tide_isect_block_sums", V, N.ptr(rects), N.ptr(eb_sums), s)
