@@ -252,6 +252,8 @@ def test_radix_sort_pairs_stable(gpu, n, begin, end):
     ([0, 1, 2, 3000, 3000], 32, 8),
     ([0, 300_000, 300_001, 1_000_000], 32, 8),
     ([0, 8192, 8192, 8192], 7, 4),
+    ([0, 0, 4096, 4097, 70_000], 26, 4),          # three 9-bit passes (512 digits)
+    ([0, 3, 50_000], 9, 8),                        # one 9-bit pass
 ])
 def test_segmented_sort_pairs_u32(gpu, segs, bits, vbytes):
     """Each segment sorted stably on its own (numpy argsort kind='stable')."""
@@ -286,7 +288,8 @@ def test_segmented_sort_pairs_u32(gpu, segs, bits, vbytes):
 
 
 @pytest.mark.parametrize("segs,key_bits", [([0, 70_000], 25), ([0, 5000, 5000, 90_000, 131_073], 19),
-                                           ([0, 40_000], 32)])
+                                           ([0, 40_000], 32), ([0, 1, 60_000, 60_000, 99_999], 27),
+                                           ([0, 33_000], 18)])
 def test_segmented_sort_pairs_u32_range(gpu, segs, key_bits):
     """The range form sorts keys in [base, base + 2^bits - 1) into the same
     order as a full stable sort, with the 0xffffffff sentinels (culled depth
