@@ -587,7 +587,10 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   constexpr int NA = NV + 2;
   __shared__ float4 s_g0[BATCH];
   __shared__ float2 s_g1[BATCH];
-  __shared__ float s_col[BATCH][CDIM];
+  // three colours padded to four: the walk reads them with one 16-byte read
+  // at the same t * 16 address as s_g0
+  constexpr int CPAD = CDIM == 3 ? 4 : CDIM;
+  __shared__ __align__(16) float s_col[BATCH][CPAD];
   __shared__ float s_vrc[BLOCK][CDIM];  // dL/dcolor of each pixel
   __shared__ int32_t s_id[BATCH];
   __shared__ uint8_t s_list[WAVES][BATCH];
@@ -820,11 +823,15 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
               uint32_t rb = (hb >> (16 * rr)) & 0xffffu;
               const float* vrc = &s_vrc[wave * 64 + 32 * oh + 16 * rr][0];
               const float dy = rr == 0 ? dy0 : dy1;
+              // the second row's pairs follow the first row's popcount ones,
+              // so the loop advances only its pointer
+              const float2* pp =
+                  &s_pair[wave][slot + (rr == 0 ? 0u : (uint32_t)__popc(hb & 0xffffu))];
               float a0 = 0.f, a1 = 0.f, a2 = 0.f;
               while (rb != 0u) {
                 const int jc = __builtin_ctz(rb);
                 rb &= rb - 1u;
-                const float2 pr = s_pair[wave][slot++];
+                const float2 pr = *pp++;
                 const float dx = gxr - (float)jc;
                 const float vs = pr.y;
                 const float mx = vs * dx;
