@@ -174,7 +174,7 @@ def _median_time(fn, repeats=3):
 
 def cpu_baseline(width, height, gpu_stats, seed=0):
     """The CPU oracle (oracle/step_ref.py + oracle/optim_ref.py) timed on the
-    host cores (BASELINE.md section 2): all threads of the box's CPU share, 1
+    host cores: all threads of the box's CPU share, 1
     warm-up and the median of 3 repeats per sample.
 
     * cfg1 (10k Gaussians, one 256x256 camera, L1, Adam) runs in full.
@@ -927,7 +927,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the TideGS step is single-GPU; "
-              "see DESIGN.md for how it would shard by camera). Run with --gpus 1.",
+              "a multi-GPU run would shard the cameras over ranks). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 

@@ -21,8 +21,8 @@
 // component tensors or one unified [N,59] table.  The building blocks are
 // shared with the projection backward's fused update (resident_optim.cuh).
 //
-// Sophia (no reference; Liu et al. 2023, arXiv 2305.14342, Alg. 3 with the
-// per-coordinate clip of SURVEY row A14):
+// Sophia (no reference; Liu et al. 2023, arXiv 2305.14342, Alg. 3, with a
+// per-coordinate clip of the update ratio):
 //   m  = b1*m + (1-b1)*g
 //   h  = b2*h + (1-b2)*g*g        (only on Hessian-refresh steps)
 //   p -= lr_col * clamp(m / max(h, eps), -rho, rho)
