@@ -289,7 +289,8 @@ def test_segmented_sort_pairs_u32(gpu, segs, bits, vbytes):
 
 @pytest.mark.parametrize("segs,key_bits", [([0, 70_000], 25), ([0, 5000, 5000, 90_000, 131_073], 19),
                                            ([0, 40_000], 32), ([0, 1, 60_000, 60_000, 99_999], 27),
-                                           ([0, 33_000], 18)])
+                                           ([0, 33_000], 18), ([0, 4096], 1), ([0, 2, 9000], 8),
+                                           ([0, 12_345], 9)])
 def test_segmented_sort_pairs_u32_range(gpu, segs, key_bits):
     """The range form sorts keys in [base, base + 2^bits - 1) into the same
     order as a full stable sort, with the 0xffffffff sentinels (culled depth
