@@ -185,6 +185,17 @@ int tgs_radix_sort_pairs_noalloc(uint64_t* keys, uint32_t* vals, uint64_t* keys_
  * n_segments+1 (<= 65) non-decreasing offsets from 0 to n.  Double-buffered
  * like tgs_radix_sort_pairs. */
 size_t tgs_segmented_sort_workspace_size(uint64_t n, uint32_t n_segments);
+/* Beside the reference's interface: tgs_segmented_sort_pairs_u32 with 4-byte
+ * values whose first pass's per-tile digit counts are already at the start of
+ * the workspace (word tile_base[s] * 256 + d * (tile_base[s + 1] -
+ * tile_base[s]) + t: digit d among keys [4096 t, 4096 t + 4096) of segment s;
+ * tile_base sums ceil(size / 4096) over the earlier segments; the first pass
+ * takes ceil(bits / passes) bits, passes = ceil(bits / 8)). */
+int tgs_segmented_sort_pairs_u32_hist0(uint32_t* keys, uint32_t* vals, uint32_t* keys_alt,
+                                       uint32_t* vals_alt, uint64_t n, uint32_t n_segments,
+                                       const uint32_t* seg_offsets, int begin_bit, int end_bit,
+                                       void* workspace, size_t workspace_bytes, int* selector,
+                                       tgs_stream_t stream);
 int tgs_segmented_sort_pairs_u32(uint32_t* keys, void* vals, uint32_t* keys_alt, void* vals_alt,
                                  uint32_t value_bytes, uint64_t n, uint32_t n_segments,
                                  const uint32_t* seg_offsets, int begin_bit, int end_bit,
@@ -393,6 +404,17 @@ int tgs_tide_isect_emit_blocked(uint32_t n_entries, const int32_t* cam_offsets, 
                                 const uint64_t* entry_rects, const uint32_t* block_base,
                                 uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
                                 int32_t* flatten_ids, tgs_stream_t stream);
+/* Beside the reference's interface: tgs_tide_isect_emit_blocked that also
+ * counts the tile-bit sort's first-pass digits (tile & digit_mask) into hist,
+ * in the layout tgs_segmented_sort_pairs_u32_hist0 reads (segments = cameras,
+ * isect_cam_offsets = the C + 1 host-side first intersections per camera);
+ * hist (hist_words uint32 words, e.g. the sort's workspace) is cleared first. */
+int tgs_tide_isect_emit_blocked_hist(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,
+                                     const uint64_t* entry_rects, const uint32_t* block_base,
+                                     uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
+                                     int32_t* flatten_ids, const uint32_t* isect_cam_offsets,
+                                     uint32_t digit_mask, uint32_t* hist, uint64_t hist_words,
+                                     tgs_stream_t stream);
 int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, uint32_t C,
                            uint32_t tile_width, uint32_t tile_height, uint32_t tile_n_bits,
                            int32_t* offsets, tgs_stream_t stream);

@@ -112,6 +112,12 @@ SIGNATURES = {
     "tgs_tide_isect_emit_blocks": (U32, [U32]),
     "tgs_tide_isect_block_sums": (ctypes.c_int, [U32, P, P, P]),
     "tgs_tide_isect_emit_blocked": (ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P]),
+    "tgs_tide_isect_emit_blocked_hist": (
+        ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P, U32, P, U64, P]),
+    "tgs_segmented_sort_pairs_u32_hist0": (
+        ctypes.c_int,
+        [P, P, P, P, U64, U32, P, ctypes.c_int, ctypes.c_int, P, SZ, ctypes.POINTER(ctypes.c_int),
+         P]),
     "tgs_tide_offset_encode": (ctypes.c_int, [U32, P, U32, U32, U32, U32, P, P]),
     "tgs_tide_isect_ids": (ctypes.c_int, [U32, P, P, P, P, P]),
     "tgs_tide_rasterize_fwd": (

@@ -409,7 +409,7 @@ extern "C" size_t tgs_segmented_sort_workspace_size(uint64_t n, uint32_t n_segme
 template <typename K, typename V>
 static int radix_passes(K* keys, V* vals, K* keys_alt, V* vals_alt, const RadixSegs& sg,
                         int begin_bit, int end_bit, void* workspace, int* selector,
-                        hipStream_t stream) {
+                        hipStream_t stream, bool first_hist_ready = false) {
   const uint64_t tiles = sg.tile_base[sg.n];
   const uint64_t hist_n = tiles * SORT_BINS;
   auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
@@ -427,9 +427,11 @@ static int radix_passes(K* keys, V* vals, K* keys_alt, V* vals_alt, const RadixS
   while (shift < end_bit) {
     const int bits = (end_bit - shift + passes - 1) / passes;
     const uint32_t mask = (1u << bits) - 1u;
-    hipLaunchKernelGGL((radix_hist_kernel<K>), dim3((unsigned)tiles), dim3(SORT_THREADS), 0,
-                       stream, kin, sg, shift, mask, hist);
-    TGS_LAUNCH_CHECK("radix_hist");
+    if (!(first_hist_ready && shift == begin_bit)) {
+      hipLaunchKernelGGL((radix_hist_kernel<K>), dim3((unsigned)tiles), dim3(SORT_THREADS), 0,
+                         stream, kin, sg, shift, mask, hist);
+      TGS_LAUNCH_CHECK("radix_hist");
+    }
     int rc = exclusive_scan_u32(hist, hist_scan, hist_n, scan_ws, stream);
     if (rc) return rc;
     hipLaunchKernelGGL((radix_scatter_kernel<K, V>), dim3((unsigned)tiles), dim3(SORT_THREADS), 0,
@@ -574,7 +576,7 @@ static int segmented_sort_u32(uint32_t* keys, void* vals, uint32_t* keys_alt, vo
                               uint32_t value_bytes, uint64_t n, uint32_t n_segments,
                               const uint32_t* seg_offsets, uint32_t key_base, uint32_t key_cap,
                               int begin_bit, int end_bit, void* workspace, size_t workspace_bytes,
-                              int* selector, hipStream_t stream);
+                              int* selector, hipStream_t stream, bool first_hist_ready);
 
 extern "C" int tgs_segmented_sort_pairs_u32(uint32_t* keys, void* vals, uint32_t* keys_alt,
                                             void* vals_alt, uint32_t value_bytes, uint64_t n,
@@ -584,7 +586,26 @@ extern "C" int tgs_segmented_sort_pairs_u32(uint32_t* keys, void* vals, uint32_t
                                             hipStream_t stream) {
   return segmented_sort_u32(keys, vals, keys_alt, vals_alt, value_bytes, n, n_segments,
                             seg_offsets, 0u, 0xffffffffu, begin_bit, end_bit, workspace,
-                            workspace_bytes, selector, stream);
+                            workspace_bytes, selector, stream, false);
+}
+
+// The same sort (4-byte values) with the first pass's per-tile digit counts
+// already in the workspace, counted by the producer of the keys: uint32 word
+// tile_base[s] * 256 + d * (tile_base[s + 1] - tile_base[s]) + t holds the
+// count of digit d ((key >> begin_bit) & (2^w - 1), w the first pass's width:
+// the key bits split into ceil(bits / 8) passes of ceil(bits / passes) bits)
+// among keys [t * 4096, t * 4096 + 4096) of segment s, where tile_base[s] sums
+// ceil(segment size / 4096) over the segments before s.
+extern "C" int tgs_segmented_sort_pairs_u32_hist0(uint32_t* keys, uint32_t* vals,
+                                                  uint32_t* keys_alt, uint32_t* vals_alt,
+                                                  uint64_t n, uint32_t n_segments,
+                                                  const uint32_t* seg_offsets, int begin_bit,
+                                                  int end_bit, void* workspace,
+                                                  size_t workspace_bytes, int* selector,
+                                                  hipStream_t stream) {
+  return segmented_sort_u32(keys, vals, keys_alt, vals_alt, 4, n, n_segments, seg_offsets, 0u,
+                            0xffffffffu, begin_bit, end_bit, workspace, workspace_bytes, selector,
+                            stream, true);
 }
 
 // The same sort on key_bits bits of min(key - key_base, 2^key_bits - 1) (keys
@@ -602,14 +623,14 @@ extern "C" int tgs_segmented_sort_pairs_u32_range(uint32_t* keys, void* vals, ui
   const uint32_t cap = key_bits == 32 ? 0xffffffffu : (1u << key_bits) - 1u;
   return segmented_sort_u32(keys, vals, keys_alt, vals_alt, value_bytes, n, n_segments,
                             seg_offsets, key_base, cap, 0, key_bits, workspace, workspace_bytes,
-                            selector, stream);
+                            selector, stream, false);
 }
 
 static int segmented_sort_u32(uint32_t* keys, void* vals, uint32_t* keys_alt, void* vals_alt,
                               uint32_t value_bytes, uint64_t n, uint32_t n_segments,
                               const uint32_t* seg_offsets, uint32_t key_base, uint32_t key_cap,
                               int begin_bit, int end_bit, void* workspace, size_t workspace_bytes,
-                              int* selector, hipStream_t stream) {
+                              int* selector, hipStream_t stream, bool first_hist_ready) {
   TGS_CHECK_ARG(selector != nullptr, "segmented_sort: null selector");
   *selector = 0;
   if (n <= 1 || end_bit <= begin_bit) return TGS_OK;
@@ -644,7 +665,9 @@ static int segmented_sort_u32(uint32_t* keys, void* vals, uint32_t* keys_alt, vo
   if (tiles == 0) return TGS_OK;
   if (value_bytes == 4)
     return radix_passes<uint32_t, uint32_t>(keys, (uint32_t*)vals, keys_alt, (uint32_t*)vals_alt,
-                                            sg, begin_bit, end_bit, workspace, selector, stream);
+                                            sg, begin_bit, end_bit, workspace, selector, stream,
+                                            first_hist_ready);
+  TGS_CHECK_ARG(!first_hist_ready, "segmented_sort: a precounted first pass needs 4-byte values");
   return radix_passes<uint32_t, uint64_t>(keys, (uint64_t*)vals, keys_alt, (uint64_t*)vals_alt, sg,
                                           begin_bit, end_bit, workspace, selector, stream);
 }

@@ -568,13 +568,47 @@ __global__ void __launch_bounds__(256) tide_isect_block_sums_kernel(
   if (threadIdx.x == 0) block_sums[blockIdx.x] = s_w[0] + s_w[1] + s_w[2] + s_w[3];
 }
 
+// The tile-bit sort's first-pass digit counts, counted while emitting (the
+// layout of tgs_segmented_sort_pairs_u32_hist0: segments = cameras, sort
+// tiles of EMIT_SORT_TILE intersections).  A block's outputs are consecutive
+// slots: their first EMIT_HWIN sort tiles are counted in LDS and added once
+// per (tile, digit); slots past them add to the global counts directly.
+#define EMIT_SORT_TILE 4096  // the sort's tile for 4-byte keys and values
+#define EMIT_HWIN 4
+struct EmitHist {
+  uint32_t* hist;      // tile_base[C] * 256 words
+  uint64_t words;      // bound of every index written
+  uint32_t mask;       // first-pass digit mask
+  uint32_t seg_start[TIDE_MAX_CAMS + 1];  // first intersection slot of each camera
+  uint32_t tile_base[TIDE_MAX_CAMS + 1];  // first sort tile of each camera
+};
+
+__device__ __forceinline__ void emit_hist_add(const EmitHist& eh, uint32_t c, uint32_t g,
+                                              uint32_t d, uint32_t n) {
+  const uint32_t tb = eh.tile_base[c];
+  const uint64_t idx = (uint64_t)tb * 256u + (uint64_t)d * (eh.tile_base[c + 1] - tb) + (g - tb);
+  if (idx < eh.words) atomicAdd(&eh.hist[idx], n);
+}
+
+template <bool HIST>
 __global__ void __launch_bounds__(256) tide_isect_emit_blocked_kernel(
     uint32_t n_entries, const int32_t* __restrict__ cam_offsets, uint32_t C,
     const uint64_t* __restrict__ rects, const uint32_t* __restrict__ block_base, uint32_t tw,
-    uint32_t tile_n_bits, uint32_t* __restrict__ keys, int32_t* __restrict__ flatten_ids) {
+    uint32_t tile_n_bits, uint32_t* __restrict__ keys, int32_t* __restrict__ flatten_ids,
+    EmitHist eh) {
   __shared__ int32_t s_off[TIDE_MAX_CAMS + 1];
   __shared__ uint32_t s_tot[EMIT_ITEMS][4];  // per round, each wavefront's area sum
+  __shared__ uint32_t s_h[HIST ? EMIT_HWIN : 1][256];
   if (threadIdx.x <= C) s_off[threadIdx.x] = cam_offsets[threadIdx.x];
+  uint32_t g_lo = 0;  // sort tile of the block's first slot
+  if (HIST) {
+#pragma unroll
+    for (int j = 0; j < EMIT_HWIN; ++j) s_h[j][threadIdx.x] = 0u;
+    const uint32_t r0 = block_base[blockIdx.x];
+    uint32_t cl = 0;
+    while (cl + 1 < C && eh.seg_start[cl + 1] <= r0) ++cl;
+    g_lo = eh.tile_base[cl] + (r0 - eh.seg_start[cl]) / EMIT_SORT_TILE;
+  }
   const uint32_t base = blockIdx.x * EMIT_ENTRIES;
   const uint32_t wave = threadIdx.x >> 6;
   uint64_t v[EMIT_ITEMS];
@@ -616,11 +650,36 @@ __global__ void __launch_bounds__(256) tide_isect_emit_blocked_kernel(
         for (uint32_t x = x0; x < x1; ++x) {
           keys[cur] = cam_enc | (y * tw + x);
           flatten_ids[cur] = id;
+          if (HIST) {
+            const uint32_t g = eh.tile_base[c] + (cur - eh.seg_start[c]) / EMIT_SORT_TILE;
+            const uint32_t d = (y * tw + x) & eh.mask;
+            if (g - g_lo < EMIT_HWIN) atomicAdd(&s_h[g - g_lo][d], 1u);
+            else emit_hist_add(eh, c, g, d, 1u);
+          }
           ++cur;
         }
     }
     run += round;
   }
+  if (HIST) {
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < EMIT_HWIN; ++j) {
+      const uint32_t n = s_h[j][threadIdx.x];
+      const uint32_t g = g_lo + (uint32_t)j;
+      if (n != 0u && g < eh.tile_base[C]) {
+        uint32_t cg = 0;
+        while (cg + 1 < C && eh.tile_base[cg + 1] <= g) ++cg;
+        emit_hist_add(eh, cg, g, threadIdx.x, n);
+      }
+    }
+  }
+}
+
+__global__ void tide_zero_u32_kernel(uint32_t* __restrict__ p, uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
 }
 
 // isect_offset_encode (isect_tiles.cu:234-301) over camera|tile keys.
@@ -1229,10 +1288,52 @@ extern "C" int tgs_tide_isect_emit_blocked(uint32_t n_entries, const int32_t* ca
   TGS_CHECK_ARG(cam_offsets && entry_rects && block_base && keys && flatten_ids,
                 "tide_isect_emit_blocked: null");
   TGS_CHECK_ARG(tile_n_bits <= 16, "tide_isect_emit_blocked: tile_n_bits must be <= 16");
-  hipLaunchKernelGGL(tide_isect_emit_blocked_kernel, dim3(tgs_tide_isect_emit_blocks(n_entries)),
-                     dim3(256), 0, stream, n_entries, cam_offsets, C, entry_rects, block_base,
-                     tile_width, tile_n_bits, keys, flatten_ids);
+  hipLaunchKernelGGL(tide_isect_emit_blocked_kernel<false>,
+                     dim3(tgs_tide_isect_emit_blocks(n_entries)), dim3(256), 0, stream, n_entries,
+                     cam_offsets, C, entry_rects, block_base, tile_width, tile_n_bits, keys,
+                     flatten_ids, EmitHist{});
   TGS_RETURN_LAUNCH("tgs_tide_isect_emit_blocked");
+}
+
+extern "C" int tgs_tide_isect_emit_blocked_hist(
+    uint32_t n_entries, const int32_t* cam_offsets, uint32_t C, const uint64_t* entry_rects,
+    const uint32_t* block_base, uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
+    int32_t* flatten_ids, const uint32_t* isect_cam_offsets, uint32_t digit_mask,
+    uint32_t* hist, uint64_t hist_words, hipStream_t stream) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  TGS_CHECK_ARG(cam_offsets && entry_rects && block_base && keys && flatten_ids &&
+                    isect_cam_offsets && hist,
+                "tide_isect_emit_blocked_hist: null");
+  TGS_CHECK_ARG(tile_n_bits <= 16, "tide_isect_emit_blocked_hist: tile_n_bits must be <= 16");
+  TGS_CHECK_ARG(digit_mask <= 255u, "tide_isect_emit_blocked_hist: digit_mask must be < 256");
+  EmitHist eh{};
+  eh.hist = hist;
+  eh.mask = digit_mask;
+  uint32_t tiles = 0;
+  for (uint32_t c = 0; c <= C; ++c) {
+    TGS_CHECK_ARG(c == 0 || isect_cam_offsets[c] >= isect_cam_offsets[c - 1],
+                  "tide_isect_emit_blocked_hist: offsets decrease");
+    eh.seg_start[c] = isect_cam_offsets[c];
+    eh.tile_base[c] = tiles;
+    if (c < C)
+      tiles += (isect_cam_offsets[c + 1] - isect_cam_offsets[c] + EMIT_SORT_TILE - 1) /
+               EMIT_SORT_TILE;
+  }
+  const uint64_t words = (uint64_t)tiles * 256u;
+  TGS_CHECK_ARG(words <= hist_words, "tide_isect_emit_blocked_hist: histogram buffer too small");
+  eh.words = words;
+  if (words) {
+    hipLaunchKernelGGL(tide_zero_u32_kernel, dim3((unsigned)((words + 255) / 256 < 4096 ? (words + 255) / 256 : 4096)),
+                       dim3(256), 0, stream, hist, words);
+    TGS_LAUNCH_CHECK("tide_zero_u32");
+  }
+  if (n_entries == 0) return TGS_OK;
+  hipLaunchKernelGGL(tide_isect_emit_blocked_kernel<true>,
+                     dim3(tgs_tide_isect_emit_blocks(n_entries)), dim3(256), 0, stream, n_entries,
+                     cam_offsets, C, entry_rects, block_base, tile_width, tile_n_bits, keys,
+                     flatten_ids, eh);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_emit_blocked_hist");
 }
 
 extern "C" int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, uint32_t C,

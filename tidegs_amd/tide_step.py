@@ -390,13 +390,19 @@ class TideStep:
         offsets = self._buf("offsets", n_buckets, torch.int32)
         self._begin("isect_sort")
         if n_isects:
-            N.call("tgs_tide_isect_emit_blocked", V, N.ptr(cam_offsets), C, N.ptr(rects),
-                   N.ptr(eb_base), tw, tile_bits, N.ptr(keys), N.ptr(fids), s)
-            sel = ctypes.c_int(0)
+            # the emission also counts the tile sort's first-pass digits into
+            # the sort's workspace, which then skips that pass's histogram
             tws = self._buf("sort_ws2", lib.tgs_segmented_sort_workspace_size(n_isects, C),
                             torch.uint8)
-            N.call("tgs_segmented_sort_pairs_u32", N.ptr(keys), N.ptr(fids), N.ptr(keys2),
-                   N.ptr(fids2), 4, n_isects, C, _segments(isect_segs), 0, tile_bits,
+            segs = _segments(isect_segs)
+            passes = (tile_bits + 7) // 8
+            mask0 = (1 << ((tile_bits + passes - 1) // passes)) - 1
+            N.call("tgs_tide_isect_emit_blocked_hist", V, N.ptr(cam_offsets), C, N.ptr(rects),
+                   N.ptr(eb_base), tw, tile_bits, N.ptr(keys), N.ptr(fids), segs, mask0,
+                   N.ptr(tws), tws.numel() // 4, s)
+            sel = ctypes.c_int(0)
+            N.call("tgs_segmented_sort_pairs_u32_hist0", N.ptr(keys), N.ptr(fids), N.ptr(keys2),
+                   N.ptr(fids2), n_isects, C, segs, 0, tile_bits,
                    N.ptr(tws), tws.numel(), ctypes.byref(sel), s)
             if sel.value:
                 keys, fids = keys2, fids2
