@@ -135,6 +135,68 @@ def test_blocked_emit_matches_offset_emit(gpu, V, C):
     np.testing.assert_array_equal(to_np(f)[:n_isects], to_np(f_ref)[:n_isects])
 
 
+@pytest.mark.parametrize("V,C,big", [(3000, 4, 0.0), (20_000, 6, 0.02), (70_000, 16, 0.001)])
+def test_emit_hist_then_hist0_sort(gpu, V, C, big):
+    """tgs_tide_isect_emit_blocked_hist + tgs_segmented_sort_pairs_u32_hist0 (the
+    emission counting the first pass's digit histogram) give the same sorted
+    keys and flatten ids as a stable per-camera sort of the emitted keys on the
+    tile bits (numpy), with empty cameras and rectangles spanning many sort
+    tiles (counted by the global-atomic path)."""
+    announce(f"emission histogram + hist0 sort V={V} C={C} big={big}")
+    import ctypes
+    from tidegs_amd import _native as N
+    lib = N.load()
+    rng = np.random.default_rng(V * 7 + C)
+    tw, th = 120, 68
+    x0 = rng.integers(0, tw, V)
+    y0 = rng.integers(0, th, V)
+    wide = rng.random(V) < big
+    x1 = np.minimum(x0 + np.where(wide, rng.integers(20, 120, V), rng.integers(0, 5, V)), tw)
+    y1 = np.minimum(y0 + np.where(wide, rng.integers(20, 68, V), rng.integers(0, 4, V)), th)
+    rc = (x0 | (x1 << 8) | (y0 << 16) | (y1 << 24)).astype(np.uint64)
+    ids = rng.integers(0, 1 << 30, V).astype(np.uint64)
+    rects = torch.from_numpy(((rc << np.uint64(32)) | ids).view(np.int64)).to(gpu)
+    cuts = np.sort(rng.choice(np.arange(1, V), size=C - 2, replace=False))
+    cam = np.concatenate([[0], cuts[:1], cuts[:1], cuts[1:], [V]]).astype(np.int64)  # camera 1 empty
+    cam_off = torch.tensor(cam.astype(np.int32), device=gpu)
+    area = (x1 - x0) * (y1 - y0)
+    isect_off = np.array([area[cam[c]:cam[c + 1]].sum() for c in range(C)]).cumsum()
+    segs = [0] + [int(v) for v in isect_off]
+    n_isects = segs[-1]
+    tile_bits = (tw * th).bit_length()
+    s = N.stream_handle()
+    nb = lib.tgs_tide_isect_emit_blocks(V)
+    sums = torch.empty(nb, dtype=torch.int32, device=gpu)
+    base = torch.empty(nb, dtype=torch.int32, device=gpu)
+    ws2 = torch.empty(lib.tgs_scan_workspace_size(nb), dtype=torch.uint8, device=gpu)
+    N.call("tgs_tide_isect_block_sums", V, N.ptr(rects), N.ptr(sums), s)
+    N.call("tgs_exclusive_scan_u32", N.ptr(sums), N.ptr(base), nb, N.ptr(ws2), ws2.numel(), s)
+    k = torch.empty(n_isects, dtype=torch.int32, device=gpu)
+    f = torch.empty(n_isects, dtype=torch.int32, device=gpu)
+    N.call("tgs_tide_isect_emit_blocked", V, N.ptr(cam_off), C, N.ptr(rects), N.ptr(base), tw,
+           tile_bits, N.ptr(k), N.ptr(f), s)
+    k_in, f_in = to_np(k).view(np.uint32), to_np(f)
+    hs = (ctypes.c_uint32 * (C + 1))(*segs)
+    passes = (tile_bits + 7) // 8
+    mask0 = (1 << ((tile_bits + passes - 1) // passes)) - 1
+    ws = torch.empty(lib.tgs_segmented_sort_workspace_size(n_isects, C), dtype=torch.uint8,
+                     device=gpu)
+    k2, f2 = torch.empty_like(k), torch.empty_like(f)
+    N.call("tgs_tide_isect_emit_blocked_hist", V, N.ptr(cam_off), C, N.ptr(rects), N.ptr(base),
+           tw, tile_bits, N.ptr(k), N.ptr(f), hs, mask0, N.ptr(ws), ws.numel() // 4, s)
+    np.testing.assert_array_equal(to_np(k).view(np.uint32), k_in)
+    sel = ctypes.c_int(0)
+    N.call("tgs_segmented_sort_pairs_u32_hist0", N.ptr(k), N.ptr(f), N.ptr(k2), N.ptr(f2),
+           n_isects, C, hs, 0, tile_bits, N.ptr(ws), ws.numel(), ctypes.byref(sel), s)
+    ko, fo = (k2, f2) if sel.value else (k, f)
+    ko, fo = to_np(ko).view(np.uint32), to_np(fo)
+    tmask = np.uint32((1 << tile_bits) - 1)
+    for a, b in zip(segs[:-1], segs[1:]):
+        order = np.argsort(k_in[a:b] & tmask, kind="stable") + a
+        np.testing.assert_array_equal(ko[a:b], k_in[order])
+        np.testing.assert_array_equal(fo[a:b], f_in[order])
+
+
 def test_tide_step_isect_bit_exact(gpu):
     announce("tide step isect")
     sc = _scene(seed=2)
