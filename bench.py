@@ -42,6 +42,17 @@ BYTES = {
     "raster_bwd": lambda s: s["C"] * s["P"] * 24 + s["I"] * 40 + s["V"] * 72,
     "project_bwd": lambda s: s["T"] * (4 + 4 + 4 + 236 + 236) + s["V"] * (4 + 36),
     "adam": lambda s: s["T"] * 1656,
+    # intersection stages, as this design's passes move them: the depth sort
+    # of the V entries (per pass 4 B key + 8 B (rectangle, entry) read and
+    # written, + the 4 B key read of its histogram), the per-block area sums
+    # (8 B rectangle read); the emission (8 B rectangle read per entry, 4 B
+    # key + 4 B flatten id written per intersection), the tile-bit sort (per
+    # pass 8 B read + 8 B written per intersection, + 4 B histogram key read
+    # on every pass but the first, which the emission counts) and the offset
+    # encode (4 B key read per intersection, 4 B per bucket written)
+    "isect_scan": lambda s: s["V"] * (s["passes_d"] * (24 + 4) + 8),
+    "isect_sort": lambda s: (8 * s["V"] + 8 * s["I"] + s["passes_t"] * 16 * s["I"]
+                             + (s["passes_t"] - 1) * 4 * s["I"] + 4 * s["I"] + 4 * s["buckets"]),
     # fused: the row read once, p/m/v written, m/v read; no gradient rows
     "project_bwd_update": lambda s: (s["T"] * (4 + 4 + 4 + 236 + 2 * 236 + 3 * 236)
                                      + s["V"] * (4 + 36)),
@@ -65,24 +76,89 @@ SIMDS = 1024  # 256 CUs x 4 SIMDs
 XCDS = 8      # GRBM_GUI_ACTIVE sums the 8 XCDs' busy clocks
 
 
+def source_sha16(rel: str) -> str:
+    """First 16 hex digits of the SHA-256 of a repository file."""
+    import hashlib
+
+    return hashlib.sha256((ROOT / rel).read_bytes()).hexdigest()[:16]
+
+
 def profiled_valu(kernel: str):
     """VALU counters of one launch of `kernel` at cfg3 from the committed
     rocprofv3 PMC summary (profiles/*_valu.md): SQ_INSTS_VALU (wave64
     instructions), SQ_ACTIVE_INST_VALU (VALU quad-cycles summed over waves),
     SQ_THREAD_CYCLES_VALU (active lanes x VALU instructions), GRBM_GUI_ACTIVE
-    and the launch's duration in that run, or None."""
+    and the launch's duration in that run, or None.  The summary names the
+    source file the kernel was built from and its hash at profiling time
+    (``valu_source <kernel>: <file> <sha16>``); ``source_matches`` tells
+    whether that file is unchanged since, i.e. whether the counts describe the
+    kernel this run timed."""
     import re
 
     for f in sorted((ROOT / "profiles").glob("*_valu.md")):
-        m = re.search(rf"^valu_counters {re.escape(kernel)}: (.*)$", f.read_text(), re.M)
+        text = f.read_text()
+        m = re.search(rf"^valu_counters {re.escape(kernel)}: (.*)$", text, re.M)
         if m:
-            return {k: float(v) for k, v in re.findall(r"(\w+)=([0-9.eE+-]+)", m.group(1))}
+            out = {k: float(v) for k, v in re.findall(r"(\w+)=([0-9.eE+-]+)", m.group(1))}
+            src = re.search(rf"^valu_source {re.escape(kernel)}: (\S+) ([0-9a-f]{{16}})$", text,
+                            re.M)
+            out["source"] = f"{src.group(1)} {src.group(2)}" if src else None
+            out["source_matches"] = bool(src) and (ROOT / src.group(1)).exists() and \
+                source_sha16(src.group(1)) == src.group(2)
+            return out
     return None
 
 
 # tgs_valu_probe's instruction forms, in its `form` order
 VALU_FORMS = ("mul_f32_vgpr", "mul_f32_sgpr", "add_u32_vgpr", "xor_b32_sgpr", "fma_f32_vgpr",
               "exp_f32")
+# the probe is a measurement aid of this benchmark only: its own library,
+# built from bench_valu_probe.hip beside this file, not part of libtidegs_amd.so
+PROBE_SRC = ROOT / "bench_valu_probe.hip"
+PROBE_LIB = ROOT / "bench_valu_probe.so"
+_probe = None
+
+
+def build_valu_probe() -> Path:
+    """Compile bench_valu_probe.so for gfx950 (hipcc, the library's flags)."""
+    import subprocess
+
+    from tidegs_amd import build as B
+
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [B._hipcc(), *B.HIPCC_FLAGS, "-shared", str(PROBE_SRC), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
+def valu_probe_lib():
+    """The probe library (after torch, so that both share one HIP runtime);
+    built here if missing."""
+    global _probe
+    if _probe is None:
+        import ctypes
+
+        import torch  # noqa: F401
+
+        if not PROBE_LIB.exists():
+            build_valu_probe()
+        lib = ctypes.CDLL(str(PROBE_LIB))
+        lib.tgs_valu_probe.restype = ctypes.c_int
+        lib.tgs_valu_probe.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                       ctypes.c_int32, ctypes.c_void_p]
+        _probe = lib
+    return _probe
+
+
+def valu_probe(out, blocks: int, iters: int, form: int, stream: int) -> None:
+    """Launch tgs_valu_probe (8 * iters wave64 VALU instructions of one form
+    per wavefront, 4 wavefronts per block) into out[blocks * 256]."""
+    rc = valu_probe_lib().tgs_valu_probe(out.data_ptr(), blocks, iters, form, stream)
+    if rc != 0:
+        raise RuntimeError(f"tgs_valu_probe failed (code {rc})")
 
 
 def valu_peak(dev, blocks: int = 8192, iters: int = 4096, form: int = 0) -> float:
@@ -93,16 +169,14 @@ def valu_peak(dev, blocks: int = 8192, iters: int = 4096, form: int = 0) -> floa
     VALU roofline's peak."""
     import torch
 
-    from tidegs_amd import _native as N
-
     out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
-    s = N.stream_handle(dev)
-    N.call("tgs_valu_probe", N.ptr(out), blocks, 64, form, s)  # warm-up
+    s = torch.cuda.current_stream(dev).cuda_stream
+    valu_probe(out, blocks, 64, form, s)  # warm-up
     best = float("inf")
     for _ in range(3):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        N.call("tgs_valu_probe", N.ptr(out), blocks, iters, form, s)
+        valu_probe(out, blocks, iters, form, s)
         b.record()
         b.synchronize()
         best = min(best, a.elapsed_time(b) * 1e-3)
@@ -127,6 +201,7 @@ def valu_roofline(c: dict, live_pairs: int, event_ms: float, peak: float):
     rate = c["SQ_INSTS_VALU"] / (event_ms * 1e-3)
     out = {"bound": "valu", "frac": round(rate / peak, 4),
            "measure": "VALU issue rate / two-source FP32 VGPR stream (tgs_valu_probe)",
+           "counts_from": c.get("source"), "counts_match_source": c.get("source_matches"),
            "insts_per_launch": int(c["SQ_INSTS_VALU"]),
            "insts_per_s": round(rate / 1e9, 1) * 1e9, "peak_insts_per_s": round(peak / 1e9, 1) * 1e9,
            "busy_4cycle_basis": round(busy, 4),
@@ -270,20 +345,32 @@ WORKLOADS = {
 
 def _stage_kernels(ts, stats, args, stage_ms, C, P):
     Vvis = int(ts.last_visible_entries)
+    tile_bits = (ts.tw * ts.th).bit_length()
     shape = {"N": ts.params.shape[0], "C": C, "P": P, "V": stats.entries, "Vvis": Vvis,
-             "I": stats.n_isects, "T": stats.touched_rows, "tiles": ts.tw * ts.th}
+             "I": stats.n_isects, "T": stats.touched_rows, "tiles": ts.tw * ts.th,
+             "buckets": C * ts.tw * ts.th, "passes_d": (ts.last_depth_key_bits + 7) // 8,
+             "passes_t": (tile_bits + 7) // 8}
+    # the reference design's figures for the same stages (isect_tiles.cu:14-301
+    # count + emit, 20 B per visible entry + 12 B per intersection, and cub's
+    # LSD sort of 8 B key + 4 B value pairs, 24 B per intersection and pass
+    # over the 32 + tile + camera bits in passes of 8)
+    ref_passes = (32 + tile_bits + (C - 1).bit_length() + 7) // 8
+    scope = {"isect_scan": 20 * stats.entries + 12 * stats.n_isects,
+             "isect_sort": 24 * ref_passes * stats.n_isects}
     kernels = {}
     for name, f in BYTES.items():
         if name in stage_ms and stage_ms[name] > 0:
             b = f(shape)
             kernels[name] = {"ms": stage_ms[name], "bytes": b,
                              "GBs": round(b / (stage_ms[name] * 1e-3) / 1e9, 1)}
+            if name in scope:
+                kernels[name]["reference_design_bytes"] = scope[name]
     return kernels
 
 
 def _tile_load(ts, stats):
     """Max and 99th percentile of the intersections per (camera, tile) of the
-    last step, from its bucket offsets."""
+    step ``stats`` describes, from that step's bucket offsets."""
     import torch
 
     offs = ts.last["offsets"].reshape(-1).to(torch.int64)
@@ -294,7 +381,17 @@ def _tile_load(ts, stats):
 
 
 def bench_step(args, dev):
-    """Full TideGS step (cfg3, cfg4) or the rasterizer pair alone (cfg2)."""
+    """Full TideGS step (cfg3, cfg4) or the rasterizer pair alone (cfg2).
+
+    Every step (warm-up, timed, stage-timed and the pair-counting one) runs
+    from the same scene state: the seeded scene as generated, with cold
+    optimizer moments.  The resident table, the moments and the slot
+    bookkeeping are snapshotted before the first step and put back before
+    each step, outside its timed bracket, so that a step does the whole
+    forward + backward + update of that one state however many steps ran
+    before it, and the counts reported beside the time (visible entries,
+    intersections, live pairs) and the profiles describe the step that was
+    timed."""
     import torch
 
     from tidegs_amd import scenes
@@ -312,15 +409,25 @@ def bench_step(args, dev):
     table = scenes.padded_table(sc.params.contiguous())
     del sc.params
     ts = TideStep(table, sc.width, sc.height, batch_size=C, fuse_update=not args.split_update)
+    snap = ts.snapshot()
+
+    def one_step(**kw):
+        """One step from the pinned state: (stats, wall seconds between two
+        device synchronisations around the step alone)."""
+        ts.restore(snap)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        st = ts.step(sc.viewmats, sc.Ks, sc.gt, **kw)
+        torch.cuda.synchronize()
+        return st, time.perf_counter() - t0
 
     for _ in range(args.warmup):
-        ts.step(sc.viewmats, sc.Ks, sc.gt)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
+        one_step()
+    wall = []
     for _ in range(args.steps):
-        stats = ts.step(sc.viewmats, sc.Ks, sc.gt)
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+        stats, dt = one_step()
+        wall.append(dt)
+    ms = sum(wall) * 1000.0 / args.steps
 
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration * (1 << 20) // 4, device=dev)
@@ -331,20 +438,20 @@ def bench_step(args, dev):
         del src, dst
 
     # Per-stage kernel times from HIP events on the launch stream (separate
-    # pass so the timed loop above carries no event overhead).
+    # steps, so the timed ones above carry no event overhead).
     stage_ms = {}
     if not args.no_stage_timing or args.workload == "cfg2":
         reps = 3
         acc = {}
         for _ in range(reps):
-            st = ts.step(sc.viewmats, sc.Ks, sc.gt, timing=True)
+            stats, _ = one_step(timing=True)
             for k, v in ts.stage_ms.items():
                 acc[k] = acc.get(k, 0.0) + v
         stage_ms = {k: round(v / reps, 4) for k, v in acc.items()}
-        stats = st
-        # one more step, untimed, with the forward counting the composited
-        # (Gaussian, pixel) pairs (its counting walk is slower than the plain one)
-        ts.step(sc.viewmats, sc.Ks, sc.gt, count_pairs=True)
+    # one more step, untimed, with the forward counting the composited
+    # (Gaussian, pixel) pairs (its counting walk is slower than the plain one)
+    stats, _ = one_step(count_pairs=True)
+    tile_load = _tile_load(ts, stats)
     P = sc.width * sc.height
     kernels = _stage_kernels(ts, stats, args, stage_ms, C, P)
     default_cfg = (args.workload == "cfg3" and
@@ -362,6 +469,9 @@ def bench_step(args, dev):
         # the compositing kernels are limited by VALU issue, not HBM
         valu = profiled_valu(dominant) if default_cfg else None
         if valu:
+            # the compositing kernels are limited by VALU issue, not HBM: the
+            # VALU roofline below is the one that bounds them
+            roofline["limited_by"] = "valu"
             rates = {name: valu_peak(dev, form=f) for f, name in enumerate(VALU_FORMS)}
             roofline["valu"] = valu_roofline(valu, getattr(ts, "last_live_pairs", 0), d["ms"],
                                              rates[VALU_FORMS[0]])
@@ -391,21 +501,34 @@ def bench_step(args, dev):
                    "height": sc.height, "visible_entries": stats.entries,
                    "touched_rows": stats.touched_rows, "isects": stats.n_isects,
                    "isects_per_tile": round(stats.n_isects / (C * ts.tw * ts.th), 1),
-                   **_tile_load(ts, stats),
+                   **tile_load, "scene_state": "seeded scene, restored before every step",
                    "optimizer_update": "split" if args.split_update else "fused",
                    "live_pairs": int(getattr(ts, "last_live_pairs", 0))},
         "bwd_hbm_GBs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1) if bwd_ms else None,
         "roofline": roofline,
         "stage_ms": stage_ms,
+        # step time not covered by any stage bracket (host launch latency at
+        # the step's start and its final synchronisation)
+        "unbracketed_ms": round(ms - sum(stage_ms.values()), 3) if stage_ms else None,
         "kernels": kernels,
         "cpu_baseline": None,
     }
     if args.workload == "cfg3" and not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.width, args.height, stats)
+    if default_cfg and not args.no_dropin:
+        # the same step through the drop-in ops at TideGS's unchanged
+        # per-camera call sites, in its own loop after the headline
+        del ts, snap
+        torch.cuda.empty_cache()
+        d = bench_dropin(args, dev, steps=3, warmup=1)
+        line["dropin"] = {"ms_per_step": d["ms_per_step"], "steps": d["steps"],
+                          "warmup": d["warmup"], "workload": d["config"]["workload"],
+                          "visible_entries": d["config"]["visible_entries"],
+                          "isects": d["config"]["isects"]}
     return line
 
 
-def bench_dropin(args, dev):
+def bench_dropin(args, dev, steps=None, warmup=None):
     """cfg3 through the drop-in ops at TideGS's own call sites, camera by
     camera, as the reference's batch loop runs them
     (``strategies/base_engine.py:329-425`` filters,
@@ -503,22 +626,37 @@ def bench_dropin(args, dev):
         opt.step(state["it"], g, touched, grads)
         state["visible"], state["isects"], state["touched"] = sum(counts), n_isect, touched.numel()
 
-    for _ in range(args.warmup):
-        step()
+    # every step from the same scene state, as in bench_step: the component
+    # tensors and the optimizer state are put back before each step, outside
+    # its timed bracket
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
+    saved = {name: getattr(g, "_" + name).clone() for name in comp}
+    opt_snap = opt.snapshot()
+
+    def one_step():
+        for name in comp:
+            getattr(g, "_" + name).copy_(saved[name])
+        opt.restore(opt_snap)
+        state["it"] = 0
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
         step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
+    for _ in range(warmup):
+        one_step()
+    ms = sum(one_step() for _ in range(steps)) * 1000.0 / steps
     return {
         "metric": "ms/train-step (fwd+bwd+Adam) at 4M Gaussians, 16×1080p, drop-in ops at "
                   "TideGS's per-camera call sites",
         "value": round(ms, 3),
         "unit": "ms",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms, 3),
         "higher_is_better": False,
         "scaling": "weak",
@@ -918,6 +1056,8 @@ def main():
     ap.add_argument("--height", type=int, default=1080)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-timing", action="store_true")
+    ap.add_argument("--no-dropin", action="store_true",
+                    help="cfg3: skip the drop-in call-site step timed after the headline")
     ap.add_argument("--split-update", action="store_true",
                     help="cfg3/cfg4: optimizer update as its own launch over materialised "
                          "gradient rows instead of inside the projection backward")

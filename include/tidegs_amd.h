@@ -37,16 +37,6 @@ int tgs_abi_version(void);
 const char* tgs_last_error(void);
 /* Zero/constant fill used instead of hipMemsetAsync (kernel node under capture). */
 int tgs_fill_u32(void* ptr, uint64_t n_words, uint32_t value, tgs_stream_t stream);
-/* Measurement aid with no counterpart in the reference: `blocks` workgroups of
- * 256 threads each run `iters` rounds of 8 independent operations of one
- * instruction form (8 * iters wave64 VALU instructions per wavefront) and
- * store their sums to out[blocks * 256].  form 0: v_mul_f32 on VGPRs (the
- * fastest-issuing form: its rate is the peak the compositing kernels' VALU
- * roofline is quoted against); 1: v_mul_f32 with an SGPR operand; 2:
- * v_add_u32 on VGPRs; 3: v_xor_b32 with an SGPR operand; 4: v_fma_f32 on
- * VGPRs; 5: v_exp_f32. */
-int tgs_valu_probe(float* out, uint32_t blocks, uint32_t iters, int32_t form,
-                   tgs_stream_t stream);
 
 /* ---- projection ------------------------------------------------------- */
 /* Replaces fully_fused_projection_fwd_tensor
@@ -350,7 +340,12 @@ int tgs_tide_compact(uint64_t n_rows, uint32_t C, const uint32_t* masks, const u
  * capacity (rows beyond the device count do nothing).  isect_totals (device,
  * may be null) receives the per-camera intersection counts [C] (int64, the
  * sums of the rectangles' areas; the call zeroes it first), so the host can
- * size the intersection buffers while the depth sort runs. */
+ * size the intersection buffers while the depth sort runs.  depth_range
+ * (device, may be null) receives 64 {min, max} uint32 pairs (the call
+ * initialises them) whose min / max are the smallest and largest depth key
+ * written, culled entries' 0xffffffff excluded: the host checks with them
+ * that the depth sort's key range, taken from tgs_tide_visibility's
+ * depth_range, holds every key. */
 int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touched_dev,
                          const int32_t* touched, const int32_t* visit_base,
                          const int32_t* visits, const uint32_t* masks, uint32_t C,
@@ -360,7 +355,7 @@ int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touched_dev,
                          float far_plane, float radius_clip, int32_t sh_degree,
                          uint32_t tile_size, uint32_t tile_width, uint32_t tile_height,
                          float* splats, uint32_t* depth_keys, uint64_t* entry_rects,
-                         int64_t* isect_totals, tgs_stream_t stream);
+                         int64_t* isect_totals, uint32_t* depth_range, tgs_stream_t stream);
 /* Intersections of the batch in the order of the reference's sort
  * (isect_tiles.cu:73-98,189-227: camera, tile, depth bits, entry).  After
  * tgs_segmented_sort_pairs_u32 of (depth_keys, entry_rects) per camera:
@@ -405,16 +400,17 @@ int tgs_tide_isect_emit_blocked(uint32_t n_entries, const int32_t* cam_offsets, 
                                 uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
                                 int32_t* flatten_ids, tgs_stream_t stream);
 /* Beside the reference's interface: tgs_tide_isect_emit_blocked that also
- * counts the tile-bit sort's first-pass digits (tile & digit_mask) into hist,
- * in the layout tgs_segmented_sort_pairs_u32_hist0 reads (segments = cameras,
- * isect_cam_offsets = the C + 1 host-side first intersections per camera);
- * hist (hist_words uint32 words, e.g. the sort's workspace) is cleared first. */
+ * counts the digits of the first pass of tgs_segmented_sort_pairs_u32_hist0
+ * over bits [0, tile_n_bits) (tile & (2^w - 1), w = ceil(tile_n_bits / p),
+ * p = ceil(tile_n_bits / 8)) into hist, in the layout that sort reads
+ * (segments = cameras, isect_cam_offsets = the C + 1 host-side first
+ * intersections per camera); hist (hist_words uint32 words, e.g. the sort's
+ * workspace) is cleared first. */
 int tgs_tide_isect_emit_blocked_hist(uint32_t n_entries, const int32_t* cam_offsets, uint32_t C,
                                      const uint64_t* entry_rects, const uint32_t* block_base,
                                      uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
                                      int32_t* flatten_ids, const uint32_t* isect_cam_offsets,
-                                     uint32_t digit_mask, uint32_t* hist, uint64_t hist_words,
-                                     tgs_stream_t stream);
+                                     uint32_t* hist, uint64_t hist_words, tgs_stream_t stream);
 int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, uint32_t C,
                            uint32_t tile_width, uint32_t tile_height, uint32_t tile_n_bits,
                            int32_t* offsets, tgs_stream_t stream);

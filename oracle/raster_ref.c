@@ -145,3 +145,73 @@ void FN(oracle_raster_bwd)(int C, int D, const REAL* means2d, const REAL* conics
     }
   }
 }
+
+/* Which compositing decisions of the forward (the alpha >= 1/255 test and
+ * the T <= 1e-4 stop of rasterize_to_pixels_fwd.cu:110-131) differ between
+ * two sets of splat parameters over the same intersection lists: set A
+ * (means2d_a, conics_a, opac_a) and set B, e.g. the same Gaussians projected
+ * by two float32 evaluations.  A pixel whose sequence of decisions differs
+ * is flagged in flip_pix [C,H,W] (uint8), and every entry that composites
+ * into such a pixel under either set is flagged in entry_flag [*] (uint8):
+ * those are the entries whose gradients a float32 rounding of the
+ * projection can move by a whole pixel's contribution.  mark_pix [C,H,W]
+ * (nullable) names more pixels whose composited entries are flagged too
+ * (e.g. the neighbourhood through which a loss couples pixels). */
+static int FN(decide)(const REAL* means2d, const REAL* conics, const REAL* opac, int g, REAL px,
+                      REAL py, REAL* T) {
+  /* 0: skipped, 1: composited, 2: stop (T would reach the threshold) */
+  const REAL dx = means2d[2 * (int64_t)g] - px, dy = means2d[2 * (int64_t)g + 1] - py;
+  const REAL a = conics[3 * (int64_t)g], b = conics[3 * (int64_t)g + 1],
+             cc = conics[3 * (int64_t)g + 2];
+  const REAL sigma = (REAL)0.5 * (a * dx * dx + cc * dy * dy) + b * dx * dy;
+  const REAL alpha = rmin((REAL)0.999, opac[g] * rexp(-sigma));
+  if (sigma < 0 || alpha < (REAL)1 / (REAL)255) return 0;
+  const REAL next_T = *T * (1 - alpha);
+  if (next_T <= (REAL)1e-4) return 2;
+  *T = next_T;
+  return 1;
+}
+
+void FN(oracle_raster_decision_flips)(int C, const REAL* means2d_a, const REAL* conics_a,
+                                      const REAL* opac_a, const REAL* means2d_b,
+                                      const REAL* conics_b, const REAL* opac_b, int W, int H,
+                                      int tile, int tw, int th, const int32_t* offsets,
+                                      const int32_t* flat, int n_isects, const uint8_t* mark_pix,
+                                      uint8_t* flip_pix, uint8_t* entry_flag) {
+  for (int c = 0; c < C; ++c) {
+    for (int i = 0; i < H; ++i) {
+      for (int j = 0; j < W; ++j) {
+        const int tid = (i / tile) * tw + (j / tile);
+        const int64_t toff = (int64_t)c * th * tw + tid;
+        const int start = offsets[toff];
+        const int end = (c == C - 1 && tid == tw * th - 1) ? n_isects : offsets[toff + 1];
+        const REAL px = (REAL)j + (REAL)0.5, py = (REAL)i + (REAL)0.5;
+        const int64_t pid = ((int64_t)c * H + i) * W + j;
+        REAL Ta = 1, Tb = 1;
+        int differ = 0, done_a = 0, done_b = 0;
+        for (int idx = start; idx < end && !(done_a && done_b); ++idx) {
+          const int g = flat[idx];
+          const int da = done_a ? -1 : FN(decide)(means2d_a, conics_a, opac_a, g, px, py, &Ta);
+          const int db = done_b ? -1 : FN(decide)(means2d_b, conics_b, opac_b, g, px, py, &Tb);
+          if (da != db) differ = 1;
+          if (da == 2) done_a = 1;
+          if (db == 2) done_b = 1;
+        }
+        flip_pix[pid] = (uint8_t)differ;
+        if (!(differ || (mark_pix && mark_pix[pid]))) continue;
+        /* second walk: flag the entries composited under either set */
+        Ta = 1;
+        Tb = 1;
+        done_a = done_b = 0;
+        for (int idx = start; idx < end && !(done_a && done_b); ++idx) {
+          const int g = flat[idx];
+          const int da = done_a ? -1 : FN(decide)(means2d_a, conics_a, opac_a, g, px, py, &Ta);
+          const int db = done_b ? -1 : FN(decide)(means2d_b, conics_b, opac_b, g, px, py, &Tb);
+          if (da == 1 || db == 1) entry_flag[g] = 1;
+          if (da == 2) done_a = 1;
+          if (db == 2) done_b = 1;
+        }
+      }
+    }
+  }
+}

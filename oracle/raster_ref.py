@@ -171,3 +171,31 @@ def rasterize_bwd(means2d, conics, colors, opac, W, H, tile_size, offsets, flatt
        ctypes.c_int(th), _p(offsets), _p(flatten_ids), ctypes.c_int(flatten_ids.size), _p(alphas),
        _p(last_ids), _p(v_colors), _p(v_alphas), _p(vm), _p(vc), _p(vcol), _p(vo), _p(va))
     return vm, vc, vcol, vo, va
+
+
+def decision_flips(splats_a, splats_b, W, H, tile_size, offsets, flatten_ids,
+                   dtype=np.float32, mark=None):
+    """Compositing decisions (alpha >= 1/255, the T <= 1e-4 stop) that differ
+    between two parameter sets of the same entries over the same intersection
+    lists.  ``splats_*`` = (means2d [*,2], conics [*,3], opacities [*]).
+    Returns (flipped pixels [C,H,W] bool, entries composited under either set
+    at a flipped pixel or at a pixel of ``mark`` [C,H,W] bool)."""
+    suffix = "f32" if dtype == np.float32 else "f64"
+    cvt = lambda a: np.ascontiguousarray(a, dtype=dtype)  # noqa: E731
+    ma, ca, oa = map(cvt, splats_a)
+    mb, cb, ob = map(cvt, splats_b)
+    assert ma.shape == mb.shape and ca.shape == cb.shape and oa.shape == ob.shape
+    offsets = np.ascontiguousarray(offsets, dtype=np.int32)
+    flatten_ids = np.ascontiguousarray(flatten_ids, dtype=np.int32)
+    C, th, tw = offsets.shape
+    flip = np.zeros((C, H, W), dtype=np.uint8)
+    flag = np.zeros(oa.shape[0], dtype=np.uint8)
+    mark = None if mark is None else np.ascontiguousarray(mark, dtype=np.uint8)
+    assert mark is None or mark.shape == (C, H, W)
+    fn = getattr(_lib(), f"oracle_raster_decision_flips_{suffix}")
+    fn.restype = None
+    fn(ctypes.c_int(C), _p(ma), _p(ca), _p(oa), _p(mb), _p(cb), _p(ob), ctypes.c_int(W),
+       ctypes.c_int(H), ctypes.c_int(tile_size), ctypes.c_int(tw), ctypes.c_int(th),
+       _p(offsets), _p(flatten_ids), ctypes.c_int(flatten_ids.size), _p(mark), _p(flip),
+       _p(flag))
+    return flip.astype(bool), flag.astype(bool)

@@ -24,13 +24,28 @@ Each oracle comparison runs in four stages:
     compositing forward, loss and its gradient, compositing backward, and the
     projection + SH + activation backward into the row gradients, each within
     relative L2 1e-4 (measured 1e-7..3e-5).
-(D) the oracle end to end from the rows (its own float64 projection).  At
-    1080p a float32 and a float64 forward differ at a few alpha = 1/255
-    cut-offs (a pixel moves by up to 4e-3), and where such a pixel crosses
-    its random target the L1 gradient changes sign: one flip alone moves the
-    loss gradient by 2/sqrt(3 W H) = 8e-4 relative L2 at 1920x1080.  So (D)
-    is bounded loosely (1e-2; 5e-2 for the 320x256 window, where one flip is
-    4e-3) and prints the flips; the 1e-4 bound is held in (C).
+(D) the oracle end to end from the rows, with its projection in float32 as
+    the kernels compute it, against the GPU's row gradients.  The target is
+    drawn 0.3 away from the GPU's rendered image in every channel (above or
+    below it at random, inside [0, 1]), so that no pixel's L1 sign can differ
+    between the two evaluations: a single sign flip would move the loss
+    gradient by 2 / sqrt(3 W H) (8e-4 relative L2 at 1920x1080) whatever
+    the arithmetic.  Two float32 projections of one Gaussian still differ:
+    at 1080p its mean lands ~1e-4 px apart (up to 2e-3 px where the camera
+    transform cancels), which (1) puts a few alpha = 1/255 and T = 1e-4
+    decisions on opposite sides of their cut, each moving a whole pixel's
+    contribution, and (2) moves every position-dependent gradient by about
+    that shift over the Gaussian's size (~6e-5 relative).  The oracle finds
+    the decisions of (1) itself (``raster_ref.decision_flips``: its float32
+    splat values against the GPU's records over the same lists) and the rows
+    composited at such a pixel (well under 5%) are set aside; every other
+    row is held to relative L2 <= 1e-4 per gradient group on the 250k-row
+    subset at 1920x1080 (measured up to 9.2e-5, the floor that (2) sets) and
+    to 2e-4 on the dense window, whose stacks are deeper (measured up to
+    1.01e-4).  gsplat's own test compares its CUDA and torch rasterizers on
+    identical inputs at rtol 1e-3..5e-3 (test_basic.py:537-541).  The
+    distances over all rows, and to the oracle's float64 projection, are
+    printed.
 
 """
 import numpy as np
@@ -151,13 +166,31 @@ def _check_downstream(ts, stats, params, g_filters, vm, K, gt, W, H, grads):
         assert err < 1e-4, (name, err)
 
 
-def _parity(gpu, params, vm, K, gt, W, H, label, end_to_end_bound):
+def _target_away_from(images, seed):
+    """A [C,3,H,W] target in 0-255 units whose every channel lies 0.3 from
+    the [C,H,W,3] image in [0, 1] (above or below at random; below where
+    above would leave [0, 1], above where below would)."""
+    img = np.asarray(images, np.float64)
+    sgn = np.where(np.random.default_rng(seed).random(img.shape) < 0.5, -1.0, 1.0)
+    t = img + 0.3 * sgn
+    t = np.where(t > 1.0, img - 0.3, t)
+    t = np.where(t < 0.0, img + 0.3, t)
+    t = np.clip(t, 0.0, 1.0)
+    assert np.abs(np.clip(img, 0, None) - t).min() >= 0.1 - 1e-6
+    return torch.from_numpy((t * 255.0).transpose(0, 3, 1, 2).astype(np.float32))
+
+
+def _parity(gpu, params, vm, K, gt, W, H, label, end_to_end_bound=1e-4):
     """forward_backward on the GPU (resident table at the bench's 256-byte row
     pitch) against the step oracle: (A) filters, (B) render projection, (C)
-    the rest on identical inputs, (D) the oracle end to end."""
+    the rest on identical inputs, (D) the oracle end to end.  ``gt`` seeds
+    the target of (D), drawn away from the GPU's image."""
     table = scenes.padded_table(params.to(gpu).contiguous())
     C = vm.shape[0]
     ts = TideStep(table, W, H, batch_size=C)
+    ts.forward_backward(vm, K, gt)
+    torch.cuda.synchronize()
+    gt = _target_away_from(to_np(ts.last["images"]), int(gt.flatten()[0]))
     touched, grads, stats = ts.forward_backward(vm, K, gt)
     torch.cuda.synchronize()
     # (A) filters: exact off float32 rounding boundaries
@@ -181,28 +214,55 @@ def _parity(gpu, params, vm, K, gt, W, H, label, end_to_end_bound):
     assert stats.entries > 50_000 and flips <= max(3, stats.entries // 20_000)
     _check_render_projection(ts, params, g_filters, vm, K, W, H)       # (B)
     _check_downstream(ts, stats, params, g_filters, vm, K, gt, W, H, grads)  # (C)
-    # (D) the oracle end to end from the row parameters (its own float64
-    # projection, intersected on the GPU's float32 means/radii/depths)
+    # (D) the oracle end to end from the row parameters (its own projection,
+    # intersected on the GPU's float32 means/radii/depths): float32 as the
+    # kernels compute, held to the bound; float64 printed beside it
     isect_inputs = []
     for c in range(C):
         rec = _camera_lists(ts, c, stats.n_isects)[0]
         isect_inputs.append((rec[:, 0:2], rec[:, 7], rec[:, 3]))
-    o_touched, o_grads, o_losses, o_images, _ = SR.batch_grads(
-        params, vm, K, gt, W, H, filters=[torch.from_numpy(f) for f in g_filters],
-        isect_inputs=isect_inputs)
-    np.testing.assert_array_equal(to_np(touched), to_np(o_touched))
     imgs = to_np(ts.last["images"])
-    sign_flips = 0
+    g = to_np(grads)
+    # entries whose compositing decisions (alpha >= 1/255, the T stop) the two
+    # float32 projections put on opposite sides of a cut at some pixel: the
+    # oracle's decision walk over the GPU's intersection lists with the
+    # oracle's float32 splat values against the GPU's records
+    excluded = np.zeros(0, np.int64)
+    n_flip_pix = 0
     for c in range(C):
-        _image_close(imgs[c].reshape(-1, 3), o_images[c].reshape(-1, 3))
-        target = np.clip(to_np(gt[c]).transpose(1, 2, 0) / 255.0, 0, 1)
-        sign_flips += int((np.sign(imgs[c] - target) != np.sign(o_images[c] - target)).sum())
-    np.testing.assert_allclose(stats.losses(W, H), o_losses, rtol=1e-5)
-    g, og = to_np(grads), to_np(o_grads)
-    for name, sl in GROUPS.items():
-        err = rel_l2(g[:, sl], og[:, sl])
-        print(f"  row grad {name} (end to end): rel_l2={err:.2e}; L1 sign flips {sign_flips}")
-        assert err < end_to_end_bound, (name, err)
+        rec, toffs, flat = _camera_lists(ts, c, stats.n_isects)
+        f = SR._render_entries(params, torch.from_numpy(g_filters[c]), vm[c], K[c], W, H, 3,
+                               torch.float32)
+        flip, flag = R.decision_flips(
+            (f.m2d.numpy().reshape(-1, 2), f.conics[0].numpy(), f.opac.numpy().reshape(-1)),
+            (rec[:, 0:2], rec[:, 4:7], rec[:, 2]), W, H, 16, toffs, flat)
+        n_flip_pix += int(flip.sum())
+        excluded = np.union1d(excluded, g_filters[c][flag])
+    keep = ~np.isin(to_np(touched).astype(np.int64), excluded)
+    print(f"  {label}: {n_flip_pix} pixels with a compositing decision flipped by the "
+          f"projection's float32 rounding; {int((~keep).sum())} of {keep.size} rows composited "
+          "there set aside")
+    assert (~keep).mean() < 0.05
+    for proj_dtype in (torch.float32, torch.float64):
+        o_touched, o_grads, o_losses, o_images, _ = SR.batch_grads(
+            params, vm, K, gt, W, H, filters=[torch.from_numpy(f) for f in g_filters],
+            isect_inputs=isect_inputs, proj_dtype=proj_dtype)
+        np.testing.assert_array_equal(to_np(touched), to_np(o_touched))
+        sign_flips = 0
+        for c in range(C):
+            _image_close(imgs[c].reshape(-1, 3), o_images[c].reshape(-1, 3))
+            target = np.clip(to_np(gt[c]).transpose(1, 2, 0) / 255.0, 0, 1)
+            sign_flips += int((np.sign(imgs[c] - target) != np.sign(o_images[c] - target)).sum())
+        assert sign_flips == 0
+        np.testing.assert_allclose(stats.losses(W, H), o_losses, rtol=1e-5)
+        og = to_np(o_grads).astype(np.float64)
+        for name, sl in GROUPS.items():
+            err = rel_l2(g[:, sl], og[:, sl])
+            err_kept = rel_l2(g[keep, sl], og[keep, sl])
+            print(f"  row grad {name} (end to end, {proj_dtype}): rel_l2={err:.2e} over all "
+                  f"rows, {err_kept:.2e} over the rows with no flipped decision")
+            if proj_dtype == torch.float32:
+                assert err_kept < end_to_end_bound, (name, err_kept)
 
 
 def test_cfg3_subset_vs_oracle(gpu):
@@ -213,8 +273,7 @@ def test_cfg3_subset_vs_oracle(gpu):
     params = sc.params[rows].contiguous()
     cams = [0, 9]
     gt = torch.rand((2, 3, sc.height, sc.width), generator=g) * 255.0
-    _parity(gpu, params, sc.viewmats[cams], sc.Ks[cams], gt, sc.width, sc.height, "cfg3 subset",
-            end_to_end_bound=1e-2)
+    _parity(gpu, params, sc.viewmats[cams], sc.Ks[cams], gt, sc.width, sc.height, "cfg3 subset")
 
 
 def test_cfg3_dense_window_vs_oracle(gpu):
@@ -229,7 +288,7 @@ def test_cfg3_dense_window_vs_oracle(gpu):
     g = torch.Generator().manual_seed(8)
     gt = torch.rand((2, 3, H, W), generator=g) * 255.0
     _parity(gpu, sc.params, sc.viewmats[cams], K, gt, W, H, "cfg3 dense window",
-            end_to_end_bound=5e-2)
+            end_to_end_bound=2e-4)
 
 
 def test_cfg3_full_step(gpu):
@@ -262,6 +321,9 @@ def test_cfg3_full_step(gpu):
     T = touched.numel()
     print(f"  cfg3: {stats.entries} entries, {T} touched rows, {stats.n_isects} isects")
     assert stats.entries > 40_000_000 and stats.n_isects > 80_000_000 and T > 3_000_000
+    # every projected depth key lies inside the range the visibility pass gave
+    # the depth sort (no repair pass was needed)
+    assert split.depth_sort_repairs == 0
     check_isect_properties(split, C, split.tw, split.th)
     masks = L["masks"][:n].to(torch.int64) & 0xFFFFFFFF
     assert torch.equal(touched.long(), torch.nonzero(masks).flatten())
@@ -312,6 +374,7 @@ def test_cfg3_full_step(gpu):
     before = pf.clone()
     st = fused.step(vm, K, gt)
     torch.cuda.synchronize()
+    assert fused.depth_sort_repairs == 0
     assert st.touched_rows == T and st.optimizer["touched_rows"] == T
     assert all(np.isfinite(st.losses(W, H)))
     assert bool(torch.isfinite(fused.params).all())

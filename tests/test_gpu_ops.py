@@ -405,6 +405,55 @@ def test_rasterize_fwd_bwd(gpu, D, tile, bg, packed, absgrad):
         assert rel_l2(to_np(bgs.grad), ref_vbg) < 1e-5
 
 
+@pytest.mark.parametrize("D,tile", [(3, 16), (4, 8)])
+def test_rasterize_nonfinite_colour(gpu, D, tile):
+    """A Gaussian with an infinite colour channel reaches only the pixels it
+    composites, as in the reference (which adds c * alpha * T only there):
+    everywhere else the forward stays finite and equal to the oracle's, and
+    the backward's gradients are non-finite exactly where the oracle's are,
+    equal elsewhere.  (The walks multiply colours by zero for Gaussians that
+    fail the alpha test; a batch holding a non-finite colour takes the
+    select form instead.)"""
+    announce(f"raster non-finite colour D={D} tile={tile}")
+    C, W, H = 2, 200, 120
+    m2d, conics, colors, opacs, offs, flat = _raster_case(gpu, seed=91 + D, C=C, D=D, W=W, H=H,
+                                                          tile=tile)
+    # a visible Gaussian (projected conic) inside the frame that composites
+    # into a few pixels (the first such candidate, by the oracle's forward)
+    live = torch.nonzero((conics[..., 0] > 0) & (m2d[..., 0] > 20) & (m2d[..., 0] < W - 20) &
+                         (m2d[..., 1] > 20) & (m2d[..., 1] < H - 20)).tolist()
+    base = to_np(colors).copy()
+    for cam, gid in live[len(live) // 2:]:
+        colors_np = base.copy()
+        colors_np[cam, gid, 1] = np.inf
+        np_args = (to_np(m2d).reshape(-1, 2), to_np(conics).reshape(-1, 3),
+                   colors_np.reshape(-1, D), to_np(opacs).reshape(-1), W, H, tile, to_np(offs),
+                   to_np(flat))
+        ref_c, ref_a, ref_last = R.rasterize_fwd(*np_args)
+        fin = np.isfinite(ref_c)
+        if 0 < (~fin).sum() and fin.mean() > 0.99:
+            break
+    else:
+        pytest.fail("no Gaussian composites into a few pixels")
+    colors = torch.from_numpy(colors_np).to(gpu)
+    leaves = [t.clone().requires_grad_() for t in (m2d, conics, colors, opacs)]
+    rc, ra = ops.rasterize_to_pixels(*leaves, W, H, tile, offs, flat)
+    got = to_np(rc)
+    np.testing.assert_array_equal(np.isfinite(got), fin)
+    assert rel_l2(got[fin], ref_c[fin]) < 1e-5
+    assert rel_l2(to_np(ra)[..., 0], ref_a) < 1e-5
+    g = torch.Generator().manual_seed(D)
+    wc = torch.randn(rc.shape, generator=g)
+    (rc * wc.to(gpu)).sum().backward()
+    ref = R.rasterize_bwd(*np_args, ref_a, ref_last, to_np(wc))[:4]
+    widths = (2, 3, D, 1)
+    for leaf, r, w in zip(leaves, ref, widths):
+        v, r = to_np(leaf.grad).reshape(-1, w), np.asarray(r).reshape(-1, w)
+        f = np.isfinite(r)
+        np.testing.assert_array_equal(np.isfinite(v), f)
+        assert f.mean() > 0.99 and rel_l2(v[f], r[f]) < 1e-4
+
+
 def test_fused_ssim(gpu):
     announce("fused_ssim")
     g = torch.Generator().manual_seed(0)
@@ -489,18 +538,19 @@ def test_tide_loss_kernel(gpu, B, H, W):
 
 @pytest.mark.parametrize("form", [0, 1, 2, 3, 4, 5])
 def test_valu_probe_sums(gpu, form):
-    """tgs_valu_probe (the VALU-rate measurement kernel) computes what it
+    """tgs_valu_probe (bench.py's VALU-rate measurement kernel, in its own
+    library bench_valu_probe.so) computes what it
     claims, per thread 8 chains from a_k = tid + k (u_k = 7 tid + k), summed,
     against the same recurrences in float64 / integers: 0 a_k <- a_k z with
     z = x - (tid mod 64) 1e-9 in float32; 1 a_k <- a_k x; 2 u_k <- u_k + 3 tid
     + 1 (low 16 bits summed); 3 u_k <- u_k ^ bits(x); 4 a_k <- fma(a_k, z, y),
     y = (tid mod 64) 1e-9; 5 a_k <- 2^-a_k from a_k = k / 10."""
-    from tidegs_amd import _native as N
+    from bench import valu_probe
 
     blocks, iters, x = 3, 40, np.float32(0.999999)
     announce(f"valu probe form {form}: {blocks} blocks x {iters} rounds")
     out = torch.full((blocks * 256,), float("nan"), device=gpu)
-    N.call("tgs_valu_probe", N.ptr(out), blocks, iters, form, N.stream_handle(gpu))
+    valu_probe(out, blocks, iters, form, torch.cuda.current_stream(gpu).cuda_stream)
     torch.cuda.synchronize(gpu)
     tid = np.arange(256)
     lane = (tid % 64).astype(np.float32)

@@ -177,13 +177,11 @@ def test_emit_hist_then_hist0_sort(gpu, V, C, big):
            tile_bits, N.ptr(k), N.ptr(f), s)
     k_in, f_in = to_np(k).view(np.uint32), to_np(f)
     hs = (ctypes.c_uint32 * (C + 1))(*segs)
-    passes = (tile_bits + 7) // 8
-    mask0 = (1 << ((tile_bits + passes - 1) // passes)) - 1
     ws = torch.empty(lib.tgs_segmented_sort_workspace_size(n_isects, C), dtype=torch.uint8,
                      device=gpu)
     k2, f2 = torch.empty_like(k), torch.empty_like(f)
     N.call("tgs_tide_isect_emit_blocked_hist", V, N.ptr(cam_off), C, N.ptr(rects), N.ptr(base),
-           tw, tile_bits, N.ptr(k), N.ptr(f), hs, mask0, N.ptr(ws), ws.numel() // 4, s)
+           tw, tile_bits, N.ptr(k), N.ptr(f), hs, N.ptr(ws), ws.numel() // 4, s)
     np.testing.assert_array_equal(to_np(k).view(np.uint32), k_in)
     sel = ctypes.c_int(0)
     N.call("tgs_segmented_sort_pairs_u32_hist0", N.ptr(k), N.ptr(f), N.ptr(k2), N.ptr(f2),
@@ -216,6 +214,51 @@ def test_tide_step_isect_bit_exact(gpu):
     np.testing.assert_array_equal(to_np(ts.last["isect_ids"]), o_ids)
     np.testing.assert_array_equal(to_np(ts.last["flatten_ids"]), o_flat)
     np.testing.assert_array_equal(to_np(ts.last["offsets"]), R.isect_offset_encode(o_ids, C, tw, th))
+
+
+def test_depth_sort_repair_keeps_reference_order(gpu, monkeypatch):
+    """A depth-key range that misses projected keys (forced from the host: the
+    range helper returns a base above the smallest keys and too few bits for
+    the largest) makes the ranked depth sort tie those keys; the projection's
+    own range check then re-sorts on all 32 bits and the intersections are
+    still the reference's, bit for bit.  With the true range nothing is
+    repaired and every projected key lies inside it."""
+    announce("tide step depth sort repair")
+    from tidegs_amd import tide_step as TS
+    sc = _scene(seed=2)
+    C = sc.n_cams
+    tw, th = -(-sc.width // 16), -(-sc.height // 16)
+
+    def run(ts):
+        ts.forward_backward(sc.viewmats, sc.Ks, sc.gt)
+        sp = to_np(ts.last["splats"])
+        offs = to_np(ts.last["cam_offsets"])
+        cams = np.zeros(sp.shape[0], np.int64)
+        for c in range(C):
+            cams[offs[c]:offs[c + 1]] = c
+        _, o_ids, o_flat = R.isect_tiles(sp[:, 0:2], sp[:, 7].astype(np.int32), sp[:, 3], 16,
+                                         tw, th, camera_ids=cams)
+        np.testing.assert_array_equal(to_np(ts.last["isect_ids"]), o_ids)
+        np.testing.assert_array_equal(to_np(ts.last["flatten_ids"]), o_flat)
+        return sp
+
+    ts = TideStep(sc.params.to(gpu).contiguous(), sc.width, sc.height, batch_size=C,
+                  keep_isect_ids=True)
+    sp = run(ts)
+    assert ts.depth_sort_repairs == 0
+    keys = sp[:, 3].view(np.uint32)[sp[:, 7] > 0].astype(np.int64)
+    true_range = TS.depth_key_range(int(keys.min()), int(keys.max()))
+    base, bits = true_range
+    assert keys.min() >= base and keys.max() - base < (1 << bits) - 1
+
+    def narrow(lo, hi):
+        return lo + (hi - lo) // 4, max(1, ((hi - lo) // 4).bit_length())
+
+    monkeypatch.setattr(TS, "depth_key_range", narrow)
+    ts2 = TideStep(sc.params.to(gpu).contiguous(), sc.width, sc.height, batch_size=C,
+                   keep_isect_ids=True)
+    run(ts2)
+    assert ts2.depth_sort_repairs == 1
 
 
 @pytest.mark.parametrize("pitch", [59, 64])

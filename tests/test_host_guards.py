@@ -66,3 +66,40 @@ def test_depth_key_range():
     assert depth_key_range(5, 5)[1] == ((5 + DEPTH_KEY_SLACK) - 0 + 1).bit_length()
     base, bits = depth_key_range(0x7F000000, 0x7F7FFFFF)
     assert bits <= 32 and 0x7F7FFFFF + DEPTH_KEY_SLACK - base < (1 << bits) - 1
+
+
+def test_depth_range_holds():
+    """The projection's own depth-key range against the ranked sort's
+    [key_base, key_base + 2^bits - 1): keys at the base and just under the cap
+    hold; one key below the base or at the cap (where it would tie with the
+    culled sentinel) does not; slots with nothing written ({~0, 0}) are
+    ignored."""
+    from tidegs_amd.tide_step import RANGE_SLOTS, depth_range_holds
+    empty = [0xFFFFFFFF, 0] * RANGE_SLOTS
+    base, bits = 1000, 10
+    cap = (1 << bits) - 1
+
+    def slots(lo, hi):
+        s = list(empty)
+        s[6], s[7] = lo, hi
+        s[40], s[41] = (lo + hi) // 2, (lo + hi) // 2
+        return s
+
+    assert depth_range_holds(empty, base, bits)
+    assert depth_range_holds(slots(base, base + cap - 1), base, bits)
+    assert not depth_range_holds(slots(base - 1, base + 5), base, bits)
+    assert not depth_range_holds(slots(base, base + cap), base, bits)
+    assert depth_range_holds(slots(0, 0xFFFFFFFE), 0, 32)
+
+
+def test_hist0_sort_refuses_offset_first_pass():
+    """tgs_segmented_sort_pairs_u32_hist0 trusts a first-pass histogram counted
+    from bit 0, so it refuses any other begin_bit before launching anything."""
+    import ctypes
+    from tidegs_amd import _native as N
+    lib = N.load()
+    sel = ctypes.c_int(0)
+    segs = (ctypes.c_uint32 * 2)(0, 16)
+    rc = lib.tgs_segmented_sort_pairs_u32_hist0(None, None, None, None, 16, 1, segs, 1, 13,
+                                                None, 0, ctypes.byref(sel), None)
+    assert rc != 0 and "bit 0" in N.last_error()

@@ -219,3 +219,74 @@ def test_raster_backward_matches_finite_differences():
             fd[idx] = (lp - lm) / (2 * h)
         err = np.linalg.norm(fd - grad) / max(np.linalg.norm(fd), 1e-30)
         assert err < 1e-5, (name, err)
+
+
+def _one_tile(means2d, conics, opac):
+    """One 16x16 tile holding every Gaussian, front to back in input order."""
+    n = len(opac)
+    return (np.asarray(means2d, np.float64), np.asarray(conics, np.float64),
+            np.asarray(opac, np.float64), np.zeros((1, 1, 1), np.int32),
+            np.arange(n, dtype=np.int32))
+
+
+def test_decision_flips_identical_sets():
+    """The same parameters on both sides flip nothing and flag nothing."""
+    m, q, o, offs, flat = _one_tile([[5.3, 7.1], [9.0, 4.2], [8.0, 8.0]],
+                                    [[0.5, 0.1, 0.7], [0.2, 0.0, 0.3], [1.0, 0.0, 1.0]],
+                                    [0.6, 0.9, 0.4])
+    flip, flag = R.decision_flips((m, q, o), (m, q, o), 16, 16, 16, offs, flat)
+    assert not flip.any() and not flag.any()
+    # a marked pixel flags the Gaussians composited there: at pixel (7, 7)
+    # (centre (7.5, 7.5)) alpha = 0.6 exp(-1.354), 0.9 exp(-1.858) and
+    # 0.4 exp(-0.25), all above 1/255
+    mark = np.zeros((1, 16, 16), bool)
+    mark[0, 7, 7] = True
+    flip, flag = R.decision_flips((m, q, o), (m, q, o), 16, 16, 16, offs, flat,
+                                  dtype=np.float64, mark=mark)
+    assert not flip.any()
+    np.testing.assert_array_equal(flag, [True, True, True])
+
+
+def test_decision_flips_alpha_ring():
+    """An isotropic Gaussian (conic (1, 0, 1)) at a pixel centre passes the
+    alpha test where o exp(-r^2 / 2) >= 1/255, i.e. r^2 <= 2 ln(255 o): raising
+    its opacity from o_a to o_b adds exactly the pixels with r^2 in
+    (2 ln(255 o_a), 2 ln(255 o_b)] (values chosen away from pixel distances),
+    and flags that Gaussian only; a second Gaussian far from the ring is not
+    flagged."""
+    c = (7.3, 8.6)
+    o_a, o_b = 0.04, 0.3
+    m = [list(c), [1.5, 1.5]]
+    q = [[1.0, 0.0, 1.0], [4.0, 0.0, 4.0]]
+    _, _, _, offs, flat = _one_tile(m, q, [o_a, 0.9])
+    flip, flag = R.decision_flips((m, q, [o_a, 0.9]), (m, q, [o_b, 0.9]), 16, 16, 16,
+                                  offs, flat, dtype=np.float64)
+    j, i = np.meshgrid(np.arange(16) + 0.5, np.arange(16) + 0.5)
+    r2 = (j - c[0]) ** 2 + (i - c[1]) ** 2
+    lo, hi = 2 * np.log(255 * o_a), 2 * np.log(255 * o_b)
+    assert np.abs(r2 - lo).min() > 1e-3 and np.abs(r2 - hi).min() > 1e-3
+    want = (r2 > lo) & (r2 <= hi)
+    assert want.sum() > 10
+    np.testing.assert_array_equal(flip[0], want)
+    np.testing.assert_array_equal(flag, [True, False])
+
+
+def test_decision_flips_transmittance_stop():
+    """Five Gaussians centred on pixel (8, 8) (alpha = opacity there): with
+    opacities 0.95 the transmittance after three is 1.25e-4 and the fourth
+    stops the pixel (6.25e-6 <= 1e-4), so three composite; with the third at
+    0.5 and the fourth at 0.9 it is 1.25e-3 after three and 1.25e-4 after
+    four, so the fifth stops it and four composite.  The centre pixel's decisions differ, and all
+    four Gaussians composited under the second set are flagged; a pixel far
+    from the stack (where no Gaussian passes the alpha test) is not flipped."""
+    c = [8.5, 8.5]
+    m = [c] * 5
+    q = [[8.0, 0.0, 8.0]] * 5
+    a = [0.95] * 5
+    b = [0.95, 0.95, 0.5, 0.9, 0.95]
+    _, _, _, offs, flat = _one_tile(m, q, a)
+    flip, flag = R.decision_flips((m, q, a), (m, q, b), 16, 16, 16, offs, flat,
+                                  dtype=np.float64)
+    assert flip[0, 8, 8]
+    assert not flip[0, 0, 0] and not flip[0, 15, 15]
+    np.testing.assert_array_equal(flag, [True, True, True, True, False])

@@ -30,7 +30,6 @@ SIGNATURES = {
     "tgs_abi_version": (ctypes.c_int, []),
     "tgs_last_error": (ctypes.c_char_p, []),
     "tgs_fill_u32": (ctypes.c_int, [P, U64, U32, P]),
-    "tgs_valu_probe": (ctypes.c_int, [P, U32, U32, ctypes.c_int32, P]),
     "tgs_fully_fused_projection_fwd": (
         ctypes.c_int,
         [U32, U32, P, P, P, P, P, P, I32, I32, F32, F32, F32, F32, P, P, P, P, P, P],
@@ -104,7 +103,7 @@ SIGNATURES = {
     "tgs_tide_project_fwd": (
         ctypes.c_int,
         [U32, P, P, P, P, P, U32, P, U32, P, P, P, I32, I32, F32, F32, F32, F32, I32, U32, U32,
-         U32, P, P, P, P, P]),
+         U32, P, P, P, P, P, P]),
     "tgs_tide_isect_totals": (ctypes.c_int, [U32, P, P, P, U32, P, P]),
     "tgs_tide_isect_count": (ctypes.c_int, [U32, P, P, P]),
     "tgs_tide_isect_segments": (ctypes.c_int, [U32, P, P, P, P]),
@@ -113,7 +112,7 @@ SIGNATURES = {
     "tgs_tide_isect_block_sums": (ctypes.c_int, [U32, P, P, P]),
     "tgs_tide_isect_emit_blocked": (ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P]),
     "tgs_tide_isect_emit_blocked_hist": (
-        ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P, U32, P, U64, P]),
+        ctypes.c_int, [U32, P, U32, P, P, U32, U32, P, P, P, P, U64, P]),
     "tgs_segmented_sort_pairs_u32_hist0": (
         ctypes.c_int,
         [P, P, P, P, U64, U32, P, ctypes.c_int, ctypes.c_int, P, SZ, ctypes.POINTER(ctypes.c_int),

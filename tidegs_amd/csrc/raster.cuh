@@ -458,6 +458,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     const bool have = (int)tr < BATCH && idx < range_end;
     SplatData<CDIM> s;
     if (have) src.load(flatten_ids[idx], s);
+    bool odd_colour = false;
     if (have) {
       const StagedGeo sg = stage_geo<CDIM>(s);
       s_rec[tr].g0 = sg.g0;
@@ -465,9 +466,15 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
       s_box[tr] = sg.box;
       s_cov[tr] = sg.cov;
 #pragma unroll
-      for (int k = 0; k < CDIM; ++k) s_rec[tr].col[k] = s.col[k];
+      for (int k = 0; k < CDIM; ++k) {
+        s_rec[tr].col[k] = s.col[k];
+        odd_colour |= !__builtin_isfinite(s.col[k]);
+      }
     }
-    __syncthreads();
+    // a batch with a non-finite colour walks with selects instead of
+    // multiplying colours by zero (inf * 0 would reach pixels the Gaussian
+    // does not composite)
+    const bool safe_walk = __syncthreads_or(odd_colour) != 0;
     const int32_t batch_size = min(BATCH, range_end - batch_start);
     const uint64_t alive = tgs_ballot(T > 0.f);
     if (!alive) continue;
@@ -484,38 +491,45 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     // the batch start as a VGPR operand too (the contributor index add pairs)
     int32_t bs_v;
     asm volatile("v_mov_b32 %0, %1" : "=v"(bs_v) : "s"(batch_start));
+    auto walk = [&](auto safe_tag) {
+      constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
-    for (int W = 0; W < WORDS; ++W) {
-      if (W * 32 >= n_list) break;
-      uint32_t m = T < 0.f ? 0u : mw[W];
-      // every lane runs the body (no exec-mask branches): a lane with no
-      // entry left reads staged record 0 and changes nothing; a Gaussian
-      // failing the alpha test, or the one that would take T to the
-      // threshold, adds exactly zero; a lane reaching the threshold clears m
-      if (tgs_ballot(m != 0u)) do {
-        const bool act = m != 0u;
-        const int bit = __builtin_ctz(m | 0x80000000u);  // 31 where m is empty
-        m &= m - 1u;
-        const int te = my_list[W * 32 + bit];
-        const int t = act ? te : 0;
-        const StagedRec<CDIM>& rec = s_rec[t];
-        const float4 g0 = rec.g0;
-        const float4 g1 = rec.g1;
-        const float power = raster_power(g0, make_float2(g1.x, g1.y), g0.x - px, g0.y - py);
-        const bool pass = act && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
-        const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
-        const float next_T = T * (1.f - alpha);
-        const bool stop = pass && next_T <= 1e-4f;
-        const bool comp = pass && !stop;
-        m = stop ? 0u : m;
-        const float vis = comp ? alpha * T : 0.f;
+      for (int W = 0; W < WORDS; ++W) {
+        if (W * 32 >= n_list) break;
+        uint32_t m = T < 0.f ? 0u : mw[W];
+        // every lane runs the body (no exec-mask branches): a lane with no
+        // entry left reads staged record 0 and changes nothing; a Gaussian
+        // failing the alpha test, or the one that would take T to the
+        // threshold, adds exactly zero; a lane reaching the threshold clears m
+        if (tgs_ballot(m != 0u)) do {
+          const bool act = m != 0u;
+          const int bit = __builtin_ctz(m | 0x80000000u);  // 31 where m is empty
+          m &= m - 1u;
+          const int te = my_list[W * 32 + bit];
+          const int t = act ? te : 0;
+          const StagedRec<CDIM>& rec = s_rec[t];
+          const float4 g0 = rec.g0;
+          const float4 g1 = rec.g1;
+          const float power = raster_power(g0, make_float2(g1.x, g1.y), g0.x - px, g0.y - py);
+          const bool pass = act && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
+          const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
+          const float next_T = T * (1.f - alpha);
+          const bool stop = pass && next_T <= 1e-4f;
+          const bool comp = pass && !stop;
+          m = stop ? 0u : m;
+          const float vis = comp ? alpha * T : 0.f;
 #pragma unroll
-        for (int k = 0; k < CDIM; ++k) pix[k] = fmaf(rec.col[k], vis, pix[k]);
-        cur_idx = comp ? (uint32_t)(bs_v + t) : cur_idx;
-        if (COUNT) n_comp += comp ? 1 : 0;
-        T = comp ? next_T : (stop ? -T : T);
-      } while (tgs_ballot(m != 0u));
-    }
+          for (int k = 0; k < CDIM; ++k)
+            pix[k] = SAFE ? (comp ? fmaf(rec.col[k], vis, pix[k]) : pix[k])
+                          : fmaf(rec.col[k], vis, pix[k]);
+          cur_idx = comp ? (uint32_t)(bs_v + t) : cur_idx;
+          if (COUNT) n_comp += comp ? 1 : 0;
+          T = comp ? next_T : (stop ? -T : T);
+        } while (tgs_ballot(m != 0u));
+      }
+    };
+    if (safe_walk) walk(std::true_type{});
+    else walk(std::false_type{});
   }
   T = fabsf(T);
   if (inside) {
@@ -674,6 +688,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
     const int32_t g = have ? flatten_ids[idx] : 0;
     SplatData<CDIM> s;
     if (have) src.load(g, s);
+    bool odd_colour = false;
     if (have) {
       const StagedGeo sg = stage_geo<CDIM>(s);
       s_g0[tr] = sg.g0;
@@ -682,9 +697,14 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
       s_cov[tr] = sg.cov;
       s_id[tr] = g;
 #pragma unroll
-      for (int k = 0; k < CDIM; ++k) s_col[tr][k] = s.col[k];
+      for (int k = 0; k < CDIM; ++k) {
+        s_col[tr][k] = s.col[k];
+        odd_colour |= !__builtin_isfinite(s.col[k]);
+      }
     }
-    __syncthreads();
+    // a batch with a non-finite colour keeps the colour sum behind a pixel
+    // with a select (a Gaussian failing the exact test must not add 0 * inf)
+    const bool safe_walk = __syncthreads_or(odd_colour) != 0;
     // batch entry t is global index batch_end - t; a pixel composites the
     // entries at or before its last contributor: t >= t_min
     const int t_min = batch_end - bin_final;
@@ -750,45 +770,51 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       // 2. per-pixel walk over entries [a, e_end), back to front
+      auto walk = [&](auto safe_tag) {
+        constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
-      for (int W = 0; W < WORDS; ++W) {
-        if (W * 32 >= e_end || W * 32 + 32 <= a) continue;
-        const int lo_b = max(a - W * 32, 0), hi_b = min(e_end - W * 32, 32);
-        const uint32_t range = (hi_b >= 32 ? 0xffffffffu : ((1u << hi_b) - 1u)) &
-                               ~((1u << lo_b) - 1u);
-        uint32_t mw = m[W] & range;
-        while (tgs_ballot(mw != 0u)) {
-          if (mw != 0u) {
-            const int li = W * 32 + __builtin_ctz(mw);
-            mw &= mw - 1u;
-            const int t = s_list[wave][li];
-            const float4 g0 = s_g0[t];
-            const float2 g1 = s_g1[t];
-            const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
-            // predicated rather than branched: a pixel failing the exact
-            // test keeps T and the colour buffer and writes (0, 0), the value
-            // its zeroed slot already holds
-            const bool pass = !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
-            const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
-            const float alpha = fminf(0.999f, raw);
-            const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
-            const float Tn = T * ra;
-            T = pass ? Tn : T;
-            // v_alpha = sum_k (c_k T - buffer_k ra) v_rc_k + ra tf_term
-            float cv = 0.f;
+        for (int W = 0; W < WORDS; ++W) {
+          if (W * 32 >= e_end || W * 32 + 32 <= a) continue;
+          const int lo_b = max(a - W * 32, 0), hi_b = min(e_end - W * 32, 32);
+          const uint32_t range = (hi_b >= 32 ? 0xffffffffu : ((1u << hi_b) - 1u)) &
+                                 ~((1u << lo_b) - 1u);
+          uint32_t mw = m[W] & range;
+          while (tgs_ballot(mw != 0u)) {
+            if (mw != 0u) {
+              const int li = W * 32 + __builtin_ctz(mw);
+              mw &= mw - 1u;
+              const int t = s_list[wave][li];
+              const float4 g0 = s_g0[t];
+              const float2 g1 = s_g1[t];
+              const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
+              // predicated rather than branched: a pixel failing the exact
+              // test keeps T and the colour buffer and writes (0, 0), the
+              // value its zeroed slot already holds
+              const bool pass = !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
+              const float raw = __builtin_amdgcn_exp2f(power);  // opacity * exp(-sigma)
+              const float alpha = fminf(0.999f, raw);
+              const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
+              const float Tn = T * ra;
+              T = pass ? Tn : T;
+              // v_alpha = sum_k (c_k T - buffer_k ra) v_rc_k + ra tf_term
+              float cv = 0.f;
 #pragma unroll
-            for (int k = 0; k < CDIM; ++k) cv = fmaf(s_col[t][k], v_rc[k], cv);
-            const float v_alpha = fmaf(Tn, cv, ra * (tf_term - buffer_dot));
-            const float fac = pass ? alpha * Tn : 0.f;
-            buffer_dot = fmaf(fac, cv, buffer_dot);
-            // reference: the sigma terms only where alpha was not clamped
-            const float v_sigma = pass && raw <= 0.999f ? -raw * v_alpha : 0.f;
-            const uint32_t slot = (uint32_t)s_poh[wave][half][li] - base +
-                                  (uint32_t)__popc(s_emh[wave][half][li] & lt_half);
-            s_pair[wave][slot] = make_float2(fac, v_sigma);
+              for (int k = 0; k < CDIM; ++k) cv = fmaf(s_col[t][k], v_rc[k], cv);
+              const float v_alpha = fmaf(Tn, cv, ra * (tf_term - buffer_dot));
+              const float fac = pass ? alpha * Tn : 0.f;
+              buffer_dot = SAFE ? (pass ? fmaf(fac, cv, buffer_dot) : buffer_dot)
+                                : fmaf(fac, cv, buffer_dot);
+              // reference: the sigma terms only where alpha was not clamped
+              const float v_sigma = pass && raw <= 0.999f ? -raw * v_alpha : 0.f;
+              const uint32_t slot = (uint32_t)s_poh[wave][half][li] - base +
+                                    (uint32_t)__popc(s_emh[wave][half][li] & lt_half);
+              s_pair[wave][slot] = make_float2(fac, v_sigma);
+            }
           }
         }
-      }
+      };
+      if (safe_walk) walk(std::true_type{});
+      else walk(std::false_type{});
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

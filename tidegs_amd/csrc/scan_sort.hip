@@ -603,6 +603,7 @@ extern "C" int tgs_segmented_sort_pairs_u32_hist0(uint32_t* keys, uint32_t* vals
                                                   int end_bit, void* workspace,
                                                   size_t workspace_bytes, int* selector,
                                                   hipStream_t stream) {
+  TGS_CHECK_ARG(begin_bit == 0, "segmented_sort_hist0: the precounted first pass starts at bit 0");
   return segmented_sort_u32(keys, vals, keys_alt, vals_alt, 4, n, n_segments, seg_offsets, 0u,
                             0xffffffffu, begin_bit, end_bit, workspace, workspace_bytes, selector,
                             stream, true);

@@ -339,7 +339,7 @@ __device__ __forceinline__ uint32_t project_entry(
     const float* campos, int W, int H, float eps2d, float near_plane, float far_plane,
     float radius_clip, int sh_degree, uint32_t tile_size, uint32_t tw, uint32_t th, uint32_t e,
     float4* __restrict__ splats, uint32_t* __restrict__ depth_keys,
-    uint64_t* __restrict__ entry_rects) {
+    uint64_t* __restrict__ entry_rects, uint32_t& key) {
   const ProjResult r =
       project_forward(p, Sigma, cam, W, H, eps2d, near_plane, far_plane, radius_clip);
   float4* out = splats + (uint64_t)e * 3;
@@ -347,6 +347,7 @@ __device__ __forceinline__ uint32_t project_entry(
     out[0] = make_float4(0.f, 0.f, 0.f, 0.f);
     out[1] = make_float4(0.f, 0.f, 0.f, 0.f);
     out[2] = make_float4(0.f, 0.f, 0.f, 0.f);
+    key = 0xffffffffu;
     depth_keys[e] = 0xffffffffu;
     entry_rects[e] = (uint64_t)e;  // empty rectangle
     return 0u;
@@ -372,7 +373,8 @@ __device__ __forceinline__ uint32_t project_entry(
   const uint32_t x0 = clampu(floorf(txx - trd), tw), x1 = clampu(ceilf(txx + trd), tw);
   const uint32_t y0 = clampu(floorf(tyy - trd), th), y1 = clampu(ceilf(tyy + trd), th);
   // depth > near_plane > 0, so the float bits order like the depths
-  depth_keys[e] = __float_as_uint(r.depth);
+  key = __float_as_uint(r.depth);
+  depth_keys[e] = key;
   entry_rects[e] = ((uint64_t)pack_rect(x0, x1, y0, y1) << 32) | e;
   return (x1 - x0) * (y1 - y0);  // x1 >= x0 and y1 >= y0 (clamped floor / ceil)
 }
@@ -382,7 +384,11 @@ __device__ __forceinline__ uint32_t project_entry(
 // set bits of its visibility mask); SH coefficients stay in registers.  With
 // isect_totals (zeroed by the launch) the per-camera intersection counts are
 // summed too: a wave sum per camera step, LDS counters per workgroup, one
-// 64-bit atomic per camera and workgroup.
+// 64-bit atomic per camera and workgroup.  With depth_range (TIDE_RANGE_SLOTS
+// {min, max} pairs, initialised by the launch) the smallest and largest depth
+// key written (culled entries' sentinels excluded) are folded in as the
+// visibility pass does, so the host can check that the depth sort's key
+// range, taken from the visibility pass, holds every key.
 __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
     uint32_t n_touched, const uint32_t* __restrict__ n_touched_dev,
     const int32_t* __restrict__ touched,
@@ -392,11 +398,13 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
     float radius_clip, int sh_degree, uint32_t tile_size, uint32_t tw, uint32_t th,
     float4* __restrict__ splats,
     uint32_t* __restrict__ depth_keys, uint64_t* __restrict__ entry_rects,
-    int64_t* __restrict__ isect_totals) {
+    int64_t* __restrict__ isect_totals, uint32_t* __restrict__ depth_range) {
   __shared__ CamLDS s_cam;
   __shared__ uint32_t s_area[TIDE_MAX_CAMS];
+  __shared__ uint32_t s_rng[2];
   load_cams_lds(tc, s_cam);
   if (threadIdx.x < TIDE_MAX_CAMS) s_area[threadIdx.x] = 0u;
+  if (threadIdx.x < 2) s_rng[threadIdx.x] = threadIdx.x == 0 ? 0xffffffffu : 0u;
   __syncthreads();
   const uint32_t limit = n_touched_dev ? min(*n_touched_dev, n_touched) : n_touched;
   if (blockIdx.x * blockDim.x >= limit) return;  // the whole workgroup
@@ -418,24 +426,44 @@ __global__ void __launch_bounds__(256) tide_project_fwd_kernel(
   // LDS broadcast, and the lanes seeing camera c write consecutive entries of
   // its list (coalesced records)
   int j = 0;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
   for (uint32_t c = 0; c < tc.C; ++c) {
     uint32_t area = 0u;
     if ((mask >> c) & 1u) {
       const uint32_t e = (uint32_t)vis[j++];
+      uint32_t key;
       area = project_entry(p, Sigma, opac, sh, s_cam.cam[c], s_cam.campos[c], W, H, eps2d,
                            near_plane, far_plane, radius_clip, sh_degree, tile_size, tw, th, e,
-                           splats, depth_keys, entry_rects);
+                           splats, depth_keys, entry_rects, key);
+      if (key != 0xffffffffu) {
+        kmin = min(kmin, key);
+        kmax = max(kmax, key);
+      }
     }
     if (isect_totals) {
       const uint32_t wsum = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan(area), 63);
       if ((threadIdx.x & 63u) == 0u && wsum) atomicAdd(&s_area[c], wsum);
     }
   }
-  if (isect_totals) {
-    __syncthreads();
-    if (threadIdx.x < tc.C && s_area[threadIdx.x])
-      atomicAdd((unsigned long long*)&isect_totals[threadIdx.x],
-                (unsigned long long)s_area[threadIdx.x]);
+  if (depth_range) {  // wave min / max, then one LDS update per wavefront
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, off, 64));
+      kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, off, 64));
+    }
+    if ((threadIdx.x & 63) == 0 && kmax >= kmin) {
+      atomicMin(&s_rng[0], kmin);
+      atomicMax(&s_rng[1], kmax);
+    }
+  }
+  if (isect_totals || depth_range) __syncthreads();
+  if (isect_totals && threadIdx.x < tc.C && s_area[threadIdx.x])
+    atomicAdd((unsigned long long*)&isect_totals[threadIdx.x],
+              (unsigned long long)s_area[threadIdx.x]);
+  if (depth_range && threadIdx.x == 0 && s_rng[1] >= s_rng[0]) {
+    uint32_t* slot = depth_range + 2 * (blockIdx.x % TIDE_RANGE_SLOTS);
+    atomicMin(&slot[0], s_rng[0]);
+    atomicMax(&slot[1], s_rng[1]);
   }
 }
 
@@ -1187,11 +1215,15 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touche
                                     int32_t sh_degree, uint32_t tile_size, uint32_t tile_width,
                                     uint32_t tile_height,
                                     float* splats, uint32_t* depth_keys, uint64_t* entry_rects,
-                                    int64_t* isect_totals, hipStream_t stream) {
+                                    int64_t* isect_totals, uint32_t* depth_range,
+                                    hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;
   if (isect_totals)
     hipLaunchKernelGGL(tide_zero_i64_kernel, dim3(1), dim3(64), 0, stream, isect_totals, C);
+  if (depth_range)
+    hipLaunchKernelGGL(tide_range_init_kernel, dim3(1), dim3(2 * TIDE_RANGE_SLOTS), 0, stream,
+                       depth_range);
   if (n_touched == 0) TGS_RETURN_LAUNCH("tgs_tide_project_fwd");
   TGS_CHECK_ARG(touched && visit_base && visits && masks && params && viewmats && Ks && campos &&
                     splats && depth_keys && entry_rects,
@@ -1208,7 +1240,8 @@ extern "C" int tgs_tide_project_fwd(uint32_t n_touched, const uint32_t* n_touche
                      params, row_stride,
                      W, H,
                      eps2d, near_plane, far_plane, radius_clip, sh_degree, tile_size, tile_width,
-                     tile_height, (float4*)splats, depth_keys, entry_rects, isect_totals);
+                     tile_height, (float4*)splats, depth_keys, entry_rects, isect_totals,
+                     depth_range);
   TGS_RETURN_LAUNCH("tgs_tide_project_fwd");
 }
 
@@ -1298,18 +1331,22 @@ extern "C" int tgs_tide_isect_emit_blocked(uint32_t n_entries, const int32_t* ca
 extern "C" int tgs_tide_isect_emit_blocked_hist(
     uint32_t n_entries, const int32_t* cam_offsets, uint32_t C, const uint64_t* entry_rects,
     const uint32_t* block_base, uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
-    int32_t* flatten_ids, const uint32_t* isect_cam_offsets, uint32_t digit_mask,
-    uint32_t* hist, uint64_t hist_words, hipStream_t stream) {
+    int32_t* flatten_ids, const uint32_t* isect_cam_offsets, uint32_t* hist,
+    uint64_t hist_words, hipStream_t stream) {
   int rc = check_cams(C);
   if (rc) return rc;
   TGS_CHECK_ARG(cam_offsets && entry_rects && block_base && keys && flatten_ids &&
                     isect_cam_offsets && hist,
                 "tide_isect_emit_blocked_hist: null");
-  TGS_CHECK_ARG(tile_n_bits <= 16, "tide_isect_emit_blocked_hist: tile_n_bits must be <= 16");
-  TGS_CHECK_ARG(digit_mask <= 255u, "tide_isect_emit_blocked_hist: digit_mask must be < 256");
+  TGS_CHECK_ARG(tile_n_bits >= 1 && tile_n_bits <= 16,
+                "tide_isect_emit_blocked_hist: tile_n_bits must be in [1, 16]");
   EmitHist eh{};
   eh.hist = hist;
-  eh.mask = digit_mask;
+  // the sort's first pass over bits [0, tile_n_bits): ceil(bits / 8) passes
+  // of ceil(bits / passes) bits (the split tgs_segmented_sort_pairs_u32_hist0
+  // makes)
+  const uint32_t passes = (tile_n_bits + 7) / 8;
+  eh.mask = (1u << ((tile_n_bits + passes - 1) / passes)) - 1u;
   uint32_t tiles = 0;
   for (uint32_t c = 0; c <= C; ++c) {
     TGS_CHECK_ARG(c == 0 || isect_cam_offsets[c] >= isect_cam_offsets[c - 1],

@@ -29,6 +29,7 @@ place of the second moment (Liu et al. 2023; no TideGS counterpart).
 """
 from __future__ import annotations
 
+import copy
 import ctypes
 from typing import Any, Callable, Dict, Optional, Sequence, Tuple
 
@@ -498,6 +499,35 @@ class GPUResidentAdam:
                 self.STATE_PITCH, self._fused_lrs, mode, beta1, beta2, eps,
                 float(self.batch_size), rho, update_h, N.ptr(self._error_flag))
         return args, stats
+
+    # ---- snapshot / restore ----------------------------------------------------
+    def snapshot(self) -> Dict[str, Any]:
+        """A copy of the whole optimizer state (moment tables on the device,
+        slot bookkeeping, bias terms and counters on the host), for
+        :meth:`restore`.  The resident set must not change in between."""
+        torch.cuda.current_stream(self.device).synchronize()
+        return {"exp_avg": None if self._exp_avg is None else self._exp_avg.clone(),
+                "exp_avg_sq": None if self._exp_avg_sq is None else self._exp_avg_sq.clone(),
+                "bias_host": self._bias_host.copy(), "slots": copy.deepcopy(self.slots),
+                "counters": dict(self._counters), "epoch": self._epoch}
+
+    def restore(self, snap: Dict[str, Any]) -> None:
+        """Put back a :meth:`snapshot` in place (device copies queued on the
+        current stream; the tables keep their addresses)."""
+        if snap["epoch"] != self._epoch or snap["slots"].capacity != self.slots.capacity:
+            raise RuntimeError("[GPUResidentAdam] restore: the resident set changed since the "
+                               "snapshot")
+        for table, saved in ((self._exp_avg, snap["exp_avg"]),
+                             (self._exp_avg_sq, snap["exp_avg_sq"])):
+            if saved is not None:
+                table.copy_(saved)
+        for _, event in self._staging:  # no queued upload may still read the host table
+            if event is not None:
+                event.synchronize()
+        self._bias_host[...] = snap["bias_host"]
+        self._bias_terms.copy_(torch.from_numpy(self._bias_host))
+        self.slots = copy.deepcopy(snap["slots"])
+        self._counters = dict(snap["counters"])
 
     # ---- stats ----------------------------------------------------------------
     def get_stats(self) -> Dict[str, Any]:

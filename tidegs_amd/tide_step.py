@@ -138,6 +138,18 @@ def depth_key_range(lo: int, hi: int) -> tuple:
     return base, min((top - base + 1).bit_length(), 32)
 
 
+def depth_range_holds(slots, key_base: int, key_bits: int) -> bool:
+    """True when every depth key the projection wrote (the min / max over its
+    {min, max} slot pairs, sentinels excluded) ranks below the ranked sort's
+    cap: key_base <= key < key_base + 2^key_bits - 1."""
+    slots = [v & 0xFFFFFFFF for v in slots]
+    lo, hi = min(slots[0::2]), max(slots[1::2])
+    if hi < lo:  # no key written
+        return True
+    cap = (1 << key_bits) - 1
+    return key_base <= lo and hi - key_base < cap
+
+
 def _segments(offsets) -> "ctypes.Array":
     """Host uint32 array of segment offsets for tgs_segmented_sort_pairs_u32."""
     return (ctypes.c_uint32 * len(offsets))(*[int(o) for o in offsets])
@@ -207,6 +219,10 @@ class TideStep:
         self.stage_ms: Dict[str, float] = {}
         self.last_visible_entries = 0
         self.last_live_pairs = 0  # composited (Gaussian, pixel) pairs of the last counting step
+        self.last_depth_key_bits = 32  # key bits of the last step's depth sort
+        # steps whose projected depth keys fell outside the visibility pass's
+        # range, so that the depth sort was redone on all 32 bits
+        self.depth_sort_repairs = 0
 
     # ---- stage timing (HIP events on the launch stream) ----------------------
     def _begin(self, name: str):
@@ -279,7 +295,9 @@ class TideStep:
         viewmats = viewmats.to(self.device, torch.float32).contiguous()
         Ks = Ks.to(self.device, torch.float32).contiguous()
         campos = self._buf("campos", 3 * C, torch.float32).view(C, 3)
+        self._begin("camera_centers")
         N.call("tgs_tide_camera_centers", C, N.ptr(viewmats), N.ptr(campos), s)
+        self._end()
         gt = gt.to(self.device, torch.float32).contiguous()
         lib = N.load()
 
@@ -325,15 +343,20 @@ class TideStep:
         # the projection also sums the per-camera intersection counts (the
         # rectangles' areas); they go to the host while the depth sort runs
         isect_tot = self._buf("isect_totals", C, torch.int64)
+        # and the range of the depth keys it writes, to check the depth sort's
+        # range (taken from the visibility pass) against
+        proj_range = self._buf("proj_range", 2 * RANGE_SLOTS, torch.int32)
         self._begin("project_fwd")
         N.call("tgs_tide_project_fwd", n, N.ptr(totals) + 4 * C, N.ptr(touched),
                N.ptr(visit_base), N.ptr(visits), N.ptr(masks), C, N.ptr(P), self.row_stride,
                N.ptr(viewmats), N.ptr(Ks), N.ptr(campos), W, H, self.eps2d, self.near, self.far,
                0.0, self.sh_degree, self.TILE, tw, th, N.ptr(splats), N.ptr(dkeys), N.ptr(rects),
-               N.ptr(isect_tot), s)
+               N.ptr(isect_tot), N.ptr(proj_range), s)
         self._end()
         isect_host = self._pinned("isect_totals", C, torch.int64)
         isect_host.copy_(isect_tot, non_blocking=True)
+        range_host = self._pinned("proj_range", 2 * RANGE_SLOTS, torch.int32)
+        range_host.copy_(proj_range, non_blocking=True)
         isects_ready = self._record()
 
         totals_ready.synchronize()  # host read 1: the projection keeps the GPU busy
@@ -342,7 +365,9 @@ class TideStep:
         T = tot[C]
         if update and T:
             # per-block touch counts for the optimizer's slot bookkeeping
+            self._begin("touch_counts")
             counts_host = self.optimizer.launch_touch_counts(self.gaussians, touched[:T])
+            self._end()
             counts_ready = self._record()
 
         # 3. intersections in the reference's (camera, tile, depth, entry) order:
@@ -358,6 +383,7 @@ class TideStep:
         eb_base = self._buf("emit_block_base", n_eb, torch.int32)
         ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(n_eb), torch.uint8)
         self._begin("isect_scan")
+        key_base, key_bits = 0, 32
         if V:
             sel = ctypes.c_int(0)
             dws = self._buf("sort_ws", lib.tgs_segmented_sort_workspace_size(V, C), torch.uint8)
@@ -369,12 +395,30 @@ class TideStep:
                    N.ptr(dkeys2), N.ptr(rects2), 8, V, C, cam_segs, key_base, key_bits,
                    N.ptr(dws), dws.numel(), ctypes.byref(sel), s)
             if sel.value:
-                rects = rects2
+                dkeys, rects, dkeys2, rects2 = dkeys2, rects2, dkeys, rects
             N.call("tgs_tide_isect_block_sums", V, N.ptr(rects), N.ptr(eb_sums), s)
             N.call("tgs_exclusive_scan_u32", N.ptr(eb_sums), N.ptr(eb_base), n_eb, N.ptr(ws),
                    ws.numel(), s)
         self._end()
+        self.last_depth_key_bits = key_bits
         isects_ready.synchronize()  # host read 2: the depth sort keeps the GPU busy
+        if V and not depth_range_holds(range_host.tolist(), key_base, key_bits):
+            # a projected key outside the visibility pass's range (plus slack)
+            # tied with its neighbours in the ranked sort; a stable sort on all
+            # 32 bits of the ranked result restores the (depth, entry) order,
+            # since equal keys kept their input order in the ranked sort
+            self.depth_sort_repairs += 1
+            self._begin("depth_sort_repair")
+            sel = ctypes.c_int(0)
+            N.call("tgs_segmented_sort_pairs_u32", N.ptr(dkeys), N.ptr(rects), N.ptr(dkeys2),
+                   N.ptr(rects2), 8, V, C, cam_segs, 0, 32, N.ptr(dws), dws.numel(),
+                   ctypes.byref(sel), s)
+            if sel.value:
+                dkeys, rects, dkeys2, rects2 = dkeys2, rects2, dkeys, rects
+            N.call("tgs_tide_isect_block_sums", V, N.ptr(rects), N.ptr(eb_sums), s)
+            N.call("tgs_exclusive_scan_u32", N.ptr(eb_sums), N.ptr(eb_base), n_eb, N.ptr(ws),
+                   ws.numel(), s)
+            self._end()
         per_cam = isect_host.tolist()
         isect_segs = [0]
         for k in per_cam:
@@ -395,10 +439,8 @@ class TideStep:
             tws = self._buf("sort_ws2", lib.tgs_segmented_sort_workspace_size(n_isects, C),
                             torch.uint8)
             segs = _segments(isect_segs)
-            passes = (tile_bits + 7) // 8
-            mask0 = (1 << ((tile_bits + passes - 1) // passes)) - 1
             N.call("tgs_tide_isect_emit_blocked_hist", V, N.ptr(cam_offsets), C, N.ptr(rects),
-                   N.ptr(eb_base), tw, tile_bits, N.ptr(keys), N.ptr(fids), segs, mask0,
+                   N.ptr(eb_base), tw, tile_bits, N.ptr(keys), N.ptr(fids), segs,
                    N.ptr(tws), tws.numel() // 4, s)
             sel = ctypes.c_int(0)
             N.call("tgs_segmented_sort_pairs_u32_hist0", N.ptr(keys), N.ptr(fids), N.ptr(keys2),
@@ -451,9 +493,14 @@ class TideStep:
         if update:
             if T:
                 self._iteration += 1
+                # slot bookkeeping and the bias-term upload (host work that
+                # overlaps the raster backward; the bracket shows what of it
+                # reaches the GPU's timeline)
+                self._begin("optimizer_host")
                 counts_ready.synchronize()
                 opt_args, opt_stats = self.optimizer.fused_update_args(
                     self._iteration, self.gaussians, T, counts_host)
+                self._end()
                 self._begin("project_bwd_update")
                 N.call("tgs_tide_project_bwd_update", T, N.ptr(touched), N.ptr(visit_base),
                        N.ptr(visits), N.ptr(masks), C, N.ptr(P), self.row_stride,
@@ -486,6 +533,21 @@ class TideStep:
                           n_isects=n_isects, loss_sums=sums.view(C, 2), optimizer=opt_stats,
                           isects_per_camera=[isect_segs[c + 1] - isect_segs[c] for c in range(C)])
         return touched[:T], grads, stats
+
+    def snapshot(self) -> dict:
+        """A copy of everything a step changes (the resident table, the
+        optimizer's moments and slot bookkeeping, the iteration count), so
+        that :meth:`restore` can run a step again from the same scene state."""
+        torch.cuda.current_stream(self.device).synchronize()
+        return {"params": self.params.clone(), "optimizer": self.optimizer.snapshot(),
+                "iteration": self._iteration}
+
+    def restore(self, snap: dict) -> None:
+        """Put a :meth:`snapshot` back in place (device copies queued on the
+        current stream)."""
+        self.params.copy_(snap["params"])
+        self.optimizer.restore(snap["optimizer"])
+        self._iteration = snap["iteration"]
 
     def optimizer_step(self, touched: torch.Tensor, grads: torch.Tensor) -> dict:
         self._iteration += 1
