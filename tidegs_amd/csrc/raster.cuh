@@ -203,10 +203,11 @@ __device__ __forceinline__ float raster_power(const float4& g0, const float2& g1
 }
 
 // Compact batch entries [j_lo, batch_size) whose box meets the wave's pixel
-// strip into s_list (ascending j).  Returns the count (wave-uniform); `hits`
-// receives the membership bits of entries 0..63 (bit j set iff j is listed).
-template <int BLOCK>
-__device__ __forceinline__ int build_wave_list(const float4* s_box, uint8_t* s_list, int j_lo,
+// strip into s_list (ascending j, stored as j * SCALE).  Returns the count
+// (wave-uniform); `hits` receives the membership bits of entries 0..63 (bit j
+// set iff j is listed).
+template <int BLOCK, typename LT = uint8_t, int SCALE = 1>
+__device__ __forceinline__ int build_wave_list(const float4* s_box, LT* s_list, int j_lo,
                                                int batch_size, float x0, float x1, float y0,
                                                float y1, uint64_t& hits) {
   int count = 0;
@@ -223,7 +224,7 @@ __device__ __forceinline__ int build_wave_list(const float4* s_box, uint8_t* s_l
     // rank among the hits below this lane: mbcnt counts the mask bits of lower lanes
     const int rank = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-    if (hit) s_list[count + rank] = (uint8_t)j;
+    if (hit) s_list[count + rank] = (LT)(j * SCALE);
     count += __popcll(m);
   }
   __builtin_amdgcn_wave_barrier();
@@ -298,8 +299,8 @@ struct GeoRecs {
 // 64-bit pixel mask (bit r * TILE + j = pixel (r, j) of the strip = lane
 // r * TILE + j), stored as two 32-bit halves: s_emh[0][li] holds lanes 0..31,
 // s_emh[1][li] lanes 32..63, so that a lane reads only its own half.
-template <int TILE, int BATCH, class Geo>
-__device__ __forceinline__ void strip_masks(const uint8_t* s_list, int n_list, const Geo geo,
+template <int TILE, int BATCH, class Geo, typename LT = uint8_t, int SCALE = 1>
+__device__ __forceinline__ void strip_masks(const LT* s_list, int n_list, const Geo geo,
                                             const float4* s_box, const float4* s_cov,
                                             uint32_t (*s_emh)[BATCH], float px0, float py0,
                                             uint64_t alive) {
@@ -312,7 +313,7 @@ __device__ __forceinline__ void strip_masks(const uint8_t* s_list, int n_list, c
   for (int li0 = 0; li0 < n_list; li0 += PER) {
     const int li = li0 + e;
     if (li < n_list) {
-      const int t = s_list[li];
+      const int t = (int)s_list[li] / SCALE;
       const uint32_t m =
           cover_row<TILE>(geo.G0(t), geo.G1(t), s_box[t], s_cov[t], px0, py0 + (float)r);
       reinterpret_cast<RM*>(&s_emh[(r * TILE) >> 5][li])[((r * TILE) & 31) / TILE] =
@@ -607,7 +608,9 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   __shared__ __align__(16) float s_col[BATCH][CPAD];
   __shared__ float s_vrc[BLOCK][CDIM];  // dL/dcolor of each pixel
   __shared__ int32_t s_id[BATCH];
-  __shared__ uint8_t s_list[WAVES][BATCH];
+  // each wavefront's list of staged entries as byte offsets t * 16 (the
+  // stride of s_g0 and s_col; s_g1's is half of it)
+  __shared__ uint16_t s_list[WAVES][BATCH];
   __shared__ float4 s_box[BATCH];
   __shared__ float4 s_cov[BATCH];
   __shared__ int32_t s_bin_max[WAVES];
@@ -714,16 +717,17 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
     int n_list = 0;
     uint64_t hits = 0;
     if (alive)
-      n_list = build_wave_list<BATCH>(s_box, s_list[wave], j_lo, batch_size, wx0, wx1, wy0, wy1,
-                                      hits);
+      n_list = build_wave_list<BATCH, uint16_t, 16>(s_box, s_list[wave], j_lo, batch_size, wx0,
+                                                    wx1, wy0, wy1, hits);
     // 1. pixel masks, slot ranges and this lane's bits over the list
     uint32_t m[WORDS];
 #pragma unroll
     for (int W = 0; W < WORDS; ++W) m[W] = 0u;
     uint32_t n_pairs = 0;  // wave-uniform
     if (n_list) {
-      strip_masks<TILE, BATCH>(s_list[wave], n_list, GeoArrays{s_g0, s_g1}, s_box, s_cov,
-                               s_emh[wave], wx0, wy0, alive);
+      strip_masks<TILE, BATCH, GeoArrays, uint16_t, 16>(s_list[wave], n_list,
+                                                         GeoArrays{s_g0, s_g1}, s_box, s_cov,
+                                                         s_emh[wave], wx0, wy0, alive);
       uint32_t c_lo = 0u, c_hi = 0u;
       if (lane < n_list) {
         c_lo = (uint32_t)__popc(s_emh[wave][0][lane]);
@@ -769,7 +773,18 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // 2. per-pixel walk over entries [a, e_end), back to front
+      // 2. per-pixel walk over entries [a, e_end), back to front.  Addresses
+      //    come from VGPR bases (the lane index, not the wave-uniform SGPR
+      //    index): the list, the staged records, and the pair buffer moved
+      //    back by the segment's first slot, so a pair's slot address is
+      //    pair_v + 8 (first slot of its half + rank among the half's pixels)
+      const uint16_t* my_list = &s_list[0][0] + (tr & ~63u);
+      const char* g0_base = reinterpret_cast<const char*>(s_g0);
+      const char* g1_base = reinterpret_cast<const char*>(s_g1);
+      const char* col_base = reinterpret_cast<const char*>(&s_col[0][0]);
+      static_assert(RB_PAIRS % 64 == 0, "pair buffer in whole rows of 64 slots");
+      char* pair_v = reinterpret_cast<char*>(&s_pair[0][0]) + (tr & ~63u) * (RB_PAIRS / 64) * 8 -
+                     8 * (int)base;
       auto walk = [&](auto safe_tag) {
         constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
@@ -783,9 +798,11 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
             if (mw != 0u) {
               const int li = W * 32 + __builtin_ctz(mw);
               mw &= mw - 1u;
-              const int t = s_list[wave][li];
-              const float4 g0 = s_g0[t];
-              const float2 g1 = s_g1[t];
+              const uint32_t t16 = my_list[li];
+              const float4 g0 = *reinterpret_cast<const float4*>(g0_base + t16);
+              const float2 g1 = *reinterpret_cast<const float2*>(g1_base + (t16 >> 1));
+              float4 col = make_float4(0.f, 0.f, 0.f, 0.f);
+              if constexpr (CPAD == 4) col = *reinterpret_cast<const float4*>(col_base + t16);
               const float power = raster_power(g0, g1, g0.x - px, g0.y - py);
               // predicated rather than branched: a pixel failing the exact
               // test keeps T and the colour buffer and writes (0, 0), the
@@ -797,18 +814,20 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
               const float Tn = T * ra;
               T = pass ? Tn : T;
               // v_alpha = sum_k (c_k T - buffer_k ra) v_rc_k + ra tf_term
+              const float ck[4] = {col.x, col.y, col.z, col.w};
               float cv = 0.f;
 #pragma unroll
-              for (int k = 0; k < CDIM; ++k) cv = fmaf(s_col[t][k], v_rc[k], cv);
+              for (int k = 0; k < CDIM; ++k)
+                cv = fmaf(CPAD == 4 ? ck[k] : s_col[t16 >> 4][k], v_rc[k], cv);
               const float v_alpha = fmaf(Tn, cv, ra * (tf_term - buffer_dot));
               const float fac = pass ? alpha * Tn : 0.f;
               buffer_dot = SAFE ? (pass ? fmaf(fac, cv, buffer_dot) : buffer_dot)
                                 : fmaf(fac, cv, buffer_dot);
               // reference: the sigma terms only where alpha was not clamped
               const float v_sigma = pass && raw <= 0.999f ? -raw * v_alpha : 0.f;
-              const uint32_t slot = (uint32_t)s_poh[wave][half][li] - base +
+              const uint32_t slot = (uint32_t)s_poh[wave][half][li] +
                                     (uint32_t)__popc(s_emh[wave][half][li] & lt_half);
-              s_pair[wave][slot] = make_float2(fac, v_sigma);
+              *reinterpret_cast<float2*>(pair_v + 8 * slot) = make_float2(fac, v_sigma);
             }
           }
         }
@@ -831,7 +850,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
         int t = 0;
         if (oe < gn) {
           const int li = e0 + oe;
-          t = s_list[wave][li];
+          t = s_list[wave][li] >> 4;
           const float4 g0 = s_g0[t];
           q = staged_conic_rop(g0, s_g1[t]);
           uint32_t slot = (uint32_t)s_poh[wave][oh][li] - base;
