@@ -206,6 +206,64 @@ def test_isect_tiles_bit_exact(gpu, C):
     np.testing.assert_array_equal(to_np(offs), R.isect_offset_encode(o_ids, C, tw, th))
 
 
+@pytest.mark.parametrize("case", ["depth_ties", "negative_depth", "unsorted_cameras"])
+def test_isect_tiles_paths_bit_exact(gpu, case):
+    """isect_tiles on equal depths (ties broken by entry index: the reference's
+    stable sort of (camera, tile, depth, entry) keys), on a negative depth
+    (the reference sign-extends its bits into the key, which then sorts past
+    every tile) and on packed camera ids out of order: bit-exact with the
+    oracle in every case."""
+    announce(f"isect paths {case}")
+    sc, radii, m2d, depths, _, _ = _projected(gpu, seed=5, C=3)
+    W, H, ts = sc.width, sc.height, 16
+    tw, th = -(-W // ts), -(-H // ts)
+    depths = depths.clone()
+    if case == "depth_ties":
+        depths = torch.round(depths * 4) / 4  # a few hundred distinct depths
+    elif case == "negative_depth":
+        vis = torch.nonzero(radii.reshape(-1) > 0).reshape(-1)
+        depths.view(-1)[vis[::97]] *= -1.0
+    if case == "unsorted_cameras":
+        cam, gid = torch.nonzero(radii > 0, as_tuple=True)
+        perm = torch.randperm(cam.numel(), generator=torch.Generator().manual_seed(1)).to(gpu)
+        cam, gid = cam[perm], gid[perm]
+        args = (m2d[cam, gid].contiguous(), radii[cam, gid].contiguous(),
+                depths[cam, gid].contiguous())
+        tiles, ids, flat = ops.isect_tiles(*args, ts, tw, th, packed=True, n_cameras=3,
+                                           camera_ids=cam, gaussian_ids=gid)
+        o_tiles, o_ids, o_flat = R.isect_tiles(*[to_np(a) for a in args], ts, tw, th,
+                                               camera_ids=to_np(cam))
+    else:
+        tiles, ids, flat = ops.isect_tiles(m2d, radii, depths, ts, tw, th)
+        o_tiles, o_ids, o_flat = R.isect_tiles(to_np(m2d), to_np(radii), to_np(depths), ts, tw,
+                                               th)
+    assert ids.numel() > 10000
+    np.testing.assert_array_equal(to_np(tiles), o_tiles)
+    np.testing.assert_array_equal(to_np(ids), o_ids)
+    np.testing.assert_array_equal(to_np(flat), o_flat)
+
+
+@pytest.mark.parametrize("n,shift", [(1, 0), (7, 0), (9, 1), (4096 + 5, 3), (200_003, 1)])
+def test_isect_offset_encode_ragged(gpu, n, shift):
+    """Offsets from sorted keys of every length class of the eight-keys-per-
+    thread encoder (shorter than a thread's run, ragged tail) and from a key
+    view that is not 32-byte aligned, with empty buckets before, between and
+    after the runs; equal to the oracle's encoding."""
+    announce(f"offset encode n={n} shift={shift}")
+    C, tw, th = 3, 7, 5
+    rng = np.random.default_rng(n)
+    # buckets drawn sparsely so that many stay empty; keys sorted by bucket
+    buckets = np.sort(rng.integers(1, C * tw * th - 1, size=n))
+    tile_bits = int(tw * th).bit_length()
+    cam, tile = buckets // (tw * th), buckets % (tw * th)
+    keys = ((cam << (32 + tile_bits)) | (tile << 32) | rng.integers(0, 2**31, size=n)).astype(np.int64)
+    buf = torch.zeros(n + shift, dtype=torch.int64)
+    buf[shift:] = torch.from_numpy(keys)
+    d = buf.to(gpu)[shift:]
+    offs = ops.isect_offset_encode(d, C, tw, th)
+    np.testing.assert_array_equal(to_np(offs), R.isect_offset_encode(keys, C, tw, th))
+
+
 def test_isect_tiles_packed_and_empty(gpu):
     announce("isect packed + empty")
     sc, radii, m2d, depths, _, _ = _projected(gpu, seed=4, C=2)
