@@ -482,6 +482,12 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     uint64_t hits;
     const int n_list =
         build_wave_list<BATCH>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1, hits);
+    // list positions past the list name staged record 0, so a lane with no
+    // entry left reads a staged record without a select
+#pragma unroll
+    for (int k = 0; k < BATCH; k += 64)
+      if (n_list <= k + (int)(tr & 63)) s_list[wave][k + (tr & 63)] = 0;
+    __builtin_amdgcn_wave_barrier();
     strip_masks<TILE, BATCH>(s_list[wave], n_list, GeoRecs<CDIM>{s_rec}, s_box, s_cov,
                              s_emh[wave], wx0, wy0, alive);
     uint32_t mw[WORDS];
@@ -506,8 +512,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
           const bool act = m != 0u;
           const int bit = __builtin_ctz(m | 0x80000000u);  // 31 where m is empty
           m &= m - 1u;
-          const int te = my_list[W * 32 + bit];
-          const int t = act ? te : 0;
+          const int t = my_list[W * 32 + bit];
           const StagedRec<CDIM>& rec = s_rec[t];
           const float4 g0 = rec.g0;
           const float4 g1 = rec.g1;
@@ -515,8 +520,9 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
           const bool pass = act && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
           const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
           const float next_T = T * (1.f - alpha);
-          const bool stop = pass && next_T <= 1e-4f;
-          const bool comp = pass && !stop;
+          const bool low = next_T <= 1e-4f;
+          const bool stop = pass && low;
+          const bool comp = pass && !low;
           m = stop ? 0u : m;
           const float vis = comp ? alpha * T : 0.f;
 #pragma unroll
@@ -815,9 +821,9 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
               T = pass ? Tn : T;
               // v_alpha = sum_k (c_k T - buffer_k ra) v_rc_k + ra tf_term
               const float ck[4] = {col.x, col.y, col.z, col.w};
-              float cv = 0.f;
+              float cv = (CPAD == 4 ? ck[0] : s_col[t16 >> 4][0]) * v_rc[0];
 #pragma unroll
-              for (int k = 0; k < CDIM; ++k)
+              for (int k = 1; k < CDIM; ++k)
                 cv = fmaf(CPAD == 4 ? ck[k] : s_col[t16 >> 4][k], v_rc[k], cv);
               const float v_alpha = fmaf(Tn, cv, ra * (tf_term - buffer_dot));
               const float fac = pass ? alpha * Tn : 0.f;
