@@ -44,15 +44,15 @@ BYTES = {
     "adam": lambda s: s["T"] * 1656,
     # intersection stages, as this design's passes move them: the depth sort
     # of the V entries (per pass 4 B key + 8 B (rectangle, entry) read and
-    # written, + the 4 B key read of its histogram), the per-block area sums
-    # (8 B rectangle read); the emission (8 B rectangle read per entry, 4 B
-    # key + 4 B flatten id written per intersection), the tile-bit sort (per
-    # pass 8 B read + 8 B written per intersection, + 4 B histogram key read
-    # on every pass but the first, which the emission counts) and the offset
-    # encode (4 B key read per intersection, 4 B per bucket written)
+    # written, + the 4 B key read of its histogram), the per-block digit
+    # counts of the tile sort's first pass (8 B rectangle read); the emission
+    # fused with that first pass (8 B rectangle read per entry, 4 B key + 4 B
+    # flatten id written per intersection), the tile sort's remaining passes
+    # (8 B read + 8 B written per intersection, + 4 B histogram key read) and
+    # the offset encode (4 B key read per intersection, 4 B per bucket written)
     "isect_scan": lambda s: s["V"] * (s["passes_d"] * (24 + 4) + 8),
-    "isect_sort": lambda s: (8 * s["V"] + 8 * s["I"] + s["passes_t"] * 16 * s["I"]
-                             + (s["passes_t"] - 1) * 4 * s["I"] + 4 * s["I"] + 4 * s["buckets"]),
+    "isect_sort": lambda s: (8 * s["V"] + 8 * s["I"] + (s["passes_t"] - 1) * 20 * s["I"]
+                             + 4 * s["I"] + 4 * s["buckets"]),
     # fused: the row read once, p/m/v written, m/v read; no gradient rows
     "project_bwd_update": lambda s: (s["T"] * (4 + 4 + 4 + 236 + 2 * 236 + 3 * 236)
                                      + s["V"] * (4 + 36)),

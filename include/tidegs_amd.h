@@ -411,6 +411,37 @@ int tgs_tide_isect_emit_blocked_hist(uint32_t n_entries, const int32_t* cam_offs
                                      uint32_t tile_width, uint32_t tile_n_bits, uint32_t* keys,
                                      int32_t* flatten_ids, const uint32_t* isect_cam_offsets,
                                      uint32_t* hist, uint64_t hist_words, tgs_stream_t stream);
+/* Beside the reference's interface: the emission fused with the first pass of
+ * the tile-bit sort (the form TideStep uses).  The depth-ordered entries of
+ * each camera (cam_offsets: the C + 1 host-side first entries per camera) are
+ * taken in blocks of 1024 that never span two cameras.
+ *   tgs_tide_isect_fused_digit_bits  the first pass's width w over tile_n_bits
+ *                                    bits (ceil(bits / 8) passes of
+ *                                    ceil(bits / passes) bits);
+ *   tgs_tide_isect_fused_hist_words  hist words: blocks * 2^w;
+ *   tgs_tide_isect_fused_count       hist [camera][digit][block of the camera]
+ *                                    = the block's intersections with tile &
+ *                                    (2^w - 1) == digit;
+ *   (tgs_exclusive_scan_u32 of hist -> hist_scan)
+ *   tgs_tide_isect_fused_scatter     keys [n_isects] = camera << tile_n_bits |
+ *                                    tile and flatten ids in the order of a
+ *                                    stable sort of the emission (isect_tiles.cu
+ *                                    :73-98 over the depth-ordered entries) on
+ *                                    bits [0, w) within each camera;
+ *   (tgs_segmented_sort_pairs_u32 on bits [w, tile_n_bits) per camera, when
+ *    tile_n_bits > w, completes the tile-bit sort). */
+uint32_t tgs_tide_isect_fused_digit_bits(uint32_t tile_n_bits);
+uint64_t tgs_tide_isect_fused_hist_words(uint32_t C, const uint32_t* cam_offsets,
+                                         uint32_t tile_n_bits);
+int tgs_tide_isect_fused_count(uint32_t C, const uint32_t* cam_offsets,
+                               const uint64_t* entry_rects, uint32_t tile_width,
+                               uint32_t tile_n_bits, uint32_t* hist, uint64_t hist_words,
+                               tgs_stream_t stream);
+int tgs_tide_isect_fused_scatter(uint32_t C, const uint32_t* cam_offsets,
+                                 const uint64_t* entry_rects, uint32_t tile_width,
+                                 uint32_t tile_n_bits, const uint32_t* hist_scan,
+                                 uint64_t hist_words, uint32_t n_isects, uint32_t* keys,
+                                 int32_t* flatten_ids, tgs_stream_t stream);
 int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, uint32_t C,
                            uint32_t tile_width, uint32_t tile_height, uint32_t tile_n_bits,
                            int32_t* offsets, tgs_stream_t stream);

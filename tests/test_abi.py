@@ -18,7 +18,7 @@ def _declarations():
     for header in sorted((ROOT / "include").glob("*.h")):
         text = header.read_text()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        for m in re.finditer(r"\b(?:int|size_t|uint32_t|const char\*)\s+(tgs_\w+)\s*\(([^;]*?)\)\s*;",
+        for m in re.finditer(r"\b(?:int|size_t|uint32_t|uint64_t|const char\*)\s+(tgs_\w+)\s*\(([^;]*?)\)\s*;",
                              text, flags=re.S):
             args = m.group(2).strip()
             n_args = 0 if args in ("", "void") else args.count(",") + 1

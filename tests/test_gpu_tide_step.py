@@ -195,6 +195,85 @@ def test_emit_hist_then_hist0_sort(gpu, V, C, big):
         np.testing.assert_array_equal(fo[a:b], f_in[order])
 
 
+@pytest.mark.parametrize("V,C,big,tw,th", [(3000, 4, 0.0, 120, 68), (20_000, 6, 0.02, 120, 68),
+                                           (70_000, 16, 0.001, 120, 68), (5000, 3, 0.01, 16, 9),
+                                           (1, 1, 0.0, 120, 68)])
+def test_fused_emission_sort_matches_stable_tile_sort(gpu, V, C, big, tw, th):
+    """tgs_tide_isect_fused_count + scan + tgs_tide_isect_fused_scatter (the
+    emission written in the order of the tile-bit sort's first pass) and the
+    remaining pass give the stable per-camera sort of the emission
+    (isect_tiles.cu:73-98 over the entries in the given order) on the tile
+    bits, as numpy's stable argsort gives it: an empty camera, entries whose
+    rectangles span several 4096-intersection chunks of a block (up to 120 x
+    68 tiles), a grid whose tile bits fit one pass (16 x 9 tiles), one entry."""
+    announce(f"fused emission + first tile pass V={V} C={C} big={big} grid={tw}x{th}")
+    import ctypes
+    from tidegs_amd import _native as N
+    lib = N.load()
+    rng = np.random.default_rng(V * 13 + C + tw)
+    x0 = rng.integers(0, tw, V)
+    y0 = rng.integers(0, th, V)
+    wide = rng.random(V) < big
+    x1 = np.minimum(x0 + np.where(wide, rng.integers(min(20, tw), tw + 1, V),
+                                  rng.integers(0, 5, V)), tw)
+    y1 = np.minimum(y0 + np.where(wide, rng.integers(min(20, th), th + 1, V),
+                                  rng.integers(0, 4, V)), th)
+    if big:  # entries whose rectangles span whole chunks
+        x0[:3], y0[:3], x1[:3], y1[:3] = 0, 0, tw, th
+    rc = (x0 | (x1 << 8) | (y0 << 16) | (y1 << 24)).astype(np.uint64)
+    ids = rng.integers(0, 1 << 30, V).astype(np.uint64)
+    rects = torch.from_numpy(((rc << np.uint64(32)) | ids).view(np.int64)).to(gpu)
+    if C > 2:
+        cuts = np.sort(rng.choice(np.arange(1, V), size=C - 2, replace=False))
+        cam = np.concatenate([[0], cuts[:1], cuts[:1], cuts[1:], [V]]).astype(np.int64)  # cam 1 empty
+    else:
+        cam = np.linspace(0, V, C + 1).astype(np.int64)
+    area = (x1 - x0) * (y1 - y0)
+    segs = [0] + [int(v) for v in np.array([area[cam[c]:cam[c + 1]].sum()
+                                             for c in range(C)]).cumsum()]
+    n_isects = segs[-1]
+    tile_bits = (tw * th).bit_length()
+    s = N.stream_handle()
+    co = (ctypes.c_uint32 * (C + 1))(*[int(v) for v in cam])
+    words = int(lib.tgs_tide_isect_fused_hist_words(C, co, tile_bits))
+    hist = torch.empty(max(words, 1), dtype=torch.int32, device=gpu)
+    hscan = torch.empty_like(hist)
+    ws = torch.empty(lib.tgs_scan_workspace_size(max(words, 1)), dtype=torch.uint8, device=gpu)
+    N.call("tgs_tide_isect_fused_count", C, co, N.ptr(rects), tw, tile_bits, N.ptr(hist), words, s)
+    N.call("tgs_exclusive_scan_u32", N.ptr(hist), N.ptr(hscan), words, N.ptr(ws), ws.numel(), s)
+    k = torch.empty(max(n_isects, 1), dtype=torch.int32, device=gpu)
+    f = torch.empty_like(k)
+    N.call("tgs_tide_isect_fused_scatter", C, co, N.ptr(rects), tw, tile_bits, N.ptr(hscan), words,
+           n_isects, N.ptr(k), N.ptr(f), s)
+    w1 = int(lib.tgs_tide_isect_fused_digit_bits(tile_bits))
+    if tile_bits > w1:
+        k2, f2 = torch.empty_like(k), torch.empty_like(f)
+        tws = torch.empty(lib.tgs_segmented_sort_workspace_size(n_isects, C), dtype=torch.uint8,
+                          device=gpu)
+        sel = ctypes.c_int(0)
+        hs = (ctypes.c_uint32 * (C + 1))(*segs)
+        N.call("tgs_segmented_sort_pairs_u32", N.ptr(k), N.ptr(f), N.ptr(k2), N.ptr(f2), 4,
+               n_isects, C, hs, w1, tile_bits, N.ptr(tws), tws.numel(), ctypes.byref(sel), s)
+        if sel.value:
+            k, f = k2, f2
+    ko, fo = to_np(k)[:n_isects].view(np.uint32), to_np(f)[:n_isects]
+    # the emission in entry order (each rectangle row by row), then a stable
+    # sort on the tile bits within each camera
+    cam_of = np.zeros(V, np.int64)
+    for c in range(C):
+        cam_of[cam[c]:cam[c + 1]] = c
+    e = np.repeat(np.arange(V), area)
+    w = np.maximum(x1 - x0, 1)
+    o = np.arange(len(e)) - np.repeat(np.cumsum(area) - area, area)
+    tile = (y0[e] + o // w[e]) * tw + x0[e] + o % w[e]
+    k_in = ((cam_of[e] << tile_bits) | tile).astype(np.uint32)
+    f_in = ids[e].astype(np.uint32).view(np.int32)
+    for a, b in zip(segs[:-1], segs[1:]):
+        order = np.argsort(tile[a:b], kind="stable") + a
+        np.testing.assert_array_equal(ko[a:b], k_in[order])
+        np.testing.assert_array_equal(fo[a:b], f_in[order])
+
+
 def test_tide_step_isect_bit_exact(gpu):
     announce("tide step isect")
     sc = _scene(seed=2)

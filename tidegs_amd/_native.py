@@ -117,6 +117,11 @@ SIGNATURES = {
         ctypes.c_int,
         [P, P, P, P, U64, U32, P, ctypes.c_int, ctypes.c_int, P, SZ, ctypes.POINTER(ctypes.c_int),
          P]),
+    "tgs_tide_isect_fused_digit_bits": (U32, [U32]),
+    "tgs_tide_isect_fused_hist_words": (U64, [U32, P, U32]),
+    "tgs_tide_isect_fused_count": (ctypes.c_int, [U32, P, P, U32, U32, P, U64, P]),
+    "tgs_tide_isect_fused_scatter": (
+        ctypes.c_int, [U32, P, P, U32, U32, P, U64, U32, P, P, P]),
     "tgs_tide_offset_encode": (ctypes.c_int, [U32, P, U32, U32, U32, U32, P, P]),
     "tgs_tide_isect_ids": (ctypes.c_int, [U32, P, P, P, P, P]),
     "tgs_tide_rasterize_fwd": (

@@ -704,6 +704,230 @@ __global__ void __launch_bounds__(256) tide_isect_emit_blocked_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Emission fused with the tile-bit sort's first pass.  The depth-ordered
+// entries of each camera are taken in blocks of FE_ENTRIES (a block never
+// spans two cameras).  tide_isect_fused_count_kernel counts every block's
+// intersections by first-pass digit (tile & mask) into hist, laid out
+// [camera][digit][block of the camera], so that its exclusive scan is the
+// first output slot of every (camera, digit, block).  tide_isect_fused_
+// scatter_kernel then generates each block's intersections in emission order
+// (entries in depth order, each entry's tiles row by row) in LDS chunks of
+// FE_CHUNK, ranks each chunk stably by the digit (ballot matching and per-wave
+// digit counters, as the radix passes do), and writes every digit's run of the
+// chunk contiguously at its slot: the emission's keys and flatten ids never
+// reach memory in emission order.  Stable in the emission order, so the
+// remaining tile-bit passes give the reference's order unchanged.
+// ---------------------------------------------------------------------------
+#define FE_ENTRIES 1024
+#define FE_ITEMS (FE_ENTRIES / 256)
+#define FE_CHUNK 2048
+#define FE_KEYS (FE_CHUNK / 256)
+
+struct FusedEmit {
+  uint32_t C;
+  uint32_t tw, tile_n_bits;
+  uint32_t mask;                          // first-pass digit of a tile: tile & mask
+  uint32_t ent_off[TIDE_MAX_CAMS + 1];    // first depth-ordered entry of each camera
+  uint32_t blk_first[TIDE_MAX_CAMS + 1];  // first block of each camera
+};
+
+__device__ __forceinline__ void fe_block(const FusedEmit& fe, uint32_t b, uint32_t& c,
+                                         uint32_t& bl, uint32_t& e0, uint32_t& e1) {
+  c = 0;
+  while (c + 1 < fe.C && fe.blk_first[c + 1] <= b) ++c;
+  bl = b - fe.blk_first[c];
+  e0 = fe.ent_off[c] + bl * FE_ENTRIES;
+  e1 = min(e0 + FE_ENTRIES, fe.ent_off[c + 1]);
+}
+
+// hist word of (camera c, digit d, block bl of c)
+__device__ __forceinline__ uint64_t fe_hist_index(const FusedEmit& fe, uint32_t c, uint32_t d,
+                                                  uint32_t bl) {
+  const uint32_t nb = fe.blk_first[c + 1] - fe.blk_first[c];
+  return (uint64_t)fe.blk_first[c] * (fe.mask + 1u) + (uint64_t)d * nb + bl;
+}
+
+__global__ void __launch_bounds__(256) tide_isect_fused_count_kernel(
+    FusedEmit fe, const uint64_t* __restrict__ rects, uint32_t* __restrict__ hist) {
+  __shared__ uint32_t s_cnt[256];
+  uint32_t c, bl, e0, e1;
+  fe_block(fe, blockIdx.x, c, bl, e0, e1);
+  s_cnt[threadIdx.x] = 0u;
+  __syncthreads();
+  const uint32_t* hi = reinterpret_cast<const uint32_t*>(rects) + 1;
+  uint32_t rc[FE_ITEMS];
+#pragma unroll
+  for (int k = 0; k < FE_ITEMS; ++k) {
+    const uint32_t e = e0 + (uint32_t)k * 256u + threadIdx.x;
+    rc[k] = e < e1 ? hi[2ull * e] : 0u;  // 0: an empty rectangle
+  }
+#pragma unroll
+  for (int k = 0; k < FE_ITEMS; ++k) {
+    const uint32_t x0 = rc[k] & 255u, x1 = (rc[k] >> 8) & 255u, y0 = (rc[k] >> 16) & 255u,
+                   y1 = rc[k] >> 24;
+    for (uint32_t y = y0; y < y1; ++y)
+      for (uint32_t x = x0; x < x1; ++x) atomicAdd(&s_cnt[(y * fe.tw + x) & fe.mask], 1u);
+  }
+  __syncthreads();
+  if (threadIdx.x <= fe.mask) hist[fe_hist_index(fe, c, threadIdx.x, bl)] = s_cnt[threadIdx.x];
+}
+
+__global__ void __launch_bounds__(256) tide_isect_fused_scatter_kernel(
+    FusedEmit fe, const uint64_t* __restrict__ rects, const uint32_t* __restrict__ hist_scan,
+    uint32_t n_isects, uint32_t* __restrict__ keys, int32_t* __restrict__ flatten_ids) {
+  constexpr int WAVES = 4;
+  __shared__ uint32_t s_k[FE_CHUNK];
+  __shared__ int32_t s_v[FE_CHUNK];
+  __shared__ uint32_t s_wh[WAVES][256];
+  __shared__ uint32_t s_start[256];
+  __shared__ uint32_t s_gofs[256];
+  __shared__ uint32_t s_run[256];  // the block's slots of each digit so far
+  __shared__ uint32_t s_tot[FE_ITEMS][WAVES];
+  __shared__ uint32_t s_wsum[WAVES];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  uint32_t c, bl, e0, e1;
+  fe_block(fe, blockIdx.x, c, bl, e0, e1);
+  const uint32_t cam_enc = c << fe.tile_n_bits;
+  // the block's entries: item k of thread t is entry e0 + k * 256 + t; each
+  // entry's first intersection of the block from a scan in entry order
+  uint32_t rc[FE_ITEMS], p[FE_ITEMS];
+  int32_t id[FE_ITEMS];
+#pragma unroll
+  for (int k = 0; k < FE_ITEMS; ++k) {
+    const uint32_t e = e0 + (uint32_t)k * 256u + threadIdx.x;
+    const uint64_t v = e < e1 ? rects[e] : 0ull;  // an empty rectangle past the end
+    rc[k] = (uint32_t)(v >> 32);
+    id[k] = (int32_t)(uint32_t)v;
+    const uint32_t a = rect_tiles(rc[k]);
+    const uint32_t inc = wave_incl_scan(a);
+    p[k] = inc - a;
+    if (lane == 63) s_tot[k][wave] = inc;
+  }
+  s_run[threadIdx.x] = 0u;
+  s_gofs[threadIdx.x] = threadIdx.x <= fe.mask ? hist_scan[fe_hist_index(fe, c, threadIdx.x, bl)]
+                                               : 0u;
+  __syncthreads();
+  uint32_t n_b = 0;  // the block's intersections
+#pragma unroll
+  for (int k = 0; k < FE_ITEMS; ++k) {
+    uint32_t before = 0u, round = 0u;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const uint32_t t = s_tot[k][w];
+      before += w < wave ? t : 0u;
+      round += t;
+    }
+    p[k] += n_b + before;
+    n_b += round;
+  }
+  // s_gofs holds each digit's first slot for the block until the chunk loop
+  // turns it into per-chunk bases; keep the block bases in s_start's place
+  uint32_t gbase = s_gofs[threadIdx.x];
+  for (uint32_t q0 = 0; q0 < n_b; q0 += FE_CHUNK) {
+    const uint32_t m = min((uint32_t)FE_CHUNK, n_b - q0);
+    // 1. the chunk's intersections in emission order
+#pragma unroll
+    for (int k = 0; k < FE_ITEMS; ++k) {
+      const uint32_t a = rect_tiles(rc[k]);
+      const uint32_t lo = max(p[k], q0), hi = min(p[k] + a, q0 + FE_CHUNK);
+      if (lo < hi) {
+        const uint32_t x0 = rc[k] & 255u, x1 = (rc[k] >> 8) & 255u, y0 = (rc[k] >> 16) & 255u;
+        const uint32_t w = x1 - x0;
+        const uint32_t o = lo - p[k];  // nonzero only for an entry spanning chunks
+        uint32_t y = y0 + (o ? o / w : 0u);
+        uint32_t x = x0 + (o ? o % w : 0u);
+        for (uint32_t i = lo - q0; i < hi - q0; ++i) {
+          s_k[i] = cam_enc | (y * fe.tw + x);
+          s_v[i] = id[k];
+          if (++x == x1) {
+            x = x0;
+            ++y;
+          }
+        }
+      }
+    }
+    if (threadIdx.x < 256) {
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) s_wh[w][threadIdx.x] = 0u;
+    }
+    __syncthreads();
+    // 2. stable rank by digit: wave w owns chunk positions [w * 1024, (w + 1) * 1024)
+    //    in rounds of 64
+    uint32_t kk[FE_KEYS];
+    int32_t vv[FE_KEYS];
+    uint32_t rk[FE_KEYS];
+#pragma unroll
+    for (int r = 0; r < FE_KEYS; ++r) {
+      const uint32_t li = (uint32_t)(wave * 64 * FE_KEYS + r * 64 + lane);
+      const bool valid = li < m;
+      kk[r] = valid ? s_k[li] : 0u;
+      vv[r] = valid ? s_v[li] : 0;
+      const uint32_t d = kk[r] & fe.mask;
+      uint64_t peers = tgs_ballot(valid);
+      rk[r] = 0u;
+      if (peers) {
+        const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)d);
+        if (tgs_ballot(valid && d == d0) != peers) {
+#pragma unroll
+          for (int bb = 0; bb < 8; ++bb) {
+            if ((fe.mask >> bb) == 0u) break;
+            const bool bit = (d >> bb) & 1u;
+            const uint64_t mm = tgs_ballot(bit);
+            peers &= bit ? mm : ~mm;
+          }
+        }
+        const uint32_t before = s_wh[wave][d];
+        __builtin_amdgcn_wave_barrier();
+        if (valid && (peers >> lane) == 1ull) s_wh[wave][d] = before + (uint32_t)__popcll(peers);
+        __builtin_amdgcn_wave_barrier();
+        rk[r] = before + (uint32_t)__popcll(peers & lt);
+      }
+    }
+    __syncthreads();
+    // 3. digit t: per-wave offsets, chunk start, output base
+    uint32_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const uint32_t cnt = s_wh[w][threadIdx.x];
+      s_wh[w][threadIdx.x] = tot;
+      tot += cnt;
+    }
+    uint32_t inc = wave_incl_scan(tot);
+    if (lane == 63) s_wsum[wave] = inc;
+    __syncthreads();
+    uint32_t st = inc - tot;
+    for (int w = 0; w < wave; ++w) st += s_wsum[w];
+    s_start[threadIdx.x] = st;
+    s_gofs[threadIdx.x] = gbase + s_run[threadIdx.x] - st;
+    __syncthreads();
+    // 4. the chunk in (digit, emission) order into LDS, then each digit's run
+    //    written contiguously
+#pragma unroll
+    for (int r = 0; r < FE_KEYS; ++r) {
+      const uint32_t li = (uint32_t)(wave * 64 * FE_KEYS + r * 64 + lane);
+      if (li < m) {
+        const uint32_t d = kk[r] & fe.mask;
+        const uint32_t pos = s_start[d] + s_wh[wave][d] + rk[r];
+        s_k[pos] = kk[r];
+        s_v[pos] = vv[r];
+      }
+    }
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < m; j += 256) {
+      const uint32_t key = s_k[j];
+      const uint32_t o = s_gofs[key & fe.mask] + j;
+      if (o < n_isects) {
+        keys[o] = key;
+        flatten_ids[o] = s_v[j];
+      }
+    }
+    s_run[threadIdx.x] += tot;
+    __syncthreads();
+  }
+}
+
 __global__ void tide_zero_u32_kernel(uint32_t* __restrict__ p, uint64_t n) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (uint64_t)gridDim.x * blockDim.x)
@@ -1371,6 +1595,89 @@ extern "C" int tgs_tide_isect_emit_blocked_hist(
                      cam_offsets, C, entry_rects, block_base, tile_width, tile_n_bits, keys,
                      flatten_ids, eh);
   TGS_RETURN_LAUNCH("tgs_tide_isect_emit_blocked_hist");
+}
+
+// First-pass digit width of the tile-bit sort over tile_n_bits bits: the bits
+// split into ceil(bits / 8) passes of ceil(bits / passes) bits.
+extern "C" uint32_t tgs_tide_isect_fused_digit_bits(uint32_t tile_n_bits) {
+  if (tile_n_bits == 0) return 0;
+  const uint32_t passes = (tile_n_bits + 7) / 8;
+  return (tile_n_bits + passes - 1) / passes;
+}
+
+static int fused_emit_setup(uint32_t C, const uint32_t* cam_offsets, uint32_t tile_width,
+                            uint32_t tile_n_bits, FusedEmit& fe, uint32_t& n_blocks,
+                            const char* who) {
+  int rc = check_cams(C);
+  if (rc) return rc;
+  TGS_CHECK_ARG(cam_offsets, "%s: null camera offsets", who);
+  TGS_CHECK_ARG(tile_n_bits >= 1 && tile_n_bits <= 16, "%s: tile_n_bits must be in [1, 16]", who);
+  TGS_CHECK_ARG(tile_width >= 1 && tile_width <= 255, "%s: tile_width must be in [1, 255]", who);
+  fe = FusedEmit{};
+  fe.C = C;
+  fe.tw = tile_width;
+  fe.tile_n_bits = tile_n_bits;
+  fe.mask = (1u << tgs_tide_isect_fused_digit_bits(tile_n_bits)) - 1u;
+  uint64_t blocks = 0;
+  for (uint32_t c = 0; c <= C; ++c) {
+    TGS_CHECK_ARG(c == 0 || cam_offsets[c] >= cam_offsets[c - 1], "%s: camera offsets decrease",
+                  who);
+    fe.ent_off[c] = cam_offsets[c];
+    fe.blk_first[c] = (uint32_t)blocks;
+    if (c < C) blocks += (cam_offsets[c + 1] - cam_offsets[c] + FE_ENTRIES - 1) / FE_ENTRIES;
+  }
+  TGS_CHECK_ARG(blocks < (1ull << 31), "%s: too many entry blocks", who);
+  n_blocks = (uint32_t)blocks;
+  return TGS_OK;
+}
+
+extern "C" uint64_t tgs_tide_isect_fused_hist_words(uint32_t C, const uint32_t* cam_offsets,
+                                                    uint32_t tile_n_bits) {
+  FusedEmit fe;
+  uint32_t nb = 0;
+  if (fused_emit_setup(C, cam_offsets, 1, tile_n_bits, fe, nb, "tide_isect_fused_hist_words"))
+    return 0;
+  return (uint64_t)nb * (fe.mask + 1u);
+}
+
+extern "C" int tgs_tide_isect_fused_count(uint32_t C, const uint32_t* cam_offsets,
+                                          const uint64_t* entry_rects, uint32_t tile_width,
+                                          uint32_t tile_n_bits, uint32_t* hist,
+                                          uint64_t hist_words, hipStream_t stream) {
+  FusedEmit fe;
+  uint32_t nb = 0;
+  int rc = fused_emit_setup(C, cam_offsets, tile_width, tile_n_bits, fe, nb,
+                            "tide_isect_fused_count");
+  if (rc) return rc;
+  if (nb == 0) return TGS_OK;
+  TGS_CHECK_ARG(entry_rects && hist, "tide_isect_fused_count: null");
+  TGS_CHECK_ARG((uint64_t)nb * (fe.mask + 1u) <= hist_words,
+                "tide_isect_fused_count: histogram buffer too small");
+  hipLaunchKernelGGL(tide_isect_fused_count_kernel, dim3(nb), dim3(256), 0, stream, fe, entry_rects,
+                     hist);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_fused_count");
+}
+
+extern "C" int tgs_tide_isect_fused_scatter(uint32_t C, const uint32_t* cam_offsets,
+                                            const uint64_t* entry_rects, uint32_t tile_width,
+                                            uint32_t tile_n_bits, const uint32_t* hist_scan,
+                                            uint64_t hist_words, uint32_t n_isects,
+                                            uint32_t* keys, int32_t* flatten_ids,
+                                            hipStream_t stream) {
+  FusedEmit fe;
+  uint32_t nb = 0;
+  int rc = fused_emit_setup(C, cam_offsets, tile_width, tile_n_bits, fe, nb,
+                            "tide_isect_fused_scatter");
+  if (rc) return rc;
+  if (nb == 0 || n_isects == 0) return TGS_OK;
+  TGS_CHECK_ARG(entry_rects && hist_scan && keys && flatten_ids, "tide_isect_fused_scatter: null");
+  TGS_CHECK_ARG((uint64_t)nb * (fe.mask + 1u) <= hist_words,
+                "tide_isect_fused_scatter: histogram buffer too small");
+  TGS_CHECK_ARG(C - 1 < (1u << (32 - tile_n_bits)),
+                "tide_isect_fused_scatter: camera | tile keys do not fit 32 bits");
+  hipLaunchKernelGGL(tide_isect_fused_scatter_kernel, dim3(nb), dim3(256), 0, stream, fe,
+                     entry_rects, hist_scan, n_isects, keys, flatten_ids);
+  TGS_RETURN_LAUNCH("tgs_tide_isect_fused_scatter");
 }
 
 extern "C" int tgs_tide_offset_encode(uint32_t n_isects, const uint32_t* keys, uint32_t C,

@@ -371,17 +371,19 @@ class TideStep:
             counts_ready = self._record()
 
         # 3. intersections in the reference's (camera, tile, depth, entry) order:
-        #    depth sort of the entries per camera, per-block area sums + scan,
-        #    emission in depth order, stable sort of the tile bits per camera,
-        #    bucket offsets
+        #    depth sort of the entries per camera; each block of depth-ordered
+        #    entries' intersections counted by the tile-bit sort's first digit
+        #    (scanned: every (camera, digit, block)'s first slot); the emission
+        #    fused with that first pass; the remaining tile-bit pass per
+        #    camera; bucket offsets
         cam_segs = _segments([sum(tot[:c]) for c in range(C + 1)])
         dkeys2 = self._buf("depth_keys2", cap_v, torch.int32)
         rects2 = self._buf("entry_rects2", cap_v, torch.int64)
-        # emission in blocks of entries: each block's rectangle-area sum, scanned
-        n_eb = lib.tgs_tide_isect_emit_blocks(max(V, 1))
-        eb_sums = self._buf("emit_block_sums", n_eb, torch.int32)
-        eb_base = self._buf("emit_block_base", n_eb, torch.int32)
-        ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(n_eb), torch.uint8)
+        tile_bits = (tw * th).bit_length()
+        hist_words = max(int(lib.tgs_tide_isect_fused_hist_words(C, cam_segs, tile_bits)), 1)
+        fe_hist = self._buf("fused_hist", hist_words, torch.int32)
+        fe_scan = self._buf("fused_hist_scan", hist_words, torch.int32)
+        ws = self._buf("scan_ws2", lib.tgs_scan_workspace_size(hist_words), torch.uint8)
         self._begin("isect_scan")
         key_base, key_bits = 0, 32
         if V:
@@ -396,9 +398,10 @@ class TideStep:
                    N.ptr(dws), dws.numel(), ctypes.byref(sel), s)
             if sel.value:
                 dkeys, rects, dkeys2, rects2 = dkeys2, rects2, dkeys, rects
-            N.call("tgs_tide_isect_block_sums", V, N.ptr(rects), N.ptr(eb_sums), s)
-            N.call("tgs_exclusive_scan_u32", N.ptr(eb_sums), N.ptr(eb_base), n_eb, N.ptr(ws),
-                   ws.numel(), s)
+            N.call("tgs_tide_isect_fused_count", C, cam_segs, N.ptr(rects), tw, tile_bits,
+                   N.ptr(fe_hist), hist_words, s)
+            N.call("tgs_exclusive_scan_u32", N.ptr(fe_hist), N.ptr(fe_scan), hist_words,
+                   N.ptr(ws), ws.numel(), s)
         self._end()
         self.last_depth_key_bits = key_bits
         isects_ready.synchronize()  # host read 2: the depth sort keeps the GPU busy
@@ -415,9 +418,10 @@ class TideStep:
                    ctypes.byref(sel), s)
             if sel.value:
                 dkeys, rects, dkeys2, rects2 = dkeys2, rects2, dkeys, rects
-            N.call("tgs_tide_isect_block_sums", V, N.ptr(rects), N.ptr(eb_sums), s)
-            N.call("tgs_exclusive_scan_u32", N.ptr(eb_sums), N.ptr(eb_base), n_eb, N.ptr(ws),
-                   ws.numel(), s)
+            N.call("tgs_tide_isect_fused_count", C, cam_segs, N.ptr(rects), tw, tile_bits,
+                   N.ptr(fe_hist), hist_words, s)
+            N.call("tgs_exclusive_scan_u32", N.ptr(fe_hist), N.ptr(fe_scan), hist_words,
+                   N.ptr(ws), ws.numel(), s)
             self._end()
         per_cam = isect_host.tolist()
         isect_segs = [0]
@@ -425,7 +429,6 @@ class TideStep:
             isect_segs.append(isect_segs[-1] + int(k))
         n_isects = isect_segs[C]
         check_isect_count(n_isects)
-        tile_bits = (tw * th).bit_length()
         cap = max(n_isects, 1)
         keys = self._buf("keys", cap, torch.int32)
         keys2 = self._buf("keys2", cap, torch.int32)
@@ -434,20 +437,20 @@ class TideStep:
         offsets = self._buf("offsets", n_buckets, torch.int32)
         self._begin("isect_sort")
         if n_isects:
-            # the emission also counts the tile sort's first-pass digits into
-            # the sort's workspace, which then skips that pass's histogram
-            tws = self._buf("sort_ws2", lib.tgs_segmented_sort_workspace_size(n_isects, C),
-                            torch.uint8)
-            segs = _segments(isect_segs)
-            N.call("tgs_tide_isect_emit_blocked_hist", V, N.ptr(cam_offsets), C, N.ptr(rects),
-                   N.ptr(eb_base), tw, tile_bits, N.ptr(keys), N.ptr(fids), segs,
-                   N.ptr(tws), tws.numel() // 4, s)
-            sel = ctypes.c_int(0)
-            N.call("tgs_segmented_sort_pairs_u32_hist0", N.ptr(keys), N.ptr(fids), N.ptr(keys2),
-                   N.ptr(fids2), n_isects, C, segs, 0, tile_bits,
-                   N.ptr(tws), tws.numel(), ctypes.byref(sel), s)
-            if sel.value:
-                keys, fids = keys2, fids2
+            # intersections written in the order of the tile-bit sort's first
+            # pass, then its remaining passes
+            N.call("tgs_tide_isect_fused_scatter", C, cam_segs, N.ptr(rects), tw, tile_bits,
+                   N.ptr(fe_scan), hist_words, n_isects, N.ptr(keys), N.ptr(fids), s)
+            w1 = int(lib.tgs_tide_isect_fused_digit_bits(tile_bits))
+            if tile_bits > w1:
+                tws = self._buf("sort_ws2", lib.tgs_segmented_sort_workspace_size(n_isects, C),
+                                torch.uint8)
+                sel = ctypes.c_int(0)
+                N.call("tgs_segmented_sort_pairs_u32", N.ptr(keys), N.ptr(fids), N.ptr(keys2),
+                       N.ptr(fids2), 4, n_isects, C, _segments(isect_segs), w1, tile_bits,
+                       N.ptr(tws), tws.numel(), ctypes.byref(sel), s)
+                if sel.value:
+                    keys, fids = keys2, fids2
         N.call("tgs_tide_offset_encode", n_isects, N.ptr(keys), C, tw, th, tile_bits,
                N.ptr(offsets), s)
         self._end()
