@@ -589,7 +589,13 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
 // wave reduction.  When a batch has more pairs than the buffer holds, the list
 // is processed in consecutive segments (each Gaussian's pairs fit: <= 64).
 // ---------------------------------------------------------------------------
-#define RB_PAIRS 320  // pair-buffer slots per wavefront
+// Pair-buffer slots per wavefront.  The workgroup's LDS decides how many
+// workgroups share a CU: measured on MI355X, 26656 bytes of static LDS still
+// run 6 per CU and 26912 bytes only 5 (12.45 against 11.2 ms at cfg3), a limit
+// the compiler's occupancy remark does not show.  At 3 channels the kernel
+// uses 26400 bytes with 304 slots; 192 / 256 / 288 / 304 slots measured
+// 12.25 / 11.5 / 11.3 / 11.2 ms (fewer segments per unit).
+#define RB_PAIRS 304
 #define RB_BATCH 64  // Gaussians staged per batch
 
 template <int CDIM, int TILE, class Src, class Sink>
@@ -608,12 +614,15 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   constexpr int NA = NV + 2;
   __shared__ float4 s_g0[BATCH];
   __shared__ float2 s_g1[BATCH];
-  // three colours padded to four: the walk reads them with one 16-byte read
+  // three colours padded to four (the fourth holds the Gaussian id): the walk
+  // reads the colours with one 16-byte read
   // at the same t * 16 address as s_g0
   constexpr int CPAD = CDIM == 3 ? 4 : CDIM;
   __shared__ __align__(16) float s_col[BATCH][CPAD];
   __shared__ float s_vrc[BLOCK][CDIM];  // dL/dcolor of each pixel
-  __shared__ int32_t s_id[BATCH];
+  // the staged Gaussians' ids; at 3 channels they sit in the padding float of
+  // s_col (256 bytes of LDS that keep the workgroup within 6 per CU)
+  __shared__ int32_t s_id[CDIM == 3 ? 1 : BATCH];
   // each wavefront's list of staged entries as byte offsets t * 16 (the
   // stride of s_g0 and s_col; s_g1's is half of it)
   __shared__ uint16_t s_list[WAVES][BATCH];
@@ -704,7 +713,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
       s_g1[tr] = sg.g1;
       s_box[tr] = sg.box;
       s_cov[tr] = sg.cov;
-      s_id[tr] = g;
+      if constexpr (CDIM == 3) s_col[tr][3] = __int_as_float(g);
+      else s_id[tr] = g;
 #pragma unroll
       for (int k = 0; k < CDIM; ++k) {
         s_col[tr][k] = s.col[k];
@@ -788,8 +798,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
       const char* g0_base = reinterpret_cast<const char*>(s_g0);
       const char* g1_base = reinterpret_cast<const char*>(s_g1);
       const char* col_base = reinterpret_cast<const char*>(&s_col[0][0]);
-      static_assert(RB_PAIRS % 64 == 0, "pair buffer in whole rows of 64 slots");
-      char* pair_v = reinterpret_cast<char*>(&s_pair[0][0]) + (tr & ~63u) * (RB_PAIRS / 64) * 8 -
+      char* pair_v = reinterpret_cast<char*>(&s_pair[0][0]) + (tr >> 6) * (RB_PAIRS * 8) -
                      8 * (int)base;
       auto walk = [&](auto safe_tag) {
         constexpr bool SAFE = decltype(safe_tag)::value;
@@ -943,7 +952,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
           }
         }
         if (oh == 0 && oe < gn) {
-          s_gid[wave][oe] = s_id[t];
+          if constexpr (CDIM == 3) s_gid[wave][oe] = __float_as_int(s_col[t][3]);
+          else s_gid[wave][oe] = s_id[t];
           float* st = s_stage[wave] + oe * nval;
           st[0] = q.x * acc[0] + q.y * acc[1];
           st[1] = q.y * acc[0] + q.z * acc[1];
