@@ -307,8 +307,10 @@ __global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_
   constexpr int WAVES = SORT_THREADS / 64;
   __shared__ K s_k[SORT_TILE];
   __shared__ V s_v[SORT_TILE];
-  __shared__ uint32_t s_wh[WAVES][SORT_BINS];
-  __shared__ uint32_t s_start[SORT_BINS];
+  // per-wave digit counters, then each (wave, digit)'s first position in the
+  // tile (counts and positions stay below SORT_TILE: 16 bits, so the 8-byte
+  // value form's LDS lets 3 workgroups share a CU)
+  __shared__ uint16_t s_wh[WAVES][SORT_BINS];
   __shared__ uint32_t s_gofs[SORT_BINS];
   __shared__ uint32_t s_scan[WAVES];
   const int lane = threadIdx.x & 63;
@@ -352,22 +354,28 @@ __global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_
     const uint32_t before = s_wh[wave][d];
     __builtin_amdgcn_wave_barrier();
     // the highest lane of each digit group advances the wave's counter
-    if (valid && (peers >> lane) == 1ull) s_wh[wave][d] = before + (uint32_t)__popcll(peers);
+    if (valid && (peers >> lane) == 1ull) s_wh[wave][d] = (uint16_t)(before + (uint32_t)__popcll(peers));
     __builtin_amdgcn_wave_barrier();
     rk[r] = before + (uint32_t)__popcll(peers & lt_mask);
   }
   __syncthreads();
-  // thread t owns digit t: per-wave exclusive offsets, tile total, tile start
+  // thread t owns digit t: per-wave counts, tile total, tile start, then each
+  // wave's first position of the digit in the tile
+  uint32_t cw[WAVES];
   uint32_t tot = 0;
 #pragma unroll
   for (int w = 0; w < WAVES; ++w) {
-    const uint32_t c = s_wh[w][threadIdx.x];
-    s_wh[w][threadIdx.x] = tot;
-    tot += c;
+    cw[w] = s_wh[w][threadIdx.x];
+    tot += cw[w];
   }
   uint32_t all;
   const uint32_t st = block_exclusive_scan<uint32_t>(tot, s_scan, all);
-  s_start[threadIdx.x] = st;
+  uint32_t run = st;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    s_wh[w][threadIdx.x] = (uint16_t)run;
+    run += cw[w];
+  }
   s_gofs[threadIdx.x] = hist_scan[tr.hbase + threadIdx.x * tr.stride] - st;
   __syncthreads();
 #pragma unroll
@@ -375,7 +383,7 @@ __global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_
     const uint32_t li = wbase + (uint32_t)r * 64u + lane;
     if (li < tr.count) {
       const uint32_t d = digit_of(k[r], sg, shift, mask);
-      const uint32_t pos = s_start[d] + s_wh[wave][d] + rk[r];
+      const uint32_t pos = (uint32_t)s_wh[wave][d] + rk[r];
       s_k[pos] = k[r];
       s_v[pos] = v[r];
     }
