@@ -378,12 +378,35 @@ __device__ __forceinline__ void lane_bits(const uint32_t* half, int n_list, int 
 // last-level cache); within the camera the forward walks tiles row-major and
 // the backward column-major, the faster order of each measured on the cfg3
 // and cfg4 scenes (forward 4.64 -> 4.28 ms, backward 10.66 -> 10.18 ms at
-// cfg3 against camera-fastest).
+// cfg3 against camera-fastest).  The backward's columns are also dealt out
+// by XCD (xcd_line_order): each XCD walks whole tile columns, its own one of
+// every 8 neighbouring columns, so tiles that share Gaussians vertically
+// share an L2 (11.32 -> 11.22 ms at cfg3; the same by rows in the forward:
+// 4.50 -> 4.57 ms, not used).
 //   forward grid  (tile_w, tile_h, C)
 //   backward grid (tile_h, tile_w, C)
 // ---------------------------------------------------------------------------
 inline dim3 raster_fwd_grid(const RasterGeom& G) { return dim3(G.tile_w, G.tile_h, G.C); }
 inline dim3 raster_bwd_grid(const RasterGeom& G) { return dim3(G.tile_h, G.tile_w, G.C); }
+
+// Workgroup lin (camera-local; consecutive workgroups go to the 8 XCDs in
+// turn) -> (line, pos): line 8 * ((lin / 8) / len) + lin % 8, position
+// (lin / 8) % len, so XCD x takes line x of each block of 8 lines whole.
+// Lines past the last whole block of 8 keep the plain order.  A bijection of
+// [0, n_lines * len).
+__device__ __forceinline__ void xcd_line_order(uint32_t lin, uint32_t n_lines, uint32_t len,
+                                               uint32_t& line, uint32_t& pos) {
+  const uint32_t whole = (n_lines / 8u) * 8u * len;
+  if (lin < whole) {
+    const uint32_t j = lin >> 3;
+    line = (j / len) * 8u + (lin & 7u);
+    pos = j % len;
+  } else {
+    const uint32_t r = lin - whole;
+    line = (n_lines / 8u) * 8u + r / len;
+    pos = r % len;
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Forward
@@ -638,7 +661,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   __shared__ int32_t s_gid[WAVES][32];            // and their Gaussian ids
 
   const uint32_t cam = blockIdx.z;
-  const uint32_t ty = blockIdx.x, tx = blockIdx.y;
+  uint32_t ty, tx;
+  xcd_line_order(blockIdx.y * G.tile_h + blockIdx.x, G.tile_w, G.tile_h, tx, ty);
   const uint32_t tile_id = ty * G.tile_w + tx;
   const uint32_t tr = threadIdx.x;
   static_assert(BATCH == 64, "one list entry per lane");
