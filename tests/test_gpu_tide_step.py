@@ -272,6 +272,45 @@ def test_fused_emission_sort_matches_stable_tile_sort(gpu, V, C, big, tw, th):
         order = np.argsort(tile[a:b], kind="stable") + a
         np.testing.assert_array_equal(ko[a:b], k_in[order])
         np.testing.assert_array_equal(fo[a:b], f_in[order])
+    # and the tile offsets of the sorted keys: each (camera, tile) bucket's
+    # first intersection, empty buckets taking the next occupied one's start
+    offs = torch.empty(C * tw * th, dtype=torch.int32, device=gpu)
+    N.call("tgs_tide_offset_encode", n_isects, N.ptr(k), C, tw, th, tile_bits, N.ptr(offs), s)
+    bucket = (ko >> tile_bits).astype(np.int64) * (tw * th) + (ko & ((1 << tile_bits) - 1))
+    np.testing.assert_array_equal(
+        to_np(offs), np.searchsorted(bucket, np.arange(C * tw * th)).astype(np.int32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,C,tw,th,fill", [
+    (1, 1, 3, 2, "first"), (1, 2, 3, 2, "last"), (2, 1, 4, 4, "last"), (3, 3, 5, 1, "rand"),
+    (5, 2, 120, 68, "first"), (1000, 4, 17, 9, "rand"), (65537, 16, 120, 68, "rand"),
+    (200_000, 3, 120, 68, "sparse")])
+def test_tide_offset_encode_matches_lower_bound(gpu, n, C, tw, th, fill):
+    """tgs_tide_offset_encode on sorted camera | tile keys gives each bucket the
+    index of its first key, and empty buckets the next occupied bucket's
+    start (n_isects after the last key): isect_tiles.cu:234-301.  Key counts
+    around powers of two (the search's probe width), every key in the first
+    or the last bucket, a one-row grid, and keys confined to a few buckets."""
+    announce(f"offset encode n={n} C={C} grid={tw}x{th} fill={fill}")
+    from tidegs_amd import _native as N
+    rng = np.random.default_rng(n + C * 7 + tw)
+    tile_bits = (tw * th).bit_length()
+    nb = C * tw * th
+    if fill == "first":
+        b = np.zeros(n, np.int64)
+    elif fill == "last":
+        b = np.full(n, nb - 1, np.int64)
+    elif fill == "sparse":
+        b = np.sort(rng.choice(rng.integers(0, nb, 7), n))
+    else:
+        b = np.sort(rng.integers(0, nb, n))
+    keys = (((b // (tw * th)) << tile_bits) | (b % (tw * th))).astype(np.uint32)
+    k = torch.from_numpy(keys.view(np.int32)).to(gpu)
+    offs = torch.full((nb,), -7, dtype=torch.int32, device=gpu)
+    N.call("tgs_tide_offset_encode", n, N.ptr(k), C, tw, th, tile_bits, N.ptr(offs),
+           N.stream_handle())
+    np.testing.assert_array_equal(to_np(offs), np.searchsorted(b, np.arange(nb)).astype(np.int32))
 
 
 def test_tide_step_isect_bit_exact(gpu):
