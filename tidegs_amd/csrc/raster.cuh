@@ -842,9 +842,16 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
     for (int W = 0; W < WORDS; ++W) m[W] = 0u;
     uint32_t n_pairs = 0;  // wave-uniform
     if (n_list) {
-      strip_masks<TILE, BATCH, GeoArrays, uint16_t, 16>(s_list[wave], n_list,
-                                                         GeoArrays{s_g0, s_g1}, s_box, s_cov,
-                                                         s_emh[wave], wx0, wy0, alive);
+      // the row masks go to s_emh (pair slots, owners); at 16-pixel tiles the
+      // lane's bits come from a register transpose of the same masks
+      if constexpr (TILE == 16)
+        strip_bits<BATCH, WORDS, true, GeoArrays, uint16_t, 16>(
+            s_list[wave], n_list, GeoArrays{s_g0, s_g1}, s_box, s_cov, s_emh[wave], wx0, wy0,
+            alive, m);
+      else
+        strip_masks<TILE, BATCH, GeoArrays, uint16_t, 16>(s_list[wave], n_list,
+                                                           GeoArrays{s_g0, s_g1}, s_box, s_cov,
+                                                           s_emh[wave], wx0, wy0, alive);
       uint32_t c_lo = 0u, c_hi = 0u;
       if (lane < n_list) {
         c_lo = (uint32_t)__popc(s_emh[wave][0][lane]);
@@ -863,10 +870,19 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
       const int li_min =
           t_min <= 0 ? 0
                      : __popcll(hits & (t_min >= 64 ? ~0ull : ((1ull << t_min) - 1ull)));
-      lane_bits<WORDS, true>(s_emh[wave][half], n_list, li_min, m);
-      if (!((alive >> lane) & 1ull)) {
+      if constexpr (TILE == 16) {
+        // strip_bits left bits [0, n_list) of alive lanes; drop those before li_min
 #pragma unroll
-        for (int W = 0; W < WORDS; ++W) m[W] = 0u;
+        for (int W = 0; W < WORDS; ++W) {
+          const int lo = min(max(li_min - 32 * W, 0), 32);
+          m[W] &= lo >= 32 ? 0u : ~((1u << lo) - 1u);
+        }
+      } else {
+        lane_bits<WORDS, true>(s_emh[wave][half], n_list, li_min, m);
+        if (!((alive >> lane) & 1ull)) {
+#pragma unroll
+          for (int W = 0; W < WORDS; ++W) m[W] = 0u;
+        }
       }
     }
     int a = 0;        // first list entry of the current segment
