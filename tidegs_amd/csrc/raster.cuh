@@ -511,7 +511,10 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
   __shared__ StagedRec<CDIM> s_rec[BATCH];
   __shared__ float4 s_box[BATCH];
   __shared__ float4 s_cov[BATCH];
-  __shared__ uint8_t s_list[WAVES][BATCH];
+  // each wavefront's list of staged entries as byte offsets of their records
+  constexpr int RSZ = (int)sizeof(StagedRec<CDIM>);
+  static_assert(BATCH * RSZ < 65536, "record offsets fit 16 bits");
+  __shared__ uint16_t s_list[WAVES][BATCH];
   // the entries' row masks pass through LDS only for 8-pixel tiles (16-pixel
   // tiles transpose them in registers: strip_bits)
   constexpr int EMH = TILE == 16 ? 1 : BATCH;
@@ -575,8 +578,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     const uint64_t alive = tgs_ballot(T > 0.f);
     if (!alive) continue;
     uint64_t hits;
-    const int n_list =
-        build_wave_list<BATCH>(s_box, s_list[wave], 0, batch_size, wx0, wx1, wy0, wy1, hits);
+    const int n_list = build_wave_list<BATCH, uint16_t, RSZ>(s_box, s_list[wave], 0, batch_size,
+                                                            wx0, wx1, wy0, wy1, hits);
     // list positions past the list name staged record 0, so a lane with no
     // entry left reads a staged record without a select
 #pragma unroll
@@ -585,19 +588,20 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     __builtin_amdgcn_wave_barrier();
     uint32_t mw[WORDS];
     if constexpr (TILE == 16) {
-      strip_bits<BATCH, WORDS, false, GeoRecs<CDIM>, uint8_t, 1>(
+      strip_bits<BATCH, WORDS, false, GeoRecs<CDIM>, uint16_t, RSZ>(
           s_list[wave], n_list, GeoRecs<CDIM>{s_rec}, s_box, s_cov, nullptr, wx0, wy0, alive, mw);
     } else {
-      strip_masks<TILE, BATCH>(s_list[wave], n_list, GeoRecs<CDIM>{s_rec}, s_box, s_cov,
-                               s_emh[wave], wx0, wy0, alive);
+      strip_masks<TILE, BATCH, GeoRecs<CDIM>, uint16_t, RSZ>(
+          s_list[wave], n_list, GeoRecs<CDIM>{s_rec}, s_box, s_cov, s_emh[wave], wx0, wy0, alive);
       lane_bits<WORDS, false>(s_emh[wave][(tr & 63) >> 5], n_list, 0, mw);
     }
     // the wavefront's list addressed from the lane index (a VGPR base, so the
     // walk's address add pairs with other VALU work)
-    const uint8_t* my_list = &s_list[0][0] + (tr & ~63u) * (BATCH / 64);
-    // the batch start as a VGPR operand too (the contributor index add pairs)
-    int32_t bs_v;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(bs_v) : "s"(batch_start));
+    const uint16_t* my_list = &s_list[0][0] + (tr & ~63u) * (BATCH / 64);
+    const char* rec_base = reinterpret_cast<const char*>(s_rec);
+    // record offset of this batch's last composited Gaussian (0xffff: none);
+    // the contributor index is derived from it once per batch, not per step
+    uint32_t cur_off = 0xffffu;
     auto walk = [&](auto safe_tag) {
       constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
@@ -612,24 +616,26 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
           const bool act = m != 0u;
           const int bit = __builtin_ctz(m | 0x80000000u);  // 31 where m is empty
           m &= m - 1u;
-          const int t = my_list[W * 32 + bit];
-          const StagedRec<CDIM>& rec = s_rec[t];
+          const uint32_t off = my_list[W * 32 + bit];
+          const StagedRec<CDIM>& rec = *reinterpret_cast<const StagedRec<CDIM>*>(rec_base + off);
           const float4 g0 = rec.g0;
           const float4 g1 = rec.g1;
           const float power = raster_power(g0, make_float2(g1.x, g1.y), g0.x - px, g0.y - py);
           const bool pass = act && !(power > g1.y || power < RS_LOG2_MIN_ALPHA);
           const float alpha = fminf(0.999f, __builtin_amdgcn_exp2f(power));
           const float next_T = T * (1.f - alpha);
-          const bool low = next_T <= 1e-4f;
-          const bool stop = pass && low;
-          const bool comp = pass && !low;
+          // alpha is never NaN (fminf keeps 0.999) and T is finite, so
+          // next_T > 1e-4 is the reference's !(next_T <= 1e-4): one compare
+          const bool big = next_T > 1e-4f;
+          const bool stop = pass && !big;
+          const bool comp = pass && big;
           m = stop ? 0u : m;
           const float vis = comp ? alpha * T : 0.f;
 #pragma unroll
           for (int k = 0; k < CDIM; ++k)
             pix[k] = SAFE ? (comp ? fmaf(rec.col[k], vis, pix[k]) : pix[k])
                           : fmaf(rec.col[k], vis, pix[k]);
-          cur_idx = comp ? (uint32_t)(bs_v + t) : cur_idx;
+          cur_off = comp ? off : cur_off;
           if (COUNT) n_comp += comp ? 1 : 0;
           T = comp ? next_T : (stop ? -T : T);
         } while (tgs_ballot(m != 0u));
@@ -637,6 +643,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     };
     if (safe_walk) walk(std::true_type{});
     else walk(std::false_type{});
+    if (cur_off != 0xffffu) cur_idx = (uint32_t)batch_start + cur_off / (uint32_t)RSZ;
   }
   T = fabsf(T);
   if (inside) {
