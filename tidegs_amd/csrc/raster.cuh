@@ -371,25 +371,28 @@ __device__ __forceinline__ void lane_bits(const uint32_t* half, int n_list, int 
   }
 }
 
-// 16 x 16 bit transpose within each 16-lane row of the wavefront: lane e of a
-// row holds a 16-bit word (bit c = M[e][c]); afterwards lane c of the row
-// holds bit e = M[e][c].  Four exchange stages j = 8, 4, 2, 1: a lane whose
-// index has bit j clear keeps its bits b with b & j == 0 and takes the bits of
-// lane + j shifted up by j into the others; a lane with bit j set keeps the
-// bits with b & j set and takes the bits of lane - j shifted down by j.  The
-// partner's word comes by DPP (row_shl / row_shr), folded into the AND.
-__device__ __forceinline__ uint32_t row_transpose16(uint32_t x) {
+// Two 16 x 16 bit transposes at once within each 16-lane row of the
+// wavefront, one per 16-bit half of a word: lane e of a row holds
+// x = M[e] | N[e] << 16 (bit c of M[e] = M[e][c]); afterwards lane c holds
+// bit e = M[e][c] and bit 16 + e = N[e][c].  Four exchange stages j = 8, 4,
+// 2, 1: a lane whose index has bit j clear keeps its bits b with b & j == 0
+// and takes the bits of lane + j shifted up by j into the others; a lane with
+// bit j set keeps the bits with b & j set and takes the bits of lane - j
+// shifted down by j.  The masks repeat per half, and a bit that a shift
+// carries across the halves' boundary always lands in a position the mask
+// drops.  The partner's word comes by DPP (row_shl / row_shr).
+__device__ __forceinline__ uint32_t row_transpose16x2(uint32_t x) {
   const uint32_t l = threadIdx.x & 15u;
-#define RT_STAGE(J, M0, SHL, SHR)                                                     \
-  {                                                                                   \
-    const uint32_t up = tgs_dpp_u32<SHL, 0xf, 0xf, true>(x << J) & (0xffffu & ~(M0)); \
-    const uint32_t dn = tgs_dpp_u32<SHR, 0xf, 0xf, true>(x >> J) & (M0);              \
-    x = (l & J) ? ((x & ~(M0)) | dn) : ((x & (M0)) | up);                             \
+#define RT_STAGE(J, M0, SHL, SHR)                                         \
+  {                                                                       \
+    const uint32_t up = tgs_dpp_u32<SHL, 0xf, 0xf, true>(x << J) & ~(M0); \
+    const uint32_t dn = tgs_dpp_u32<SHR, 0xf, 0xf, true>(x >> J) & (M0);  \
+    x = (l & J) ? ((x & ~(M0)) | dn) : ((x & (M0)) | up);                 \
   }
-  RT_STAGE(8, 0x00ffu, 0x108, 0x118)  // row_shl:8 / row_shr:8
-  RT_STAGE(4, 0x0f0fu, 0x104, 0x114)
-  RT_STAGE(2, 0x3333u, 0x102, 0x112)
-  RT_STAGE(1, 0x5555u, 0x101, 0x111)
+  RT_STAGE(8, 0x00ff00ffu, 0x108, 0x118)  // row_shl:8 / row_shr:8
+  RT_STAGE(4, 0x0f0f0f0fu, 0x104, 0x114)
+  RT_STAGE(2, 0x33333333u, 0x102, 0x112)
+  RT_STAGE(1, 0x55555555u, 0x101, 0x111)
 #undef RT_STAGE
   return x;
 }
@@ -397,41 +400,37 @@ __device__ __forceinline__ uint32_t row_transpose16(uint32_t x) {
 // This lane's coverage bits over list entries [0, n_list) (TILE == 16): bit
 // li of mw[li / 32] is set when entry li's row interval (cover_row) holds the
 // lane's own pixel (strip row lane / 16, column lane % 16) and the pixel is
-// alive.  Per pass of 16 entries lane 16 r + e computes entry li0 + e on
-// strip row r, and row_transpose16 hands lane 16 r + c the pass's bits of
-// pixel (r, c): no round trip of the masks through LDS and no per-entry bit
-// extraction.  With STORE the row masks also go to s_emh as two 32-bit halves
-// per entry (s_emh[0][li]: rows 0-1, s_emh[1][li]: rows 2-3), as strip_masks
-// stores them.
+// alive.  Per word of 32 entries lane 16 r + e computes entries 32 w + e and
+// 32 w + 16 + e on strip row r, and row_transpose16x2 hands lane 16 r + c the
+// word's bits of pixel (r, c): no round trip of the masks through LDS and no
+// per-entry bit extraction.  With STORE the row masks also go to s_emh as two
+// 32-bit halves per entry (s_emh[0][li]: rows 0-1, s_emh[1][li]: rows 2-3), as
+// strip_masks stores them.
 template <int BATCH, int WORDS, bool STORE, class Geo, typename LT, int SCALE>
 __device__ __forceinline__ void strip_bits(const LT* s_list, int n_list, const Geo geo,
                                            const float4* s_box, const float4* s_cov,
                                            uint32_t (*s_emh)[BATCH], float px0, float py0,
                                            uint64_t alive, uint32_t (&mw)[WORDS]) {
-  static_assert(WORDS == 2 || WORDS == 4, "64 or 128 entries per batch");
+  static_assert(WORDS * 32 == BATCH, "one word per 32 entries");
   const int lane = threadIdx.x & 63;
   const int r = lane >> 4, e = lane & 15;
   const uint32_t alive_row = (uint32_t)(alive >> (r * 16)) & 0xffffu;
-  uint64_t acc[WORDS / 2];
+  const float py = py0 + (float)r;
+  auto cover = [&](int li) {
+    const int t = (int)s_list[li] / SCALE;
+    const uint32_t x =
+        cover_row<16>(geo.G0(t), geo.G1(t), s_box[t], s_cov[t], px0, py) & alive_row;
+    if (STORE) reinterpret_cast<uint16_t*>(&s_emh[r >> 1][li])[r & 1] = (uint16_t)x;
+    return x;
+  };
 #pragma unroll
-  for (int h = 0; h < WORDS / 2; ++h) acc[h] = 0ull;
-  for (int li0 = 0; li0 < n_list; li0 += 16) {  // wave-uniform
-    const int li = li0 + e;
+  for (int w = 0; w < WORDS; ++w) {
+    mw[w] = 0u;
+    if (32 * w >= n_list) continue;  // wave-uniform
     uint32_t x = 0u;
-    if (li < n_list) {
-      const int t = (int)s_list[li] / SCALE;
-      x = cover_row<16>(geo.G0(t), geo.G1(t), s_box[t], s_cov[t], px0, py0 + (float)r) &
-          alive_row;
-      if (STORE) reinterpret_cast<uint16_t*>(&s_emh[r >> 1][li])[r & 1] = (uint16_t)x;
-    }
-    const uint64_t b = (uint64_t)row_transpose16(x) << (li0 & 63);
-    if (WORDS == 2 || li0 < 64) acc[0] |= b;
-    else acc[WORDS / 2 - 1] |= b;
-  }
-#pragma unroll
-  for (int h = 0; h < WORDS / 2; ++h) {
-    mw[2 * h] = (uint32_t)acc[h];
-    mw[2 * h + 1] = (uint32_t)(acc[h] >> 32);
+    if (32 * w + e < n_list) x = cover(32 * w + e);
+    if (32 * w + 16 < n_list && 32 * w + 16 + e < n_list) x |= cover(32 * w + 16 + e) << 16;
+    mw[w] = row_transpose16x2(x);
   }
   if (STORE) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
