@@ -244,13 +244,17 @@ __device__ __forceinline__ int build_wave_list(const float4* s_box, LT* s_list, 
 // pixel interval is widened by far more than the rounding of the roots (the
 // hardware sqrt and reciprocal are within 1 ulp; the margin is 2^-10 of the
 // interval's extent plus 1e-3 px), so the mask contains every pixel whose
-// evaluated power passes.  Degenerate or non-finite Gaussians cover every
-// pixel (the exact test decides), invisible ones none.
+// evaluated power passes.  A row with D < 0 misses the (threshold - delta)
+// ellipse, which contains the alpha >= 1/255 one, so no box test is needed.
+// The interval's ends are clamped into the tile before rounding (first pixel
+// in [0, TILE], last in [-1, TILE - 1]), so an empty or off-tile interval
+// gives an empty mask without a separate test.  Degenerate or non-finite
+// Gaussians (mode RS_COVER_ALL) cover every pixel (the exact test decides);
+// invisible ones (RS_COVER_NONE) are never listed.
 // ---------------------------------------------------------------------------
 template <int TILE>
 __device__ __forceinline__ uint32_t cover_row(const float4& g0, const float2& g1,
-                                              const float4& box, const float4& cov, float px0,
-                                              float py) {
+                                              const float4& cov, float px0, float py) {
   constexpr uint32_t FULL = (1u << TILE) - 1u;
   const float dy = g0.y - py;
   const float h = g0.w * dy;
@@ -261,13 +265,12 @@ __device__ __forceinline__ uint32_t cover_row(const float4& g0, const float2& g1
   const float base = g0.x - px0;
   const float m = 1e-3f + 0x1p-10f * (fabsf(cen) + half) + 0x1p-20f * fabsf(base);
   // px = gx - dx  =>  j = px - px0 in [base - cen - half, base - cen + half]
-  const float lo = fmaxf(base - cen - half - m, -1.f);
-  const float hi = fminf(base - cen + half + m, (float)TILE);
-  const int jlo = max((int)ceilf(lo), 0);
-  const int jhi = min((int)floorf(hi), TILE - 1);
-  const uint32_t quad = (FULL >> (TILE - 1 - max(jhi, 0))) & (FULL << min(jlo, TILE - 1));
-  const bool in = D >= 0.f && jlo <= jhi && py >= box.z && py <= box.w;
-  return cov.w == RS_COVER_QUAD ? (in ? quad : 0u) : (cov.w == RS_COVER_ALL ? FULL : 0u);
+  const float lo = __builtin_amdgcn_fmed3f(base - cen - half - m, 0.f, (float)TILE);
+  const float hi = __builtin_amdgcn_fmed3f(base - cen + half + m, -1.f, (float)(TILE - 1));
+  const int jlo = (int)ceilf(lo);   // 0 .. TILE
+  const int jhi = (int)floorf(hi);  // -1 .. TILE - 1
+  const uint32_t quad = (FULL >> (TILE - 1 - jhi)) & (FULL << jlo);
+  return cov.w == RS_COVER_QUAD ? (D >= 0.f ? quad : 0u) : FULL;
 }
 
 // A staged Gaussian as one LDS record, so that a lane reading the entry it
@@ -301,9 +304,8 @@ struct GeoRecs {
 // s_emh[1][li] lanes 32..63, so that a lane reads only its own half.
 template <int TILE, int BATCH, class Geo, typename LT = uint8_t, int SCALE = 1>
 __device__ __forceinline__ void strip_masks(const LT* s_list, int n_list, const Geo geo,
-                                            const float4* s_box, const float4* s_cov,
-                                            uint32_t (*s_emh)[BATCH], float px0, float py0,
-                                            uint64_t alive) {
+                                            const float4* s_cov, uint32_t (*s_emh)[BATCH],
+                                            float px0, float py0, uint64_t alive) {
   using RM = typename std::conditional<TILE == 16, uint16_t, uint8_t>::type;
   constexpr int ROWS = 64 / TILE;
   constexpr int PER = 64 / ROWS;  // entries per pass
@@ -315,7 +317,7 @@ __device__ __forceinline__ void strip_masks(const LT* s_list, int n_list, const 
     if (li < n_list) {
       const int t = (int)s_list[li] / SCALE;
       const uint32_t m =
-          cover_row<TILE>(geo.G0(t), geo.G1(t), s_box[t], s_cov[t], px0, py0 + (float)r);
+          cover_row<TILE>(geo.G0(t), geo.G1(t), s_cov[t], px0, py0 + (float)r);
       reinterpret_cast<RM*>(&s_emh[(r * TILE) >> 5][li])[((r * TILE) & 31) / TILE] =
           (RM)(m & alive_row);
     }
@@ -408,9 +410,9 @@ __device__ __forceinline__ uint32_t row_transpose16x2(uint32_t x) {
 // strip_masks stores them.
 template <int BATCH, int WORDS, bool STORE, class Geo, typename LT, int SCALE>
 __device__ __forceinline__ void strip_bits(const LT* s_list, int n_list, const Geo geo,
-                                           const float4* s_box, const float4* s_cov,
-                                           uint32_t (*s_emh)[BATCH], float px0, float py0,
-                                           uint64_t alive, uint32_t (&mw)[WORDS]) {
+                                           const float4* s_cov, uint32_t (*s_emh)[BATCH],
+                                           float px0, float py0, uint64_t alive,
+                                           uint32_t (&mw)[WORDS]) {
   static_assert(WORDS * 32 == BATCH, "one word per 32 entries");
   const int lane = threadIdx.x & 63;
   const int r = lane >> 4, e = lane & 15;
@@ -419,7 +421,7 @@ __device__ __forceinline__ void strip_bits(const LT* s_list, int n_list, const G
   auto cover = [&](int li) {
     const int t = (int)s_list[li] / SCALE;
     const uint32_t x =
-        cover_row<16>(geo.G0(t), geo.G1(t), s_box[t], s_cov[t], px0, py) & alive_row;
+        cover_row<16>(geo.G0(t), geo.G1(t), s_cov[t], px0, py) & alive_row;
     if (STORE) reinterpret_cast<uint16_t*>(&s_emh[r >> 1][li])[r & 1] = (uint16_t)x;
     return x;
   };
@@ -588,10 +590,10 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
     uint32_t mw[WORDS];
     if constexpr (TILE == 16) {
       strip_bits<BATCH, WORDS, false, GeoRecs<CDIM>, uint16_t, RSZ>(
-          s_list[wave], n_list, GeoRecs<CDIM>{s_rec}, s_box, s_cov, nullptr, wx0, wy0, alive, mw);
+          s_list[wave], n_list, GeoRecs<CDIM>{s_rec}, s_cov, nullptr, wx0, wy0, alive, mw);
     } else {
       strip_masks<TILE, BATCH, GeoRecs<CDIM>, uint16_t, RSZ>(
-          s_list[wave], n_list, GeoRecs<CDIM>{s_rec}, s_box, s_cov, s_emh[wave], wx0, wy0, alive);
+          s_list[wave], n_list, GeoRecs<CDIM>{s_rec}, s_cov, s_emh[wave], wx0, wy0, alive);
       lane_bits<WORDS, false>(s_emh[wave][(tr & 63) >> 5], n_list, 0, mw);
     }
     // the wavefront's list addressed from the lane index (a VGPR base, so the
@@ -852,11 +854,11 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
       // lane's bits come from a register transpose of the same masks
       if constexpr (TILE == 16)
         strip_bits<BATCH, WORDS, true, GeoArrays, uint16_t, 16>(
-            s_list[wave], n_list, GeoArrays{s_g0, s_g1}, s_box, s_cov, s_emh[wave], wx0, wy0,
+            s_list[wave], n_list, GeoArrays{s_g0, s_g1}, s_cov, s_emh[wave], wx0, wy0,
             alive, m);
       else
         strip_masks<TILE, BATCH, GeoArrays, uint16_t, 16>(s_list[wave], n_list,
-                                                           GeoArrays{s_g0, s_g1}, s_box, s_cov,
+                                                           GeoArrays{s_g0, s_g1}, s_cov,
                                                            s_emh[wave], wx0, wy0, alive);
       uint32_t c_lo = 0u, c_hi = 0u;
       if (lane < n_list) {
