@@ -405,6 +405,9 @@ def bench_step(args, dev):
     else:
         sc = scenes.cfg2(seed=0).to(dev)
     C = sc.n_cams
+    if args.row_order == "blocks" and args.workload in ("cfg3", "cfg4"):
+        # TideGS's resident row order: Morton order within 4096-row blocks
+        sc.params = sc.params[scenes.block_layout(sc.params)]
     # the resident table in its MI355X layout: rows padded to 256 bytes
     table = scenes.padded_table(sc.params.contiguous())
     del sc.params
@@ -502,6 +505,9 @@ def bench_step(args, dev):
                    "touched_rows": stats.touched_rows, "isects": stats.n_isects,
                    "isects_per_tile": round(stats.n_isects / (C * ts.tw * ts.th), 1),
                    **tile_load, "scene_state": "seeded scene, restored before every step",
+                   "row_order": ("Morton within 4096-row blocks, blocks in seeded random order "
+                                 "(TideGS's block store)" if args.row_order == "blocks" and
+                                 args.workload in ("cfg3", "cfg4") else "generator order (random)"),
                    "optimizer_update": "split" if args.split_update else "fused",
                    "live_pairs": int(getattr(ts, "last_live_pairs", 0))},
         "bwd_hbm_GBs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1) if bwd_ms else None,
@@ -553,6 +559,8 @@ def bench_dropin(args, dev, steps=None, warmup=None):
 
     sc = scenes.cfg3(seed=0, n=args.n, n_cams=args.cams, width=args.width, height=args.height,
                      with_gt=True).to(dev)
+    if args.row_order == "blocks":
+        sc.params = sc.params[scenes.block_layout(sc.params)]
     C, W, H = sc.n_cams, sc.width, sc.height
     n = sc.params.shape[0]
     # TideGS's GPU-resident component tensors
@@ -1054,6 +1062,10 @@ def main():
     ap.add_argument("--cams", type=int, default=16)
     ap.add_argument("--width", type=int, default=1920)
     ap.add_argument("--height", type=int, default=1080)
+    ap.add_argument("--row-order", choices=("blocks", "random"), default="blocks",
+                    help="cfg3/cfg4 resident row order: TideGS's (Morton order within 4096-row "
+                         "blocks, the blocks in a seeded random slot order) or the generator's "
+                         "own random order")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-timing", action="store_true")
     ap.add_argument("--no-dropin", action="store_true",

@@ -291,8 +291,11 @@ def test_cfg3_dense_window_vs_oracle(gpu):
             end_to_end_bound=2e-4)
 
 
-def test_cfg3_full_step(gpu):
-    """The bench's configuration at full size (4M rows, 16 x 1920x1080):
+@pytest.mark.parametrize("row_order", ["random", "blocks"])
+def test_cfg3_full_step(gpu, row_order):
+    """The bench's configuration at full size (4M rows, 16 x 1920x1080), in the
+    generator's row order and in TideGS's resident order (the bench's: Morton
+    order within 4096-row blocks, scenes.block_layout):
 
     * intersections: strictly increasing (key, entry), each entry's rectangle
       covered once, key fields equal to the entry's camera / tile / depth
@@ -305,8 +308,11 @@ def test_cfg3_full_step(gpu):
     * rows that no camera sees keep their bits; everything stays finite;
     * TideStep.step (the timed path) then runs on the updated table with the
       same touched set and finite losses."""
-    announce("cfg3 full size: 4M rows, 16 cameras 1920x1080, fused update vs two-launch")
+    announce(f"cfg3 full size: 4M rows ({row_order} order), 16 cameras 1920x1080, "
+             "fused update vs two-launch")
     sc = scenes.cfg3(seed=0)
+    if row_order == "blocks":
+        sc.params = sc.params[scenes.block_layout(sc.params)]
     C, W, H = sc.n_cams, sc.width, sc.height
     base = scenes.padded_table(sc.params.to(gpu).contiguous())
     n = base.shape[0]

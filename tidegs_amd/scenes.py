@@ -99,6 +99,44 @@ def padded_table(p: torch.Tensor, pitch: int = 64) -> torch.Tensor:
     return out[:, :ROW]
 
 
+BLOCK_ROWS = 4096  # rows per block of TideGS's block store (arguments/__init__.py:190)
+
+
+def morton_codes(xyz: torch.Tensor) -> torch.Tensor:
+    """30-bit Morton codes of ``xyz`` over its bounds, as the streaming
+    initializer computes them (``storage/streaming_ply_init.py:154-168``: 10
+    bits per axis, x in the lowest bit of each triple), as int64."""
+    xyz = xyz.float()
+    lo, hi = xyz.min(0).values, xyz.max(0).values
+    q = ((xyz - lo) / (hi - lo + 1e-8) * 1023.0).to(torch.int64).clamp(0, 1023)
+
+    def spread(v):
+        v = (v | (v << 16)) & 0x030000FF
+        v = (v | (v << 8)) & 0x0300F00F
+        v = (v | (v << 4)) & 0x030C30C3
+        return (v | (v << 2)) & 0x09249249
+
+    return spread(q[:, 0]) | (spread(q[:, 1]) << 1) | (spread(q[:, 2]) << 2)
+
+
+def block_layout(params: torch.Tensor, block_rows: int = BLOCK_ROWS, seed: int = 0) -> torch.Tensor:
+    """The row order of a TideGS resident table, as a permutation of ``params``'
+    rows.  The streaming initializer writes the base file's rows in stable
+    Morton order (``storage/streaming_ply_init.py:359``), the block store and
+    the working set move them in blocks of 4096 rows (``log_storage_manager.py
+    :280-291``, ``gpu_working_set.py``), and a resident set holds its blocks in
+    whatever slots its transitions gave them: rows in Morton order within each
+    block, the blocks in a seeded random order.  The scene (its Gaussians,
+    visible entries, intersections and pixels) is the same in any row order;
+    what changes is how close in memory the Gaussians one tile touches lie."""
+    order = torch.argsort(morton_codes(params[:, :3]), stable=True)
+    n = order.numel()
+    nb = -(-n // block_rows)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed))
+    idx = (perm[:, None] * block_rows + torch.arange(block_rows)[None]).flatten()
+    return order[idx[idx < n].to(order.device)]
+
+
 def cfg1(seed: int = 0, n: int = 10_000) -> Scene:
     """10k Gaussians, one 256x256 pinhole (fx=fy=256) at the origin looking +z."""
     g = torch.Generator().manual_seed(seed)
