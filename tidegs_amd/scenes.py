@@ -129,12 +129,13 @@ def block_layout(params: torch.Tensor, block_rows: int = BLOCK_ROWS, seed: int =
     block, the blocks in a seeded random order.  The scene (its Gaussians,
     visible entries, intersections and pixels) is the same in any row order;
     what changes is how close in memory the Gaussians one tile touches lie."""
-    order = torch.argsort(morton_codes(params[:, :3]), stable=True)
+    # on the host: a one-off set-up step, kept out of the device's kernel stream
+    order = torch.argsort(morton_codes(params[:, :3].cpu()), stable=True)
     n = order.numel()
     nb = -(-n // block_rows)
     perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed))
     idx = (perm[:, None] * block_rows + torch.arange(block_rows)[None]).flatten()
-    return order[idx[idx < n].to(order.device)]
+    return order[idx[idx < n]].to(params.device)
 
 
 def cfg1(seed: int = 0, n: int = 10_000) -> Scene:
