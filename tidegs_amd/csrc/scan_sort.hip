@@ -219,7 +219,9 @@ struct TileRange {
   uint32_t hbase, stride; // hist index of digit d: hbase + d * stride
 };
 
-__device__ __forceinline__ TileRange radix_tile(const RadixSegs& sg, uint32_t b) {
+// nbins: the pass's digit count (1 << bits); the histogram holds nbins counts
+// per tile, [segment][digit][tile of segment]
+__device__ __forceinline__ TileRange radix_tile(const RadixSegs& sg, uint32_t b, uint32_t nbins) {
   uint32_t lo = 0, hi = sg.n;  // largest s with tile_base[s] <= b
   while (hi - lo > 1) {
     const uint32_t mid = (lo + hi) >> 1;
@@ -232,7 +234,7 @@ __device__ __forceinline__ TileRange radix_tile(const RadixSegs& sg, uint32_t b)
   r.start = sg.key_off[lo] + t * SORT_TILE;
   const uint32_t end = sg.key_off[lo + 1];
   r.count = end > r.start ? min((uint32_t)SORT_TILE, end - r.start) : 0u;
-  r.hbase = sg.tile_base[lo] * SORT_BINS + t;
+  r.hbase = sg.tile_base[lo] * nbins + t;
   r.stride = nts;
   return r;
 }
@@ -254,14 +256,14 @@ __device__ __forceinline__ uint32_t digit_of(K key, const RadixSegs& sg, int shi
 template <typename K>
 __global__ void __launch_bounds__(SORT_THREADS) radix_hist_kernel(const K* __restrict__ keys,
                                                                   RadixSegs sg, int shift,
-                                                                  uint32_t mask,
+                                                                  uint32_t mask, uint32_t nbins,
                                                                   uint32_t* __restrict__ hist) {
   __shared__ uint32_t s_h[SORT_THREADS / 64][SORT_BINS];
   const int wave = threadIdx.x >> 6;
 #pragma unroll
   for (int w = 0; w < SORT_THREADS / 64; ++w) s_h[w][threadIdx.x] = 0;
   __syncthreads();
-  const TileRange tr = radix_tile(sg, blockIdx.x);
+  const TileRange tr = radix_tile(sg, blockIdx.x, nbins);
   // A wavefront whose keys share one digit (common for the high digits of
   // sorted-ish keys) adds its count once instead of 64 conflicting atomics.
   // all of the thread's keys are loaded before any is counted, so the tile's
@@ -290,7 +292,9 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_hist_kernel(const K* __res
   uint32_t c = 0;
 #pragma unroll
   for (int w = 0; w < SORT_THREADS / 64; ++w) c += s_h[w][threadIdx.x];
-  hist[tr.hbase + threadIdx.x * tr.stride] = c;
+  // only the pass's digits: a narrower pass stores (and scans) fewer counts,
+  // each a line of its own in this layout
+  if (threadIdx.x < nbins) hist[tr.hbase + threadIdx.x * tr.stride] = c;
 }
 
 // One tile of 4096 keys per block.  Wave w owns keys [w*1024, (w+1)*1024) of
@@ -302,8 +306,8 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_hist_kernel(const K* __res
 template <typename K, typename V>
 __global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_eu(4))) radix_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, RadixSegs sg, int shift,
-    uint32_t mask, const uint32_t* __restrict__ hist_scan, K* __restrict__ keys_out,
-    V* __restrict__ vals_out) {
+    uint32_t mask, uint32_t nbins, const uint32_t* __restrict__ hist_scan,
+    K* __restrict__ keys_out, V* __restrict__ vals_out) {
   constexpr int WAVES = SORT_THREADS / 64;
   __shared__ K s_k[SORT_TILE];
   __shared__ V s_v[SORT_TILE];
@@ -316,7 +320,7 @@ __global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const uint64_t lt_mask = (1ull << lane) - 1ull;
-  const TileRange tr = radix_tile(sg, blockIdx.x);
+  const TileRange tr = radix_tile(sg, blockIdx.x, nbins);
 #pragma unroll
   for (int w = 0; w < WAVES; ++w) s_wh[w][threadIdx.x] = 0;
   __syncthreads();
@@ -376,7 +380,9 @@ __global__ void __launch_bounds__(SORT_THREADS) __attribute__((amdgpu_waves_per_
     s_wh[w][threadIdx.x] = (uint16_t)run;
     run += cw[w];
   }
-  s_gofs[threadIdx.x] = hist_scan[tr.hbase + threadIdx.x * tr.stride] - st;
+  // digits past nbins never occur in this pass
+  s_gofs[threadIdx.x] =
+      threadIdx.x < nbins ? hist_scan[tr.hbase + threadIdx.x * tr.stride] - st : 0u;
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < SORT_ITEMS; ++r) {
@@ -419,12 +425,12 @@ static int radix_passes(K* keys, V* vals, K* keys_alt, V* vals_alt, const RadixS
                         int begin_bit, int end_bit, void* workspace, int* selector,
                         hipStream_t stream, bool first_hist_ready = false) {
   const uint64_t tiles = sg.tile_base[sg.n];
-  const uint64_t hist_n = tiles * SORT_BINS;
+  const uint64_t hist_max = tiles * SORT_BINS;  // the workspace's layout
   auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
   uint8_t* ws = (uint8_t*)workspace;
   uint32_t* hist = (uint32_t*)ws;
-  uint32_t* hist_scan = (uint32_t*)(ws + al(hist_n * 4));
-  void* scan_ws = ws + 2 * al(hist_n * 4);
+  uint32_t* hist_scan = (uint32_t*)(ws + al(hist_max * 4));
+  void* scan_ws = ws + 2 * al(hist_max * 4);
   K* kin = keys;
   V* vin = vals;
   K* kout = keys_alt;
@@ -435,15 +441,18 @@ static int radix_passes(K* keys, V* vals, K* keys_alt, V* vals_alt, const RadixS
   while (shift < end_bit) {
     const int bits = (end_bit - shift + passes - 1) / passes;
     const uint32_t mask = (1u << bits) - 1u;
-    if (!(first_hist_ready && shift == begin_bit)) {
+    const bool given = first_hist_ready && shift == begin_bit;
+    // a histogram the caller counted keeps the 256-digit layout
+    const uint32_t nbins = given ? (uint32_t)SORT_BINS : mask + 1u;
+    if (!given) {
       hipLaunchKernelGGL((radix_hist_kernel<K>), dim3((unsigned)tiles), dim3(SORT_THREADS), 0,
-                         stream, kin, sg, shift, mask, hist);
+                         stream, kin, sg, shift, mask, nbins, hist);
       TGS_LAUNCH_CHECK("radix_hist");
     }
-    int rc = exclusive_scan_u32(hist, hist_scan, hist_n, scan_ws, stream);
+    int rc = exclusive_scan_u32(hist, hist_scan, tiles * nbins, scan_ws, stream);
     if (rc) return rc;
     hipLaunchKernelGGL((radix_scatter_kernel<K, V>), dim3((unsigned)tiles), dim3(SORT_THREADS), 0,
-                       stream, kin, vin, sg, shift, mask, hist_scan, kout, vout);
+                       stream, kin, vin, sg, shift, mask, nbins, hist_scan, kout, vout);
     TGS_LAUNCH_CHECK("radix_scatter");
     K* tk = kin;
     kin = kout;
