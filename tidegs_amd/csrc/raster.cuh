@@ -628,8 +628,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 8 : 1) raster_fwd_kern
           // alpha is never NaN (fminf keeps 0.999) and T is finite, so
           // next_T > 1e-4 is the reference's !(next_T <= 1e-4): one compare
           const bool big = next_T > 1e-4f;
-          const bool stop = pass && !big;
           const bool comp = pass && big;
+          const bool stop = pass != comp;  // pass && !big, from the lane masks
           m = stop ? 0u : m;
           const float vis = comp ? alpha * T : 0.f;
 #pragma unroll
