@@ -130,8 +130,8 @@ __global__ void __launch_bounds__(256) resident_optim_unified_kernel(
           for (int u = 0; u < OPT_UNROLL; ++u) {
             const uint32_t o = (i0 + 64u * u) * 4u;
             gv[u] = tgs_bload(rg, o, 0);
-            mv[u] = tgs_bload(rm, o, 0);
-            vv[u] = tgs_bload(rv, o, 0);
+            mv[u] = tgs_bload_nt(rm, o, 0);
+            vv[u] = tgs_bload_nt(rv, o, 0);
             pv[u] = tgs_bload(rp, o, 0);
           }
 #pragma unroll
@@ -139,9 +139,9 @@ __global__ void __launch_bounds__(256) resident_optim_unified_kernel(
             const uint32_t o = (i0 + 64u * u) * 4u;
             optim_update<SOPHIA>(gv[u], mv[u], vv[u], pv[u], s_sc[c], dsc, beta1, beta2,
                                  one_m_b1, one_m_b2, eps, batch_size, rho, update_h);
-            tgs_bstore(mv[u], rm, o, 0);
-            tgs_bstore(vv[u], rv, o, 0);
-            tgs_bstore(pv[u], rp, o, 0);
+            tgs_bstore_nt(mv[u], rm, o, 0);
+            tgs_bstore_nt(vv[u], rv, o, 0);
+            tgs_bstore_nt(pv[u], rp, o, 0);
             c += step;
             if (c >= W) c -= W;
           }
@@ -175,8 +175,8 @@ __global__ void __launch_bounds__(256) resident_optim_unified_kernel(
           if (u < n) {
             const int64_t d = tgs_readlane_i64(my_row, u) - r_first;
             gv[u] = tgs_bload(rg, voff_g, (uint32_t)(u * GB));
-            mv[u] = tgs_bload(rm, voff_s, (uint32_t)(d * SB));
-            vv[u] = tgs_bload(rv, voff_s, (uint32_t)(d * SB));
+            mv[u] = tgs_bload_nt(rm, voff_s, (uint32_t)(d * SB));
+            vv[u] = tgs_bload_nt(rv, voff_s, (uint32_t)(d * SB));
             pv[u] = tgs_bload(rp, voff_p, (uint32_t)(d * PB));
           }
         }
@@ -187,9 +187,9 @@ __global__ void __launch_bounds__(256) resident_optim_unified_kernel(
             float m1 = mv[u], v1 = vv[u], p1 = pv[u];
             optim_update<SOPHIA>(gv[u], m1, v1, p1, sc, dsc, beta1, beta2, one_m_b1, one_m_b2,
                                  eps, batch_size, rho, update_h);
-            tgs_bstore(act ? m1 : mv[u], rm, voff_s, (uint32_t)(d * SB));
-            tgs_bstore(act ? v1 : vv[u], rv, voff_s, (uint32_t)(d * SB));
-            tgs_bstore(act ? p1 : pv[u], rp, voff_p, (uint32_t)(d * PB));
+            tgs_bstore_nt(act ? m1 : mv[u], rm, voff_s, (uint32_t)(d * SB));
+            tgs_bstore_nt(act ? v1 : vv[u], rv, voff_s, (uint32_t)(d * SB));
+            tgs_bstore_nt(act ? p1 : pv[u], rp, voff_p, (uint32_t)(d * PB));
           }
         }
       } else {
@@ -209,14 +209,14 @@ __global__ void __launch_bounds__(256) resident_optim_unified_kernel(
           const float sc = SOPHIA ? lr_lane : lr_lane / tgs_readlane_f32(bias1[bc.slot], 0);
           const float dsc = SOPHIA ? 1.f : tgs_readlane_f32(denom_scale[bc.slot], 0);
           const float gv = tgs_bload(rg, voff_g, (uint32_t)(u * GB));
-          const float mv = tgs_bload(rm, voff_s, 0), vv = tgs_bload(rv, voff_s, 0);
+          const float mv = tgs_bload_nt(rm, voff_s, 0), vv = tgs_bload_nt(rv, voff_s, 0);
           const float pv = tgs_bload(rp, voff_p, 0);
           float m1 = mv, v1 = vv, p1 = pv;
           optim_update<SOPHIA>(gv, m1, v1, p1, sc, dsc, beta1, beta2, one_m_b1, one_m_b2, eps,
                                batch_size, rho, update_h);
-          tgs_bstore(act ? m1 : mv, rm, voff_s, 0);
-          tgs_bstore(act ? v1 : vv, rv, voff_s, 0);
-          tgs_bstore(act ? p1 : pv, rp, voff_p, 0);
+          tgs_bstore_nt(act ? m1 : mv, rm, voff_s, 0);
+          tgs_bstore_nt(act ? v1 : vv, rv, voff_s, 0);
+          tgs_bstore_nt(act ? p1 : pv, rp, voff_p, 0);
         }
       }
       t += n;

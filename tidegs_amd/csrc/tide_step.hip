@@ -1293,8 +1293,8 @@ __global__ void __launch_bounds__(FUSED_THREADS) tide_project_bwd_optim_kernel(
       if (u < k) {
         const uint32_t d = (uint32_t)(__builtin_amdgcn_readlane(my_row, u0 + u) - (int32_t)r_first);
         gv[u] = act ? sg[(u0 + u) * ROW_PITCH + lane] : 0.f;
-        mv[u] = tgs_bload(rm, voff_s, d * (uint32_t)SB);
-        vv[u] = tgs_bload(rv, voff_s, d * (uint32_t)SB);
+        mv[u] = tgs_bload_nt(rm, voff_s, d * (uint32_t)SB);
+        vv[u] = tgs_bload_nt(rv, voff_s, d * (uint32_t)SB);
         pv[u] = tgs_bload(rp, voff_p, d * (uint32_t)PB);
       }
     }
@@ -1305,9 +1305,9 @@ __global__ void __launch_bounds__(FUSED_THREADS) tide_project_bwd_optim_kernel(
         float m1 = mv[u], v1 = vv[u], p1 = pv[u];
         optim_update<SOPHIA, POW2_BS>(gv[u], m1, v1, p1, sc, dsc, O.beta1, O.beta2, one_m_b1, one_m_b2,
                              O.eps, O.batch_size, O.rho, O.update_h);
-        tgs_bstore(act ? m1 : mv[u], rm, voff_s, d * (uint32_t)SB);
-        tgs_bstore(act ? v1 : vv[u], rv, voff_s, d * (uint32_t)SB);
-        tgs_bstore(act ? p1 : pv[u], rp, voff_p, d * (uint32_t)PB);
+        tgs_bstore_nt(act ? m1 : mv[u], rm, voff_s, d * (uint32_t)SB);
+        tgs_bstore_nt(act ? v1 : vv[u], rv, voff_s, d * (uint32_t)SB);
+        tgs_bstore_nt(act ? p1 : pv[u], rp, voff_p, d * (uint32_t)PB);
       }
     }
     u0 += k;

@@ -88,6 +88,8 @@ __global__ __launch_bounds__(WS_THREADS) void ws_move_rows_kernel(MoveArgs a) {
     const float* __restrict__ sp = a.src + srow * SP;
     float* __restrict__ dp = a.dst + drow * DP;
     const int nel = nrows * DP;
+    // rows are streamed: non-temporal loads and stores (each byte moves once;
+    // kept-block copy 4.58 -> 5.00 TB/s, pack 4.7 -> 5.1 TB/s)
     float v[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -95,18 +97,19 @@ __global__ __launch_bounds__(WS_THREADS) void ws_move_rows_kernel(MoveArgs a) {
       v[k] = 0.0f;
       if (e < nel) {
         if constexpr (SP == DP && !UNIFIED) {
-          v[k] = sp[e];
+          v[k] = __builtin_nontemporal_load(&sp[e]);
         } else {
           const int r = e / DP;
           const int c = e - r * DP;
-          if (DP == WS_COLS || c < WS_COLS) v[k] = sp[r * SP + source_column<UNIFIED>(c)];
+          if (DP == WS_COLS || c < WS_COLS)
+            v[k] = __builtin_nontemporal_load(&sp[r * SP + source_column<UNIFIED>(c)]);
         }
       }
     }
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int e = tid + k * WS_THREADS;
-      if (e < nel) dp[e] = v[k];
+      if (e < nel) __builtin_nontemporal_store(v[k], &dp[e]);
     }
     if (a.dst_gids && tid < nrows) {
       int64_t gid;
