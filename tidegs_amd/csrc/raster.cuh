@@ -773,8 +773,8 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   const float T_final = 1.f - render_alphas[pid];
   float T = T_final;
   // the colour sum behind the current Gaussian enters v_alpha only through its
-  // dot product with dL/dcolor: buffer_dot = sum_k buffer_k v_rc_k
-  float buffer_dot = 0.f;
+  // dot product with dL/dcolor, buffer_dot = sum_k buffer_k v_rc_k, and only as
+  // tf_term - buffer_dot: the walk carries that difference (tf_dot)
   float v_rc[CDIM];
 #pragma unroll
   for (int k = 0; k < CDIM; ++k) {
@@ -789,6 +789,7 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   }
   // T_final * ra * v_ra - T_final * ra * bg_dot = ra * tf_term
   const float tf_term = T_final * v_ra - T_final * bg_dot;
+  float tf_dot = tf_term;
   const int32_t bin_final = inside ? last_ids[pid] : -1;
   const int32_t wave_bin_final = tgs_wave_max_i32(bin_final);
   // entries behind the tile's last contributor (any pixel's last_id) touch no
@@ -959,10 +960,9 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
 #pragma unroll
               for (int k = 1; k < CDIM; ++k)
                 cv = fmaf(CPAD == 4 ? ck[k] : s_col[t16 >> 4][k], v_rc[k], cv);
-              const float v_alpha = fmaf(Tn, cv, ra * (tf_term - buffer_dot));
+              const float v_alpha = fmaf(Tn, cv, ra * tf_dot);
               const float fac = pass ? alpha * Tn : 0.f;
-              buffer_dot = SAFE ? (pass ? fmaf(fac, cv, buffer_dot) : buffer_dot)
-                                : fmaf(fac, cv, buffer_dot);
+              tf_dot = SAFE ? (pass ? fmaf(-fac, cv, tf_dot) : tf_dot) : fmaf(-fac, cv, tf_dot);
               // reference: the sigma terms only where alpha was not clamped
               const float v_sigma = pass && raw <= 0.999f ? -raw * v_alpha : 0.f;
               const uint32_t slot = (uint32_t)s_poh[wave][half][li] +
