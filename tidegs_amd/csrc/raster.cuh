@@ -772,9 +772,6 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
 
   const float T_final = 1.f - render_alphas[pid];
   float T = T_final;
-  // the colour sum behind the current Gaussian enters v_alpha only through its
-  // dot product with dL/dcolor, buffer_dot = sum_k buffer_k v_rc_k, and only as
-  // tf_term - buffer_dot: the walk carries that difference (tf_dot)
   float v_rc[CDIM];
 #pragma unroll
   for (int k = 0; k < CDIM; ++k) {
@@ -789,6 +786,9 @@ __global__ void __launch_bounds__(TILE* TILE, CDIM <= 4 ? 6 : 1) raster_bwd_kern
   }
   // T_final * ra * v_ra - T_final * ra * bg_dot = ra * tf_term
   const float tf_term = T_final * v_ra - T_final * bg_dot;
+  // the colour sum behind the current Gaussian enters v_alpha only through its
+  // dot product with dL/dcolor, buffer_dot = sum_k buffer_k v_rc_k, and only as
+  // tf_term - buffer_dot: the walk carries that difference
   float tf_dot = tf_term;
   const int32_t bin_final = inside ? last_ids[pid] : -1;
   const int32_t wave_bin_final = tgs_wave_max_i32(bin_final);
